@@ -1,0 +1,240 @@
+"""Benchmark of the paged KV-cache decode step on one MI355X.
+
+One step = one decode iteration of a 24-layer model's attention data path:
+for every layer pool, append one new K/V row per sequence and run paged decode
+attention over the whole context (the fused K1+K2 launch the engine uses for
+decode-only steps). Workload "qwen-fp16-b64": Qwen2.5-0.5B layer geometry
+(14/2 heads, head_dim 64, block 16), fp16, 64 sequences with U{512..4096}
+cached tokens, 32768-block pool per layer. Inputs are resident in HBM before
+the timed region; the 24 distinct layer pools (6 GiB) keep the working set far
+above the 256 MB Infinity Cache. The step is captured once in a HIP graph and
+replayed; HIP events on the capturing stream bracket the timed replays.
+
+value = algorithmic bytes of all layers / wall time of the step (GB/s).
+Algorithmic bytes per layer: append (read k,v; write the pool rows; 4-byte
+slots) + attention (every visible K and V row once, q and out once, the
+block-table entries used, the context lengths); no credit for cache hits.
+
+Prints ONE JSON line (rank 0, N = 1 only).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "paged decode attn+append HBM GB/s (% of peak) at 1 GPU; e2e decode tok/s"
+
+
+def _log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(wl, reps: int, budget_s: float) -> dict:
+    """The oracle (op-for-op restatement of the reference CPU path) on the same
+    workload, one layer step per rep, on the host's cores."""
+    import torch
+
+    from oracle import reference_path as ref
+
+    threads = len(os.sched_getaffinity(0))
+    threads = min(threads, 16)        # the GPU box grants 16 cores per GPU
+    torch.set_num_threads(threads)
+    times = []
+    t_start = time.perf_counter()
+    for _ in range(reps):
+        pool = wl.pool  # the append rewrites the same rows each rep (idempotent)
+        t0 = time.perf_counter()
+        ref.decode_step(pool, wl.q, wl.k_new, wl.v_new, wl.cached_lens, wl.block_tables,
+                        wl.num_heads, wl.num_kv_heads, wl.block_size)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > budget_s:
+            break
+    times.sort()
+    med = times[len(times) // 2]
+    gbs = wl.algorithmic_bytes()["total"] / med / 1e9
+    return {"value": round(gbs, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{len(times)} one-layer decode steps of {wl.name} (B={wl.batch}), median "
+                      f"{med * 1e3:.1f} ms, torch CPU ({cpu_model()})"}
+
+
+def load_traffic(name: str):
+    path = os.path.join(ROOT, "profiles", f"traffic_{name}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("bytes_per_launch")
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="qwen-fp16-b64")
+    ap.add_argument("--layers", type=int, default=0, help="layer pools to rotate (0 = auto)")
+    ap.add_argument("--mode", choices=["fused", "split"], default="fused")
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--cpu-reps", type=int, default=5)
+    ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (profiling runs)")
+    ap.add_argument("--partition", type=int, default=0)
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}, "
+              f"WORLD_SIZE={world}", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from tinybatch_amd import _lib, ops
+    from tinybatch_amd.metadata import build_step_metadata
+    from tinybatch_amd.workloads import make_decode_workload
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    _lib.lib()
+
+    big = args.workload == "llama-bf16-b256"
+    t0 = time.perf_counter()
+    wl = make_decode_workload(args.workload, pool_device=(dev if big else "cpu"))
+    _log(f"workload {wl.name}: B={wl.batch} NB={wl.num_blocks} mean ctx={sum(wl.context_lens)/wl.batch:.0f} "
+         f"({time.perf_counter() - t0:.1f}s)")
+    pool_bytes = wl.pool.numel() * wl.pool.element_size()
+    L = args.layers or max(2, min(24, int((2 << 30) // pool_bytes) or 2))
+    storage = torch.empty((L,) + tuple(wl.pool.shape), dtype=wl.dtype, device=dev)
+    src = wl.pool if wl.pool.is_cuda else wl.pool.to(dev)
+    for l in range(L):
+        storage[l].copy_(src)
+    del src
+    pools = [storage[l] for l in range(L)]
+    P = args.partition or int(_lib.lib().tb_attention_partition_tokens())
+    meta = build_step_metadata(wl.positions, wl.seq_slices, wl.block_tables, wl.context_lens,
+                               block_size=wl.block_size, num_blocks=wl.num_blocks, partition_tokens=P).to(dev)
+    q = wl.q.to(dev)
+    k = wl.k_new.to(dev)
+    v = wl.v_new.to(dev)
+    out = torch.empty(wl.batch, wl.num_heads * wl.head_dim, dtype=wl.dtype, device=dev)
+    ws = ops.workspace_for(meta, wl.num_heads, wl.head_dim, dev)
+    fused = args.mode == "fused"
+
+    def step():
+        for pool in pools:
+            if fused:
+                ops.paged_attention(q, pool, meta, num_heads=wl.num_heads, out=out, k_new=k, v_new=v, workspace=ws)
+            else:
+                ops.kv_append(pool, k, v, meta.slot_mapping)
+                ops.paged_attention(q, pool, meta, num_heads=wl.num_heads, out=out, workspace=ws)
+
+    stream = torch.cuda.Stream(device=dev)
+    stream.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(stream):
+        step()                                   # eager warm-up (also exercises every launch)
+    torch.cuda.synchronize()
+    graph = None
+    if not args.no_graph:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            step()
+        torch.cuda.synchronize()
+
+    def run_once():
+        if graph is not None:
+            graph.replay()
+        else:
+            with torch.cuda.stream(stream):
+                step()
+
+    for _ in range(args.warmup):
+        run_once()
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        ev0.record(stream)
+    for _ in range(args.steps):
+        run_once()
+    with torch.cuda.stream(stream):
+        ev1.record(stream)
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / args.steps
+    _log(f"{L} layers x {args.steps} steps: {ms:.4f} ms/step")
+
+    bytes_layer = wl.algorithmic_bytes()
+    total_bytes = bytes_layer["total"] * L
+    gbs = total_bytes / (ms * 1e-3) / 1e9
+    per_launch_ms = ms / (L if fused else L)   # one attention launch per layer (plus the append in split mode)
+    achieved = bytes_layer["total"] / (per_launch_ms * 1e-3) / 1e9
+    traffic = load_traffic(f"{wl.name}_{args.mode}")
+
+    cpu = None
+    if not args.no_cpu:
+        _log("timing the CPU baseline (oracle) ...")
+        if big:
+            wl_cpu = make_decode_workload(args.workload, pool_device="cpu", batch=16)
+        else:
+            wl_cpu = wl
+        cpu = cpu_baseline(wl_cpu, args.cpu_reps, args.cpu_budget)
+        if big:
+            cpu["sample"] += " (first 16 sequences of the workload)"
+
+    kernel = "paged_attn_valu_kernel" + ("" if fused else " + kv_append_kernel")
+    line = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {torch.float16: "f16", torch.bfloat16: "bf16", torch.float32: "f32"}[wl.dtype],
+        "data": "synthetic (seeded N(0,1) pool, q, k, v; seeded random block tables)",
+        "config": {
+            "workload": f"{wl.name}: decode step, append 1 token/seq + paged attention, {L} layer pools",
+            "batch": wl.batch, "num_heads": wl.num_heads, "num_kv_heads": wl.num_kv_heads,
+            "head_dim": wl.head_dim, "block_size": wl.block_size, "num_blocks": wl.num_blocks,
+            "mean_context": round(sum(wl.context_lens) / wl.batch, 1), "layers": L,
+            "mode": args.mode, "graph": graph is not None, "partition_tokens": P,
+            "bytes_per_layer_step": bytes_layer["total"],
+        },
+        "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+        "roofline": {
+            "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": kernel,
+            "avg_launch_us": round(per_launch_ms * 1e3, 3),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

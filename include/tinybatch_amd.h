@@ -1,0 +1,153 @@
+/*
+ * tinybatch_amd — C ABI of the MI355X (gfx950) paged KV-cache data path.
+ *
+ * Every entry point takes plain device pointers, integer sizes, a dtype code and
+ * the HIP stream to launch on. Nothing here allocates, synchronises or throws:
+ * each call enqueues kernels on `stream` and returns a status code
+ * (TB_OK = 0, negative on a rejected argument or a failed launch).
+ * All kernels are stateless, so calls are reentrant; calls on one stream run
+ * in issue order, which is how the "all K/V appended before any attention
+ * read" ordering of the reference forward pass is kept
+ * (reference: src/tinybatch/model.py:127-132).
+ *
+ * Pool layout, unchanged from the reference (src/tinybatch/kv_cache.py:1-7,17-20):
+ *   pool[num_blocks][2][num_kv_heads][block_size][head_dim]   (axis 1: 0 = K, 1 = V)
+ * Slot contract (src/tinybatch/block_manager.py, kv_cache.py:35-36):
+ *   slot(pos) = table[pos / block_size] * block_size + pos % block_size
+ */
+#ifndef TINYBATCH_AMD_H
+#define TINYBATCH_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define TB_OK 0
+#define TB_ERR_INVALID_ARG (-1)  /* null pointer, bad size, inconsistent shape */
+#define TB_ERR_UNSUPPORTED (-2)  /* shape/dtype combination with no compiled kernel */
+#define TB_ERR_LAUNCH (-3)       /* hipLaunchKernel reported an error */
+
+/* element type of q / k / v / pool / out */
+#define TB_DTYPE_F32 0
+#define TB_DTYPE_F16 1
+#define TB_DTYPE_BF16 2
+
+/* Human-readable text for a status code (static storage). */
+const char* tb_status_string(int32_t status);
+
+/* ---------------------------------------------------------------------------
+ * K1 — KV append.
+ * Replaces PagedKVCache.write (src/tinybatch/kv_cache.py:25-38): for every
+ * token t with slot_mapping[t] >= 0,
+ *   pool[slot/BS][0][h][slot%BS][:] = k[t][h][:]
+ *   pool[slot/BS][1][h][slot%BS][:] = v[t][h][:]      for all kv heads h.
+ * Tokens with a negative slot are skipped (the host marks all but the last
+ * writer of a duplicated slot this way, so the result equals the reference's
+ * sequential "last sequence in batch order wins").
+ * k, v: [num_tokens][num_kv_heads][head_dim], token row stride in elements.
+ * Bytes are copied verbatim (bit-exact for every dtype).
+ */
+int32_t tb_kv_append(const void* k, int64_t k_row_stride,
+                     const void* v, int64_t v_row_stride,
+                     void* pool, int64_t num_blocks,
+                     const int32_t* slot_mapping, int32_t num_tokens,
+                     int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                     int32_t dtype, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Paged gather of one sequence into contiguous K and V.
+ * Replaces PagedKVCache.gather (src/tinybatch/kv_cache.py:40-45):
+ *   k_out[t][h][:] = pool[table[t/BS]][0][h][t%BS][:],  v_out likewise with 1,
+ * for t < context_len. k_out, v_out: [context_len][num_kv_heads][head_dim].
+ */
+int32_t tb_kv_gather(const void* pool, int64_t num_blocks,
+                     const int32_t* table, int32_t context_len,
+                     void* k_out, void* v_out,
+                     int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                     int32_t dtype, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * K2 — fused paged attention (decode rows and prefill rows on the VALU path).
+ * Replaces the per-sequence loop of Qwen2Paged.forward
+ * (src/tinybatch/model.py:130-147: gather, GQA repeat_interleave, offset-causal
+ * mask, scaled_dot_product_attention, attn_out assembly).
+ *
+ * Query row r (a token of the flat batch) of sequence b attends to positions
+ * j < row_ctx[r] = context_len[b] - q_len[b] + i + 1 of its sequence, i being
+ * the row's index inside the sequence (the mask j <= ctx - q_len + i of
+ * model.py:142-145, which is also is_causal when q_len == ctx). Query head h
+ * reads kv head h / (num_heads / num_kv_heads) (repeat_interleave, model.py:136-137).
+ *   q:   [num_rows][num_heads][head_dim], row stride q_row_stride (elements)
+ *   out: [num_rows][num_heads * head_dim], row stride out_row_stride
+ *   block_tables: [num_seqs][max_blocks_per_seq] int32 physical block ids
+ *   work_items: [num_work_items][4] int32 = (row, seq, partition, row_ctx);
+ *     partition p covers positions [p*P, min((p+1)*P, row_ctx)) with
+ *     P = partition_tokens (a multiple of 64 and of block_size, at most
+ *     64 blocks; tb_attention_partition_tokens() is the default). Every row
+ *     lists partitions 0 .. ceil(row_ctx/P)-1, row_part_offsets[num_rows+1]
+ *     is their running count (row r owns partial slots
+ *     row_part_offsets[r] ..), total_partitions = row_part_offsets[num_rows]
+ *     and max_parts_per_row is the largest per-row count.
+ *   workspace: >= tb_paged_attention_workspace_bytes(total_partitions, ...)
+ *     bytes of device memory; only touched when a row has > 1 partition.
+ * Fused decode append (k_new != NULL): each row's own newest position
+ * row_ctx-1 is read from k_new/v_new ([num_rows][num_kv_heads][head_dim]) and
+ * written to its slot in the pool by the same kernel, replacing a separate
+ * tb_kv_append. Valid only when no row reads another row's newest slot, which
+ * holds for a batch of decode rows (one new token per sequence).
+ */
+int32_t tb_attention_partition_tokens(void);
+
+size_t tb_paged_attention_workspace_bytes(int32_t total_partitions, int32_t num_heads,
+                                          int32_t head_dim);
+
+int32_t tb_paged_attention(const void* q, int64_t q_row_stride,
+                           void* pool, int64_t num_blocks,
+                           void* out, int64_t out_row_stride,
+                           const int32_t* block_tables, int32_t max_blocks_per_seq,
+                           const int32_t* work_items, int32_t num_work_items,
+                           const int32_t* row_part_offsets, int32_t num_rows,
+                           int32_t max_parts_per_row, int32_t partition_tokens,
+                           int32_t total_partitions,
+                           int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                           int32_t block_size, float scale, int32_t dtype,
+                           const void* k_new, int64_t k_row_stride,
+                           const void* v_new, int64_t v_row_stride,
+                           void* workspace, size_t workspace_bytes,
+                           hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * K3 — block copy across every layer pool in one launch.
+ * No reference counterpart: the reference shares blocks copy-free
+ * (README.md:22) and evicts by metadata only (src/tinybatch/block_manager.py:68-80).
+ * This is the data movement behind eviction compaction and copy-on-write:
+ *   for every layer l and pair i: pool_l[dst[i]] = pool_l[src[i]]   (block_bytes each)
+ * layer_pools: device array of num_layers pool base addresses.
+ * dst ids must be distinct and disjoint from the src ids (checked by the host
+ * wrapper), so the result does not depend on execution order.
+ */
+int32_t tb_block_copy(const uint64_t* layer_pools, int32_t num_layers, int64_t num_blocks,
+                      const int32_t* src_blocks, const int32_t* dst_blocks, int32_t num_pairs,
+                      int64_t block_bytes, hipStream_t stream);
+
+/* Swap-out / swap-in halves of K3 for one pool: staging[i] <-> pool[blocks[i]]
+ * (block_bytes each); staging may be device or pinned host memory.
+ * Reference counterpart: none (preemption recomputes instead of swapping,
+ * src/tinybatch/scheduler.py:141-149). */
+int32_t tb_block_gather(const void* pool, int64_t num_blocks, const int32_t* blocks,
+                        int32_t num_blocks_to_move, void* staging, int64_t block_bytes,
+                        hipStream_t stream);
+int32_t tb_block_scatter(const void* staging, void* pool, int64_t num_blocks,
+                         const int32_t* blocks, int32_t num_blocks_to_move,
+                         int64_t block_bytes, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TINYBATCH_AMD_H */

@@ -1,0 +1,94 @@
+"""The C-ABI library loads and exports every entry point include/tinybatch_amd.h declares.
+
+No kernel is launched: the argument checks below return before any HIP call,
+so these run on a machine without a GPU.
+"""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from tinybatch_amd import _lib
+from tinybatch_amd.build import LIB_PATH
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "tinybatch_amd.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^(?:const char\*|int32_t|size_t)\s+(tb_\w+)\(", text, re.M)))
+
+
+def test_library_built():
+    assert os.path.exists(LIB_PATH), "run python -m tinybatch_amd.build"
+
+
+def test_every_declared_symbol_is_exported():
+    names = _declared()
+    assert len(names) >= 9
+    out = subprocess.run(["nm", "-D", "--defined-only", LIB_PATH], capture_output=True, text=True, check=True).stdout
+    exported = {l.split()[-1] for l in out.splitlines() if l.strip()}
+    missing = [n for n in names if n not in exported]
+    assert not missing, missing
+    # and the ctypes binding covers exactly the header
+    assert sorted(_lib.SIGNATURES) == names
+
+
+def test_status_strings():
+    L = _lib.lib()
+    assert L.tb_status_string(0) == b"ok"
+    assert b"invalid" in L.tb_status_string(-1)
+    assert b"unsupported" in L.tb_status_string(-2)
+
+
+def test_append_rejects_bad_arguments_without_launching():
+    L = _lib.lib()
+    fake = ctypes.c_void_p(4096)
+    # unknown dtype
+    assert L.tb_kv_append(fake, 128, fake, 128, fake, 16, fake, 4, 2, 64, 16, 7, None) == _lib.TB_ERR_INVALID_ARG
+    # block size not a power of two
+    assert L.tb_kv_append(fake, 128, fake, 128, fake, 16, fake, 4, 2, 64, 12, 1, None) == _lib.TB_ERR_INVALID_ARG
+    # head_dim whose rows are not whole 16-byte vectors
+    assert L.tb_kv_append(fake, 120, fake, 120, fake, 16, fake, 4, 2, 60, 16, 1, None) == _lib.TB_ERR_UNSUPPORTED
+    # zero tokens is a no-op
+    assert L.tb_kv_append(None, 128, None, 128, fake, 16, None, 0, 2, 64, 16, 1, None) == _lib.TB_OK
+
+
+def test_attention_rejects_bad_arguments_without_launching():
+    L = _lib.lib()
+    f = ctypes.c_void_p(4096)
+
+    def call(**kw):
+        a = dict(q=f, qs=896, pool=f, nb=64, out=f, os=896, bt=f, mnb=4, work=f, nw=2, rpo=f, nr=2,
+                 mpr=1, pt=256, tp=2, hq=14, hkv=2, d=64, bs=16, scale=0.125, dt=1,
+                 kn=None, ks=0, vn=None, vs=0, ws=None, wsb=0)
+        a.update(kw)
+        return L.tb_paged_attention(a["q"], a["qs"], a["pool"], a["nb"], a["out"], a["os"], a["bt"], a["mnb"],
+                                    a["work"], a["nw"], a["rpo"], a["nr"], a["mpr"], a["pt"], a["tp"], a["hq"],
+                                    a["hkv"], a["d"], a["bs"], a["scale"], a["dt"], a["kn"], a["ks"], a["vn"],
+                                    a["vs"], a["ws"], a["wsb"], None)
+
+    assert call(d=96) == _lib.TB_ERR_UNSUPPORTED               # no kernel for head_dim 96
+    assert call(hq=13) == _lib.TB_ERR_INVALID_ARG              # heads not a multiple of kv heads
+    assert call(pt=100) == _lib.TB_ERR_INVALID_ARG             # partition not a whole number of chunks
+    assert call(bs=2048, pt=256) == _lib.TB_ERR_INVALID_ARG    # partition shorter than a block
+    assert call(mpr=3, ws=None) == _lib.TB_ERR_INVALID_ARG     # split rows need a workspace
+    assert call(kn=f, vn=None) == _lib.TB_ERR_INVALID_ARG      # fused append needs both k and v
+    assert call(nw=0) == _lib.TB_OK                            # empty step: nothing to launch
+
+
+def test_workspace_size_formula():
+    L = _lib.lib()
+    assert L.tb_paged_attention_workspace_bytes(10, 14, 64) == 10 * 14 * 66 * 4
+    assert L.tb_paged_attention_workspace_bytes(0, 14, 64) == 0
+
+
+def test_copy_rejects_bad_arguments_without_launching():
+    L = _lib.lib()
+    f = ctypes.c_void_p(4096)
+    assert L.tb_block_copy(f, 2, 16, f, f, 3, 100, None) == _lib.TB_ERR_INVALID_ARG   # not 16-byte blocks
+    assert L.tb_block_copy(f, 2, 16, f, f, 0, 4096, None) == _lib.TB_OK
+    assert L.tb_block_gather(f, 16, f, 3, f, 0, None) == _lib.TB_ERR_INVALID_ARG
+    assert L.tb_block_scatter(f, f, 0, f, 3, 4096, None) == _lib.TB_ERR_INVALID_ARG   # empty pool

@@ -1,0 +1,244 @@
+"""Parity of the HIP kernels (through the C ABI) with the CPU oracle.
+
+Bars: append / gather / copy bit-exact; attention max-abs <= 1e-5 at fp32 and
+rtol = atol = 2e-2 at fp16 / bf16, against the oracle in the same dtype.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import reference_path as ref
+from tinybatch_amd import ops
+from tinybatch_amd.kv_cache import PagedKVCache
+from tinybatch_amd.metadata import build_step_metadata
+from tinybatch_amd.workloads import make_decode_workload
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+TOL = {torch.float32: dict(atol=1e-5, rtol=0.0), torch.float16: dict(atol=2e-2, rtol=2e-2),
+       torch.bfloat16: dict(atol=2e-2, rtol=2e-2)}
+
+
+def _bits(t: torch.Tensor) -> torch.Tensor:
+    return t.contiguous().view(torch.int32 if t.element_size() == 4 else torch.int16)
+
+
+def _meta(positions, slices, tables, ctx, BS, NB, P=256):
+    return build_step_metadata(positions, slices, tables, ctx, block_size=BS, num_blocks=NB,
+                               partition_tokens=P).to(DEV)
+
+
+def _mixed_case(seed, Hq, Hkv, D, BS, dtype, qlens, cached, NB=None, nan_tail=False):
+    g = torch.Generator().manual_seed(seed)
+    need = [(c + n + BS - 1) // BS for c, n in zip(cached, qlens)]
+    NB = NB or sum(need) + 3
+    pool = torch.randn(NB, 2, Hkv, BS, D, generator=g).to(dtype)
+    perm = torch.randperm(NB, generator=g).tolist()
+    tables, slices, ctx, pos, at, t = [], [], [], [], 0, 0
+    for c, n, nb in zip(cached, qlens, need):
+        tables.append(perm[at:at + nb]); at += nb
+        slices.append((t, t + n)); t += n
+        ctx.append(c + n)
+        pos.extend(range(c, c + n))
+    if nan_tail:
+        # stale slots past every context hold NaN; they must never reach the output
+        for table, c in zip(tables, ctx):
+            last = table[-1]
+            off = c % BS
+            if off:
+                pool[last, :, :, off:] = float("nan")
+        for b in perm[at:]:
+            pool[b] = float("nan")
+    q = torch.randn(t, Hq, D, generator=g).to(dtype)
+    k = torch.randn(t, Hkv, D, generator=g).to(dtype)
+    v = torch.randn(t, Hkv, D, generator=g).to(dtype)
+    return dict(pool=pool, tables=tables, slices=slices, ctx=ctx, pos=pos, q=q, k=k, v=v, NB=NB)
+
+
+# ---------------------------------------------------------------- K1 append
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_append_bit_exact_mixed_batch(dtype):
+    c = _mixed_case(1, 8, 2, 64, 16, dtype, qlens=[5, 1, 17, 1], cached=[0, 40, 3, 15])
+    want = c["pool"].clone()
+    ref.kv_write(want, c["k"], c["v"], torch.tensor(c["pos"]), c["slices"], c["tables"], 16)
+    pool = c["pool"].to(DEV)
+    meta = _meta(c["pos"], c["slices"], c["tables"], c["ctx"], 16, c["NB"])
+    ops.kv_append(pool, c["k"].to(DEV), c["v"].to(DEV), meta.slot_mapping)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(pool.cpu()), _bits(want))
+
+
+def test_append_through_drop_in_write_config_shapes():
+    for name in ("qwen-fp32-b8", "qwen-fp16-b64"):
+        wl = make_decode_workload(name)
+        want = wl.pool.clone()
+        ref.kv_write(want, wl.k_new, wl.v_new, torch.tensor(wl.positions), wl.seq_slices, wl.block_tables, 16)
+        cache = PagedKVCache(1, wl.num_blocks, 16, wl.num_kv_heads, wl.head_dim, DEV, wl.dtype)
+        cache.pools[0].copy_(wl.pool.to(DEV))
+        cache.write(0, wl.k_new.to(DEV), wl.v_new.to(DEV), torch.tensor(wl.positions, device=DEV),
+                    wl.seq_slices, wl.block_tables)
+        torch.cuda.synchronize()
+        assert torch.equal(_bits(cache.pools[0].cpu()), _bits(want)), name
+
+
+def test_append_duplicate_slot_last_writer_wins():
+    dtype = torch.float16
+    pool = torch.zeros(4, 2, 2, 4, 64, dtype=dtype)
+    k = torch.randn(2, 2, 64).to(dtype)
+    v = torch.randn(2, 2, 64).to(dtype)
+    want = pool.clone()
+    ref.kv_write(want, k, v, torch.tensor([3, 3]), [(0, 1), (1, 2)], [[2], [2]], 4)
+    gp = pool.to(DEV)
+    meta = _meta([3, 3], [(0, 1), (1, 2)], [[2], [2]], [4, 4], 4, 4, P=64)
+    ops.kv_append(gp, k.to(DEV), v.to(DEV), meta.slot_mapping)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(gp.cpu()), _bits(want))
+
+
+# ---------------------------------------------------------------- gather
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_gather_bit_exact(dtype):
+    c = _mixed_case(2, 8, 4, 128, 16, dtype, qlens=[1, 1], cached=[37, 130])
+    cache = PagedKVCache(1, c["NB"], 16, 4, 128, DEV, dtype)
+    cache.pools[0].copy_(c["pool"].to(DEV))
+    for table, ctx in zip(c["tables"], c["ctx"]):
+        k, v = cache.gather(0, table, ctx)
+        K, V = ref.kv_gather(c["pool"], table, ctx)
+        assert torch.equal(_bits(k.cpu()), _bits(K)) and torch.equal(_bits(v.cpu()), _bits(V))
+
+
+# ---------------------------------------------------------------- K2 attention
+def _attention_vs_oracle(c, Hq, Hkv, dtype, P=256):
+    want = ref.attention(c["q"], c["pool"], c["slices"], c["tables"], c["ctx"], Hq, Hkv)
+    meta = _meta(c["pos"], c["slices"], c["tables"], c["ctx"], c["pool"].shape[3], c["NB"], P=P)
+    out = ops.paged_attention(c["q"].to(DEV), c["pool"].to(DEV), meta, num_heads=Hq)
+    torch.cuda.synchronize()
+    got = out.cpu()
+    assert torch.isfinite(got).all()
+    torch.testing.assert_close(got.float(), want.float(), **TOL[dtype])
+    return got, want
+
+
+def test_decode_config1_fp32_within_1e5():
+    wl = make_decode_workload("qwen-fp32-b8")
+    want = ref.decode_step(wl.pool.clone(), wl.q, wl.k_new, wl.v_new, wl.cached_lens, wl.block_tables,
+                           14, 2, 16)
+    cache = PagedKVCache(1, wl.num_blocks, 16, 2, 64, DEV, torch.float32)
+    cache.pools[0].copy_(wl.pool.to(DEV))
+    pos = torch.tensor(wl.positions, device=DEV)
+    cache.write(0, wl.k_new.to(DEV), wl.v_new.to(DEV), pos, wl.seq_slices, wl.block_tables)
+    got = cache.attention(0, wl.q.to(DEV), pos, wl.seq_slices, wl.block_tables, wl.context_lens)
+    torch.cuda.synchronize()
+    assert (got.cpu() - want).abs().max().item() <= 1e-5
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_decode_config2_fp16_full_size(fused):
+    wl = make_decode_workload("qwen-fp16-b64")
+    pool_ref = wl.pool.clone()
+    want = ref.decode_step(pool_ref, wl.q, wl.k_new, wl.v_new, wl.cached_lens, wl.block_tables, 14, 2, 16)
+    pool = wl.pool.to(DEV)
+    meta = _meta(wl.positions, wl.seq_slices, wl.block_tables, wl.context_lens, 16, wl.num_blocks)
+    q, k, v = wl.q.to(DEV), wl.k_new.to(DEV), wl.v_new.to(DEV)
+    if fused:
+        out = ops.paged_attention(q, pool, meta, num_heads=14, k_new=k, v_new=v)
+    else:
+        ops.kv_append(pool, k, v, meta.slot_mapping)
+        out = ops.paged_attention(q, pool, meta, num_heads=14)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out.cpu().float(), want.float(), **TOL[torch.float16])
+    # the appended rows land bit-exactly in both modes
+    assert torch.equal(_bits(pool.cpu()), _bits(pool_ref))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("Hq,Hkv,D", [(14, 2, 64), (32, 8, 128), (4, 4, 64), (28, 2, 128), (6, 1, 64)])
+def test_mixed_batch_attention_shapes(dtype, Hq, Hkv, D):
+    c = _mixed_case(3, Hq, Hkv, D, 16, dtype, qlens=[1, 7, 1, 20, 1], cached=[600, 0, 15, 300, 1])
+    _attention_vs_oracle(c, Hq, Hkv, dtype)
+
+
+@pytest.mark.parametrize("BS,P", [(4, 128), (8, 256), (32, 512), (64, 1024)])
+def test_block_sizes_and_partitions(BS, P):
+    c = _mixed_case(4, 14, 2, 64, BS, torch.float32, qlens=[1, 3, 1], cached=[700, 90, 2])
+    _attention_vs_oracle(c, 14, 2, torch.float32, P=P)
+
+
+def test_stale_nan_slots_never_reach_output():
+    c = _mixed_case(5, 14, 2, 64, 16, torch.float16, qlens=[1, 1, 5], cached=[33, 300, 10], nan_tail=True)
+    _attention_vs_oracle(c, 14, 2, torch.float16)
+
+
+def test_permuted_blocks_identical_output():
+    c = _mixed_case(6, 8, 2, 64, 16, torch.bfloat16, qlens=[1, 1], cached=[500, 77])
+    meta = _meta(c["pos"], c["slices"], c["tables"], c["ctx"], 16, c["NB"])
+    out1 = ops.paged_attention(c["q"].to(DEV), c["pool"].to(DEV), meta, num_heads=8)
+    perm = torch.randperm(c["NB"], generator=torch.Generator().manual_seed(1))
+    pool2 = torch.empty_like(c["pool"])
+    pool2[perm] = c["pool"]
+    tables2 = [[int(perm[b]) for b in t] for t in c["tables"]]
+    meta2 = _meta(c["pos"], c["slices"], tables2, c["ctx"], 16, c["NB"])
+    out2 = ops.paged_attention(c["q"].to(DEV), pool2.to(DEV), meta2, num_heads=8)
+    torch.cuda.synchronize()
+    assert torch.equal(out1.cpu(), out2.cpu())
+
+
+def test_long_context_split_into_many_partitions():
+    c = _mixed_case(7, 32, 8, 128, 16, torch.bfloat16, qlens=[1, 1], cached=[20000, 4095])
+    _attention_vs_oracle(c, 32, 8, torch.bfloat16)
+
+
+def test_config3_subset_bf16():
+    """Llama-3-8B decode geometry; the pool is drawn on the GPU, 8 sequences checked."""
+    wl = make_decode_workload("llama-bf16-b256", pool_device=DEV, batch=8)
+    meta = _meta(wl.positions, wl.seq_slices, wl.block_tables, wl.context_lens, 16, wl.num_blocks)
+    pool = wl.pool
+    out = ops.paged_attention(wl.q.to(DEV), pool, meta, num_heads=32, k_new=wl.k_new.to(DEV),
+                              v_new=wl.v_new.to(DEV))
+    torch.cuda.synchronize()
+    pool_cpu = pool.cpu()
+    want = ref.attention(wl.q, pool_cpu, wl.seq_slices, wl.block_tables, wl.context_lens, 32, 8)
+    torch.testing.assert_close(out.cpu().float(), want.float(), **TOL[torch.bfloat16])
+
+
+# ---------------------------------------------------------------- K3 copy
+def test_block_copy_all_layers_bit_exact():
+    cache = PagedKVCache(3, 64, 16, 2, 64, DEV, torch.bfloat16)
+    g = torch.Generator().manual_seed(8)
+    host = torch.randn(3, 64, 2, 2, 16, 64, generator=g).to(torch.bfloat16)
+    cache.storage.copy_(host.to(DEV))
+    src, dst = [1, 5, 9, 33], [40, 2, 63, 0]
+    cache.copy_blocks(src, dst)
+    torch.cuda.synchronize()
+    want = host.clone()
+    for layer in range(3):
+        for s, d in zip(src, dst):
+            want[layer, d] = host[layer, s]
+    assert torch.equal(_bits(cache.storage.cpu()), _bits(want))
+
+
+def test_block_copy_rejects_overlapping_pairs():
+    cache = PagedKVCache(1, 8, 16, 2, 64, DEV, torch.float16)
+    with pytest.raises(ValueError):
+        cache.copy_blocks([1, 2], [2, 3])
+    with pytest.raises(IndexError):
+        cache.copy_blocks([1], [8])
+
+
+def test_swap_out_swap_in_roundtrip_pinned_host():
+    cache = PagedKVCache(2, 32, 16, 2, 64, DEV, torch.float16)
+    host = torch.randn(2, 32, 2, 2, 16, 64).to(torch.float16)
+    cache.storage.copy_(host.to(DEV))
+    blocks = [3, 17, 30]
+    staging = [torch.empty(3, 2, 2, 16, 64, dtype=torch.float16, pin_memory=True) for _ in range(2)]
+    cache.swap_out(blocks, staging)
+    torch.cuda.synchronize()
+    for layer in range(2):
+        assert torch.equal(_bits(staging[layer]), _bits(host[layer, blocks]))
+    cache.storage.zero_()
+    cache.swap_in(staging, [0, 1, 2])
+    torch.cuda.synchronize()
+    for layer in range(2):
+        assert torch.equal(_bits(cache.storage[layer, :3].cpu()), _bits(host[layer, blocks]))

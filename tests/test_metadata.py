@@ -1,0 +1,82 @@
+"""Host-side step metadata: slot mapping, work list and the reference's error behaviour."""
+import numpy as np
+import pytest
+import torch
+
+from tinybatch_amd.metadata import build_step_metadata
+
+
+def _mixed():
+    # seq0: prefill of 5 (ctx 5); seq1: decode at position 9 (ctx 10); seq2: tail prefill 3 of ctx 7
+    positions = [0, 1, 2, 3, 4, 9, 4, 5, 6]
+    slices = [(0, 5), (5, 6), (6, 9)]
+    tables = [[7, 3], [1, 4, 0], [5, 6]]
+    ctx = [5, 10, 7]
+    return positions, slices, tables, ctx
+
+
+def test_slot_mapping_follows_table_rule():
+    pos, sl, tb, ctx = _mixed()
+    m = build_step_metadata(pos, sl, tb, ctx, block_size=4, num_blocks=8, partition_tokens=64)
+    want = []
+    for (s, e), t in zip(sl, tb):
+        for i in range(s, e):
+            want.append(t[pos[i] // 4] * 4 + pos[i] % 4)
+    assert m.slot_mapping_np.tolist() == want
+
+
+def test_work_items_cover_every_row_and_partition():
+    pos, sl, tb, ctx = _mixed()
+    m = build_step_metadata(pos, sl, tb, ctx, block_size=4, num_blocks=8, partition_tokens=4)
+    items = []
+    for (s, e), c in zip(sl, ctx):
+        n = e - s
+        for i in range(n):
+            row_ctx = c - n + i + 1
+            for p in range((row_ctx + 3) // 4):
+                items.append((s + i, sl.index((s, e)), p, row_ctx))
+    assert [tuple(x) for x in m.work_np.tolist()] == items
+    counts = np.diff(m.row_part_off_np)
+    for r in range(len(pos)):
+        assert counts[r] == sum(1 for it in items if it[0] == r)
+    assert m.max_parts_per_row == max(counts)
+    assert not m.decode_only
+
+
+def test_duplicate_slots_keep_the_last_writer():
+    # two sequences rewrite the same slot (fully cached prompt sharing one block)
+    m = build_step_metadata([3, 3], [(0, 1), (1, 2)], [[2], [2]], [4, 4], block_size=4, num_blocks=4,
+                            partition_tokens=64)
+    assert m.slot_mapping_np.tolist() == [-1, 11]
+
+
+def test_short_table_raises_index_error_like_the_reference():
+    with pytest.raises(IndexError):
+        build_step_metadata([8], [(0, 1)], [[0, 1]], [9], block_size=4, num_blocks=4, partition_tokens=64)
+    # write path alone (no context lengths) also checks the position
+    with pytest.raises(IndexError):
+        build_step_metadata([8], [(0, 1)], [[0, 1]], None, block_size=4, num_blocks=4, partition_tokens=64)
+
+
+def test_block_outside_pool_raises_index_error():
+    with pytest.raises(IndexError):
+        build_step_metadata([0], [(0, 1)], [[9]], [1], block_size=4, num_blocks=4, partition_tokens=64)
+
+
+def test_context_shorter_than_new_tokens_rejected():
+    with pytest.raises(ValueError):
+        build_step_metadata([0, 1], [(0, 2)], [[0]], [1], block_size=4, num_blocks=4, partition_tokens=64)
+
+
+def test_decode_only_flag_and_device_tensor_positions():
+    m = build_step_metadata(torch.tensor([5, 17]), [(0, 1), (1, 2)], [[0, 1], [2, 3, 4, 5, 6]], [6, 18],
+                            block_size=4, num_blocks=8, partition_tokens=64)
+    assert m.decode_only
+    assert m.slot_mapping_np.tolist() == [1 * 4 + 1, 6 * 4 + 1]
+
+
+def test_off_by_one_of_block_multiple_prompt_is_refused():
+    """A 16-token prompt owns exactly one block of 16; its first decode writes
+    position 16, which needs a second block (the engine must reserve it)."""
+    with pytest.raises(IndexError):
+        build_step_metadata([16], [(0, 1)], [[3]], [17], block_size=16, num_blocks=8, partition_tokens=256)

@@ -1,0 +1,97 @@
+"""ctypes binding of libtinybatch_amd.so (the C ABI in include/tinybatch_amd.h).
+
+The library must be built (``python -m tinybatch_amd.build``); there is no
+fallback path: every op raises if the library or a GPU is missing.
+torch is imported first so that the library's ``libamdhip64.so.7`` dependency
+binds to the HIP runtime torch already loaded (same SONAME) and both share one
+runtime, one device context and torch's streams.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (must be loaded before the library, see above)
+
+from .build import LIB_PATH
+
+TB_OK = 0
+TB_ERR_INVALID_ARG = -1
+TB_ERR_UNSUPPORTED = -2
+TB_ERR_LAUNCH = -3
+
+DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+
+c_i32, c_i64, c_f32, c_sz, c_vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t, ctypes.c_void_p
+
+# name -> (restype, argtypes); mirrors include/tinybatch_amd.h
+SIGNATURES = {
+    "tb_status_string": (ctypes.c_char_p, [c_i32]),
+    "tb_kv_append": (c_i32, [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp]),
+    "tb_kv_gather": (c_i32, [c_vp, c_i64, c_vp, c_i32, c_vp, c_vp, c_i32, c_i32, c_i32, c_i32, c_vp]),
+    "tb_attention_partition_tokens": (c_i32, []),
+    "tb_paged_attention_workspace_bytes": (c_sz, [c_i32, c_i32, c_i32]),
+    "tb_paged_attention": (c_i32, [
+        c_vp, c_i64,            # q, q_row_stride
+        c_vp, c_i64,            # pool, num_blocks
+        c_vp, c_i64,            # out, out_row_stride
+        c_vp, c_i32,            # block_tables, max_blocks_per_seq
+        c_vp, c_i32,            # work_items, num_work_items
+        c_vp, c_i32,            # row_part_offsets, num_rows
+        c_i32, c_i32, c_i32,    # max_parts_per_row, partition_tokens, total_partitions
+        c_i32, c_i32, c_i32, c_i32,  # num_heads, num_kv_heads, head_dim, block_size
+        c_f32, c_i32,           # scale, dtype
+        c_vp, c_i64, c_vp, c_i64,  # k_new, k_row_stride, v_new, v_row_stride
+        c_vp, c_sz, c_vp,       # workspace, workspace_bytes, stream
+    ]),
+    "tb_block_copy": (c_i32, [c_vp, c_i32, c_i64, c_vp, c_vp, c_i32, c_i64, c_vp]),
+    "tb_block_gather": (c_i32, [c_vp, c_i64, c_vp, c_i32, c_vp, c_i64, c_vp]),
+    "tb_block_scatter": (c_i32, [c_vp, c_vp, c_i64, c_vp, c_i32, c_i64, c_vp]),
+}
+
+_LIB: ctypes.CDLL | None = None
+
+
+def _hip_runtimes_mapped() -> set[str]:
+    paths = set()
+    with open("/proc/self/maps") as f:
+        for line in f:
+            if "libamdhip64" in line:
+                paths.add(os.path.realpath(line.split()[-1]))
+    return paths
+
+
+def lib() -> ctypes.CDLL:
+    """Load (once) and return the library; raises if it has not been built."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"{LIB_PATH} is missing: build it with `python -m tinybatch_amd.build` "
+            "(there is no CPU fallback for the paged KV-cache kernels)")
+    handle = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype = res
+        fn.argtypes = args
+    runtimes = _hip_runtimes_mapped()
+    if len(runtimes) > 1:
+        raise RuntimeError(f"two HIP runtimes are mapped in this process: {sorted(runtimes)}")
+    _LIB = handle
+    return handle
+
+
+def check(status: int, what: str) -> None:
+    if status != TB_OK:
+        msg = lib().tb_status_string(status).decode()
+        raise RuntimeError(f"{what} failed: {msg} (status {status})")
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def require_gpu_tensor(name: str, t: torch.Tensor) -> None:
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be a GPU tensor (no CPU fallback); got device {t.device}")

@@ -1,0 +1,143 @@
+"""Drop-in PagedKVCache backed by the HIP kernels.
+
+Same constructor, attributes and methods as the reference's
+``tinybatch.kv_cache.PagedKVCache`` (src/tinybatch/kv_cache.py:13-45):
+
+* ``pools[layer]`` is a ``[num_blocks, 2, n_kv_heads, block_size, head_dim]``
+  tensor (K = index 0, V = index 1 of axis 1), zero-initialised. The layers are
+  views into one allocation so that K3 can copy a block in every layer with
+  one launch.
+* ``write(layer, k, v, positions, seq_slices, block_tables)`` appends through
+  K1 instead of a per-sequence ``index_put`` loop.
+* ``gather(layer, table, context_len)`` returns contiguous ``[ctx, kvh, hd]``
+  K and V, as the reference does.
+
+Added for the fused data path (no reference counterpart):
+
+* ``attention(layer, q, positions, seq_slices, block_tables, context_lens)``
+  is the whole per-sequence attention region of Qwen2Paged.forward
+  (model.py:130-147) as one K2 launch; returns ``attn_out [T, Hq*D]``.
+* ``copy_blocks(src, dst)`` (K3, every layer) and ``swap_out``/``swap_in``.
+
+The per-step metadata (slot mapping, padded int32 block tables, attention work
+list) is built once and reused by every layer of the step; it is rebuilt when
+the step's arguments change.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib, ops
+from .metadata import StepMetadata, build_step_metadata
+
+
+class PagedKVCache:
+    def __init__(self, n_layers: int, num_blocks: int, block_size: int, n_kv_heads: int, head_dim: int,
+                 device: torch.device, dtype: torch.dtype, partition_tokens: int | None = None):
+        device = torch.device(device)
+        if device.type != "cuda":
+            raise RuntimeError("tinybatch_amd.PagedKVCache needs a GPU device (no CPU fallback)")
+        self.block_size = block_size
+        self.num_blocks = num_blocks
+        self.n_kv_heads = n_kv_heads
+        self.head_dim = head_dim
+        self.dtype = dtype
+        self.device = device
+        self.partition_tokens = partition_tokens or int(_lib.lib().tb_attention_partition_tokens())
+        self.storage = torch.zeros(n_layers, num_blocks, 2, n_kv_heads, block_size, head_dim,
+                                   device=device, dtype=dtype)
+        self.pools = [self.storage[i] for i in range(n_layers)]
+        self._meta_cache: list[dict] = []
+
+    def memory_bytes(self) -> int:
+        return sum(p.numel() * p.element_size() for p in self.pools)
+
+    # ---- per-step metadata -------------------------------------------------
+    def step_metadata(self, positions, seq_slices, block_tables, context_lens=None) -> StepMetadata:
+        """Build (or reuse) the step's device metadata.
+
+        Every layer of a forward pass passes the same argument objects, so the
+        metadata is built once per step: an entry is reused when the positions
+        object is the same one (held by the cache, so its identity cannot be
+        recycled) with an unchanged in-place version, and the slices, tables
+        and context lengths compare equal. write() (no context lengths) may
+        reuse an entry built for attention().
+        """
+        pos_key = (positions, positions._version) if isinstance(positions, torch.Tensor) else list(positions)
+        for e in self._meta_cache:
+            if (_same_positions(e["pos"], pos_key) and e["slices"] == [tuple(x) for x in seq_slices]
+                    and e["tables"] == block_tables
+                    and (context_lens is None or e["ctx"] == context_lens)):
+                return e["meta"]
+        meta = build_step_metadata(positions, seq_slices, block_tables, context_lens,
+                                   block_size=self.block_size, num_blocks=self.num_blocks,
+                                   partition_tokens=self.partition_tokens)
+        meta.to(self.device)
+        entry = {"pos": pos_key, "slices": [tuple(x) for x in seq_slices],
+                 "tables": [list(t) for t in block_tables],
+                 "ctx": None if context_lens is None else list(context_lens), "meta": meta}
+        self._meta_cache = [entry] + self._meta_cache[:1]
+        return meta
+
+    # ---- reference API -----------------------------------------------------
+    def write(self, layer: int, k: torch.Tensor, v: torch.Tensor, positions: torch.Tensor,
+              seq_slices: list[tuple[int, int]], block_tables: list[list[int]]) -> None:
+        """Scatter each new token's K/V into its sequence's blocks (reference kv_cache.py:25-38)."""
+        meta = self._lookup_or_build(positions, seq_slices, block_tables, None, k.shape[0])
+        ops.kv_append(self.pools[layer], k, v, meta.slot_mapping)
+
+    def gather(self, layer: int, table: list[int], context_len: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """Contiguous K, V [context_len, n_kv_heads, head_dim] (reference kv_cache.py:40-45)."""
+        nb_needed = (context_len + self.block_size - 1) // self.block_size
+        if nb_needed > len(table):
+            # the reference slices a shorter gather silently; out-of-table reads are refused here
+            raise IndexError(f"context_len {context_len} needs {nb_needed} blocks, table has {len(table)}")
+        for b in table[:nb_needed]:
+            if not 0 <= b < self.num_blocks:
+                raise IndexError(f"block id {b} outside the pool of {self.num_blocks} blocks")
+        t = torch.tensor(list(table[:max(nb_needed, 1)]), dtype=torch.int32).to(self.device)
+        return ops.kv_gather(self.pools[layer], t, context_len)
+
+    # ---- fused data path ---------------------------------------------------
+    def attention(self, layer: int, q: torch.Tensor, positions, seq_slices, block_tables, context_lens,
+                  *, num_heads: int | None = None, scale: float | None = None,
+                  out: torch.Tensor | None = None) -> torch.Tensor:
+        """attn_out [T, Hq*D] for the whole flat batch (reference model.py:130-147)."""
+        hq = num_heads if num_heads is not None else q.shape[1]
+        meta = self._lookup_or_build(positions, seq_slices, block_tables, context_lens, q.shape[0])
+        return ops.paged_attention(q, self.pools[layer], meta, num_heads=hq, scale=scale, out=out)
+
+    def decode_step(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, meta: StepMetadata,
+                    *, num_heads: int | None = None, scale: float | None = None,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+        """Append + attention of a decode-only step in one launch (fused K1+K2)."""
+        hq = num_heads if num_heads is not None else q.shape[1]
+        return ops.paged_attention(q, self.pools[layer], meta, num_heads=hq, scale=scale, out=out,
+                                   k_new=k, v_new=v)
+
+    def copy_blocks(self, src, dst) -> None:
+        """pool_l[dst[i]] <- pool_l[src[i]] in every layer (K3, one launch)."""
+        ops.block_copy(self.pools, src, dst)
+
+    def swap_out(self, blocks, staging: list[torch.Tensor]) -> None:
+        """staging[l][i] <- pools[l][blocks[i]] for every layer."""
+        for pool, st in zip(self.pools, staging):
+            ops.block_gather(pool, blocks, st)
+
+    def swap_in(self, staging: list[torch.Tensor], blocks) -> None:
+        for pool, st in zip(self.pools, staging):
+            ops.block_scatter(st, pool, blocks)
+
+    def _lookup_or_build(self, positions, seq_slices, block_tables, context_lens, num_tokens) -> StepMetadata:
+        meta = self.step_metadata(positions, seq_slices, block_tables, context_lens)
+        if meta.num_tokens != num_tokens:
+            raise ValueError(f"{num_tokens} tokens given, positions describe {meta.num_tokens}")
+        return meta
+
+
+def _same_positions(a, b) -> bool:
+    if isinstance(a, tuple) and isinstance(b, tuple):
+        return a[0] is b[0] and a[1] == b[1]
+    if isinstance(a, list) and isinstance(b, list):
+        return a == b
+    return False

@@ -1,0 +1,196 @@
+"""Once-per-step device metadata for the paged kernels.
+
+The reference converts each sequence's block table to a device tensor inside
+every layer (src/tinybatch/kv_cache.py:35,43) and builds a boolean mask per
+sequence per layer (src/tinybatch/model.py:142-145). Here the host lists that
+LLMEngine.step produces (src/tinybatch/engine.py:99-126: positions,
+seq_slices, block_tables, context_lens) are turned into int32 arrays once per
+step and uploaded in a single host-to-device copy:
+
+* ``slot_mapping[T]``  - pool slot of every token's new K/V
+  (table[pos // BS] * BS + pos % BS, kv_cache.py:35-36); -1 for tokens outside
+  every slice and for all but the last writer of a duplicated slot, so the
+  parallel append equals the reference's sequential "last in batch order wins".
+* ``block_tables[B, max_nb]`` - tables padded with 0 (padding is never read).
+* ``work[W, 4]`` - (row, seq, partition, row_ctx) for the attention kernel, where
+  row_ctx = ctx - q_len + i + 1 is the number of positions query row i may see
+  (the mask rule j <= ctx - q_len + i of model.py:139-145).
+* ``row_part_off[T + 1]`` - running count of partitions per row.
+
+Errors mirror the reference: a table too short for a position raises
+IndexError (kv_cache.py:35), a block id outside the pool raises IndexError
+(pool indexing, kv_cache.py:37,43).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+
+@dataclass
+class StepMetadata:
+    num_tokens: int
+    num_seqs: int
+    block_size: int
+    partition_tokens: int
+    max_blocks_per_seq: int
+    num_work_items: int
+    total_partitions: int
+    max_parts_per_row: int
+    decode_only: bool            # every sequence has exactly one query row
+    # host copies
+    slot_mapping_np: np.ndarray
+    block_tables_np: np.ndarray
+    work_np: np.ndarray
+    row_part_off_np: np.ndarray
+    row_ctx_np: np.ndarray       # [T] visible positions per row (0 for rows outside slices)
+    # device views (int32, one backing buffer)
+    device_buffer: torch.Tensor | None = None
+    slot_mapping: torch.Tensor | None = None
+    block_tables: torch.Tensor | None = None
+    work: torch.Tensor | None = None
+    row_part_off: torch.Tensor | None = None
+
+    def to(self, device: torch.device) -> "StepMetadata":
+        """Upload every array with one host-to-device copy (views into one buffer)."""
+        parts = [self.slot_mapping_np, self.block_tables_np.reshape(-1), self.work_np.reshape(-1),
+                 self.row_part_off_np]
+        sizes = [_pad4(p.size) for p in parts]
+        host = np.zeros(sum(sizes), dtype=np.int32)
+        offs = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
+        for p, o in zip(parts, offs):
+            host[o:o + p.size] = p.reshape(-1)
+        src = torch.from_numpy(host)
+        if device.type == "cuda":
+            src = src.pin_memory()
+        buf = src.to(device, non_blocking=True)
+        self.device_buffer = buf
+        self.slot_mapping = buf.narrow(0, int(offs[0]), parts[0].size)
+        self.block_tables = buf.narrow(0, int(offs[1]), parts[1].size).view(-1, self.max_blocks_per_seq)
+        self.work = buf.narrow(0, int(offs[2]), parts[2].size).view(-1, 4)
+        self.row_part_off = buf.narrow(0, int(offs[3]), parts[3].size)
+        return self
+
+
+def _pad4(n: int) -> int:
+    return (n + 3) // 4 * 4
+
+
+def _host_positions(positions) -> np.ndarray:
+    if isinstance(positions, torch.Tensor):
+        return positions.detach().to("cpu", torch.int64).numpy().reshape(-1)
+    return np.asarray(positions, dtype=np.int64).reshape(-1)
+
+
+def build_step_metadata(positions, seq_slices, block_tables, context_lens, *, block_size: int,
+                        num_blocks: int, partition_tokens: int, num_tokens: int | None = None,
+                        validate_attention: bool = True) -> StepMetadata:
+    """Build the per-step arrays (host side). See the module docstring."""
+    if block_size <= 0 or block_size & (block_size - 1):
+        raise ValueError(f"block_size must be a power of two, got {block_size}")
+    pos = _host_positions(positions)
+    T = int(pos.size if num_tokens is None else num_tokens)
+    if pos.size != T:
+        raise ValueError(f"positions has {pos.size} entries, expected {T}")
+    B = len(seq_slices)
+    if len(block_tables) != B:
+        raise ValueError("seq_slices and block_tables differ in length")
+    if context_lens is not None and len(context_lens) != B:
+        raise ValueError("seq_slices and context_lens differ in length")
+
+    starts = np.fromiter((s for s, _ in seq_slices), dtype=np.int64, count=B)
+    ends = np.fromiter((e for _, e in seq_slices), dtype=np.int64, count=B)
+    qlens = ends - starts
+    if B and (np.any(starts < 0) or np.any(ends > T) or np.any(qlens < 0)):
+        raise ValueError("seq_slices out of range of the flat batch")
+    tab_lens = np.fromiter((len(t) for t in block_tables), dtype=np.int64, count=B)
+    max_nb = max(1, int(tab_lens.max()) if B else 1)
+    tables = np.zeros((max(B, 1), max_nb), dtype=np.int64)
+    for b, t in enumerate(block_tables):
+        if len(t):
+            tables[b, :len(t)] = t
+    if B:
+        used = np.arange(max_nb)[None, :] < tab_lens[:, None]
+        bad = used & ((tables[:B] < 0) | (tables[:B] >= num_blocks))
+        if bad.any():
+            b, i = np.argwhere(bad)[0]
+            raise IndexError(f"block id {tables[b, i]} of sequence {b} is outside the pool of {num_blocks} blocks")
+
+    # ---- rows (query tokens that belong to a slice) ----
+    tot = int(qlens.sum()) if B else 0
+    row_seq = np.repeat(np.arange(B, dtype=np.int64), qlens)
+    seq_row_base = np.concatenate([[0], np.cumsum(qlens)[:-1]]) if B else np.zeros(0, np.int64)
+    row_i = np.arange(tot, dtype=np.int64) - np.repeat(seq_row_base, qlens)
+    row_ids = np.repeat(starts, qlens) + row_i
+
+    # ---- slot mapping (kv_cache.py:34-38) ----
+    slots = np.full(T, -1, dtype=np.int64)
+    if tot:
+        p = pos[row_ids]
+        if np.any(p < 0):
+            raise ValueError("negative position")
+        bidx = p // block_size
+        over = bidx >= tab_lens[row_seq]
+        if over.any():
+            r = int(np.argmax(over))
+            raise IndexError(f"position {int(p[r])} of sequence {int(row_seq[r])} needs block index "
+                             f"{int(bidx[r])} but its table has {int(tab_lens[row_seq[r]])} blocks")
+        s = tables[row_seq, bidx] * block_size + p % block_size
+        slots[row_ids] = s
+        # last writer wins: keep only the final occurrence of each slot
+        rev = s[::-1]
+        _, first_in_rev = np.unique(rev, return_index=True)
+        keep = np.zeros(tot, dtype=bool)
+        keep[tot - 1 - first_in_rev] = True
+        slots[row_ids[~keep]] = -1
+
+    # ---- attention work items ----
+    P = int(partition_tokens)
+    row_ctx_by_row = np.zeros(T, dtype=np.int64)
+    nparts_by_row = np.zeros(T, dtype=np.int64)
+    if tot and context_lens is not None:
+        ctx = np.asarray(context_lens, dtype=np.int64)
+        if np.any(ctx < qlens):
+            b = int(np.argmax(ctx < qlens))
+            raise ValueError(f"context_len {int(ctx[b])} of sequence {b} is shorter than its {int(qlens[b])} new tokens")
+        if validate_attention:
+            need = (ctx + block_size - 1) // block_size
+            short = (need > tab_lens) & (qlens > 0)
+            if short.any():
+                b = int(np.argmax(short))
+                raise IndexError(f"context_len {int(ctx[b])} of sequence {b} needs {int(need[b])} blocks "
+                                 f"but its table has {int(tab_lens[b])}")
+        row_ctx = np.repeat(ctx - qlens, qlens) + row_i + 1
+        row_ctx_by_row[row_ids] = row_ctx
+        nparts_by_row[row_ids] = (row_ctx + P - 1) // P
+    row_part_off = np.zeros(T + 1, dtype=np.int64)
+    np.cumsum(nparts_by_row, out=row_part_off[1:])
+    W = int(row_part_off[-1])
+    work = np.zeros((W, 4), dtype=np.int64)
+    if W:
+        has = nparts_by_row > 0
+        rows = np.nonzero(has)[0]
+        np_r = nparts_by_row[rows]
+        rep_rows = np.repeat(rows, np_r)
+        work[:, 0] = rep_rows
+        seq_of_row = np.zeros(T, dtype=np.int64)
+        seq_of_row[row_ids] = row_seq
+        work[:, 1] = seq_of_row[rep_rows]
+        work[:, 2] = np.arange(W) - np.repeat(row_part_off[rows], np_r)
+        work[:, 3] = row_ctx_by_row[rep_rows]
+    if max(T, W, max_nb, int(row_part_off[-1])) >= 2**31:
+        raise ValueError("step too large for int32 metadata")
+
+    return StepMetadata(
+        num_tokens=T, num_seqs=B, block_size=block_size, partition_tokens=P,
+        max_blocks_per_seq=max_nb, num_work_items=W, total_partitions=W,
+        max_parts_per_row=int(nparts_by_row.max()) if T else 0,
+        decode_only=bool(B) and bool(np.all(qlens == 1)),
+        slot_mapping_np=slots.astype(np.int32),
+        block_tables_np=tables[:max(B, 1)].astype(np.int32),
+        work_np=work.astype(np.int32),
+        row_part_off_np=row_part_off.astype(np.int32),
+        row_ctx_np=row_ctx_by_row.astype(np.int32),
+    )

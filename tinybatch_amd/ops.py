@@ -1,0 +1,224 @@
+"""Functional wrappers over the C ABI: argument checks, then one ctypes call.
+
+Every function launches on the current torch stream of the tensors' device
+and returns without synchronising. Temporary device arguments (block-id
+lists, pointer arrays) come from torch's caching allocator on that same
+stream, so their reuse is ordered after the kernel that reads them. Errors are raised on the host before any
+launch: shape/dtype/device mismatches as ValueError/TypeError, out-of-range
+block ids or positions as IndexError (as the reference's tensor indexing
+would), and a rejected launch as RuntimeError.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+from . import _lib
+from .metadata import StepMetadata
+
+_WORKSPACES: dict[int, torch.Tensor] = {}
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _check_pool(pool: torch.Tensor) -> tuple[int, int, int, int]:
+    _lib.require_gpu_tensor("pool", pool)
+    if pool.dim() != 5 or pool.shape[1] != 2:
+        raise ValueError(f"pool must be [num_blocks, 2, kv_heads, block_size, head_dim], got {tuple(pool.shape)}")
+    if not pool.is_contiguous():
+        raise ValueError("pool must be contiguous")
+    if pool.dtype not in _lib.DTYPE_CODE:
+        raise TypeError(f"unsupported pool dtype {pool.dtype}")
+    nb, _, hkv, bs, d = pool.shape
+    return nb, hkv, bs, d
+
+
+def _rows_view(name: str, t: torch.Tensor, n_heads: int, d: int) -> int:
+    """Validate a [T, n_heads, D] (or [T, n_heads*D]) tensor with contiguous rows; return its row stride."""
+    if t.dim() == 3:
+        if t.shape[1] != n_heads or t.shape[2] != d:
+            raise ValueError(f"{name} must be [T, {n_heads}, {d}], got {tuple(t.shape)}")
+        if t.stride(2) != 1 or t.stride(1) != d:
+            raise ValueError(f"{name} must have contiguous [heads, head_dim] rows")
+    elif t.dim() == 2:
+        if t.shape[1] != n_heads * d:
+            raise ValueError(f"{name} must be [T, {n_heads * d}], got {tuple(t.shape)}")
+        if t.stride(1) != 1:
+            raise ValueError(f"{name} must have contiguous rows")
+    else:
+        raise ValueError(f"{name} must be 2-D or 3-D, got {t.dim()}-D")
+    return t.stride(0) if t.shape[0] > 1 else n_heads * d
+
+
+def kv_append(pool: torch.Tensor, k: torch.Tensor, v: torch.Tensor, slot_mapping: torch.Tensor) -> None:
+    """K1: pool[slot] <- (k, v) for every token with slot >= 0 (reference kv_cache.py:25-38)."""
+    nb, hkv, bs, d = _check_pool(pool)
+    for name, t in (("k", k), ("v", v)):
+        _lib.require_gpu_tensor(name, t)
+        if t.dtype != pool.dtype:
+            raise TypeError(f"{name} dtype {t.dtype} != pool dtype {pool.dtype}")
+    ks = _rows_view("k", k, hkv, d)
+    vs = _rows_view("v", v, hkv, d)
+    T = k.shape[0]
+    if v.shape[0] != T or slot_mapping.numel() != T:
+        raise ValueError("k, v and slot_mapping disagree on the number of tokens")
+    if slot_mapping.dtype != torch.int32 or not slot_mapping.is_cuda or not slot_mapping.is_contiguous():
+        raise TypeError("slot_mapping must be a contiguous int32 GPU tensor")
+    st = _lib.lib().tb_kv_append(k.data_ptr(), ks, v.data_ptr(), vs, pool.data_ptr(), nb,
+                                 slot_mapping.data_ptr(), T, hkv, d, bs,
+                                 _lib.DTYPE_CODE[pool.dtype], _lib.stream_handle(pool.device))
+    _lib.check(st, "tb_kv_append")
+
+
+def kv_gather(pool: torch.Tensor, table: torch.Tensor, context_len: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Contiguous K, V [context_len, kv_heads, head_dim] of one sequence (reference kv_cache.py:40-45)."""
+    nb, hkv, bs, d = _check_pool(pool)
+    if table.dtype != torch.int32 or not table.is_cuda or not table.is_contiguous():
+        raise TypeError("table must be a contiguous int32 GPU tensor")
+    k_out = torch.empty(context_len, hkv, d, device=pool.device, dtype=pool.dtype)
+    v_out = torch.empty_like(k_out)
+    st = _lib.lib().tb_kv_gather(pool.data_ptr(), nb, table.data_ptr(), int(context_len), k_out.data_ptr(),
+                                 v_out.data_ptr(), hkv, d, bs, _lib.DTYPE_CODE[pool.dtype],
+                                 _lib.stream_handle(pool.device))
+    _lib.check(st, "tb_kv_gather")
+    return k_out, v_out
+
+
+def workspace_for(meta: StepMetadata, num_heads: int, head_dim: int, device: torch.device) -> torch.Tensor | None:
+    """Split-K partial buffer (grown on demand, cached per device)."""
+    if meta.max_parts_per_row <= 1:
+        return None
+    need = int(_lib.lib().tb_paged_attention_workspace_bytes(meta.total_partitions, num_heads, head_dim))
+    key = device.index if device.index is not None else torch.cuda.current_device()
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.empty(max(need, 1 << 20), dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
+
+
+def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, num_heads: int,
+                    scale: float | None = None, out: torch.Tensor | None = None,
+                    k_new: torch.Tensor | None = None, v_new: torch.Tensor | None = None,
+                    workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """K2: paged attention of every query row of the step (reference model.py:130-147).
+
+    q: [T, num_heads, head_dim]; returns out [T, num_heads * head_dim] in q's dtype
+    (rows outside every sequence slice are left untouched). With k_new/v_new
+    ([T, kv_heads, head_dim]) the kernel also appends each decode row's new
+    K/V (fused append); this requires a decode-only step.
+    """
+    nb, hkv, bs, d = _check_pool(pool)
+    _lib.require_gpu_tensor("q", q)
+    if q.dtype != pool.dtype:
+        raise TypeError(f"q dtype {q.dtype} != pool dtype {pool.dtype}")
+    if num_heads % hkv:
+        raise ValueError(f"num_heads {num_heads} is not a multiple of kv heads {hkv}")
+    if meta.block_size != bs:
+        raise ValueError(f"metadata block_size {meta.block_size} != pool block_size {bs}")
+    qs = _rows_view("q", q, num_heads, d)
+    T = q.shape[0]
+    if T != meta.num_tokens:
+        raise ValueError(f"q has {T} rows, metadata describes {meta.num_tokens}")
+    if out is None:
+        out = torch.empty(T, num_heads * d, device=q.device, dtype=q.dtype)
+    else:
+        _lib.require_gpu_tensor("out", out)
+        if out.dtype != q.dtype or out.shape[0] != T:
+            raise ValueError("out must match q's dtype and row count")
+    os_ = _rows_view("out", out, num_heads, d)
+    if meta.work is None:
+        raise ValueError("metadata has not been uploaded (call meta.to(device))")
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)   # scaled_dot_product_attention's default (model.py:140,146)
+    ksp = vsp = None
+    ks = vs = 0
+    if k_new is not None or v_new is not None:
+        if k_new is None or v_new is None:
+            raise ValueError("k_new and v_new go together")
+        if not meta.decode_only:
+            raise ValueError("fused append needs a decode-only step (one query row per sequence)")
+        for name, t in (("k_new", k_new), ("v_new", v_new)):
+            _lib.require_gpu_tensor(name, t)
+            if t.dtype != pool.dtype or t.shape[0] != T:
+                raise ValueError(f"{name} must be [T, kv_heads, head_dim] in the pool dtype")
+        ks = _rows_view("k_new", k_new, hkv, d)
+        vs = _rows_view("v_new", v_new, hkv, d)
+        ksp, vsp = k_new.data_ptr(), v_new.data_ptr()
+    if workspace is None:
+        workspace = workspace_for(meta, num_heads, d, q.device)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    st = _lib.lib().tb_paged_attention(
+        q.data_ptr(), qs, pool.data_ptr(), nb, out.data_ptr(), os_,
+        meta.block_tables.data_ptr(), meta.max_blocks_per_seq,
+        meta.work.data_ptr(), meta.num_work_items,
+        meta.row_part_off.data_ptr(), T,
+        max(meta.max_parts_per_row, 1), meta.partition_tokens, meta.total_partitions,
+        num_heads, hkv, d, bs, float(scale), _lib.DTYPE_CODE[q.dtype],
+        ksp, ks, vsp, vs, _ptr(workspace), ws_bytes, _lib.stream_handle(q.device))
+    _lib.check(st, "tb_paged_attention")
+    return out
+
+
+def _block_ids(name: str, ids, num_blocks: int, device) -> torch.Tensor:
+    arr = np.asarray(ids.cpu() if isinstance(ids, torch.Tensor) else ids, dtype=np.int64).reshape(-1)
+    if arr.size and (arr.min() < 0 or arr.max() >= num_blocks):
+        raise IndexError(f"{name} holds a block id outside [0, {num_blocks})")
+    return torch.from_numpy(arr.astype(np.int32)).to(device)
+
+
+def block_copy(pools: list[torch.Tensor], src, dst) -> None:
+    """K3: pool_l[dst[i]] <- pool_l[src[i]] for every layer pool l, one launch."""
+    if not pools:
+        return
+    nb = pools[0].shape[0]
+    block_bytes = pools[0][0].numel() * pools[0].element_size()
+    for p in pools:
+        _check_pool(p)
+        if p.shape != pools[0].shape or p.dtype != pools[0].dtype or p.device != pools[0].device:
+            raise ValueError("all layer pools must share shape, dtype and device")
+    s_np = np.asarray(src.cpu() if isinstance(src, torch.Tensor) else src, dtype=np.int64).reshape(-1)
+    d_np = np.asarray(dst.cpu() if isinstance(dst, torch.Tensor) else dst, dtype=np.int64).reshape(-1)
+    if s_np.size != d_np.size:
+        raise ValueError("src and dst differ in length")
+    if d_np.size != np.unique(d_np).size:
+        raise ValueError("dst block ids must be distinct")
+    if np.intersect1d(s_np, d_np).size:
+        raise ValueError("a dst block is also a src block; split the copy into rounds")
+    dev = pools[0].device
+    s_t = _block_ids("src", s_np, nb, dev)
+    d_t = _block_ids("dst", d_np, nb, dev)
+    ptrs = torch.tensor([p.data_ptr() for p in pools], dtype=torch.int64).to(dev)
+    st = _lib.lib().tb_block_copy(ptrs.data_ptr(), len(pools), nb, s_t.data_ptr(), d_t.data_ptr(), int(s_np.size),
+                                  block_bytes, _lib.stream_handle(dev))
+    _lib.check(st, "tb_block_copy")
+
+
+def block_gather(pool: torch.Tensor, blocks, staging: torch.Tensor) -> None:
+    """staging[i] <- pool[blocks[i]] (swap out); staging: [n, *pool.shape[1:]] device or pinned host."""
+    nb, _, _, _ = _check_pool(pool)
+    b_t = _block_ids("blocks", blocks, nb, pool.device)
+    n = b_t.numel()
+    if staging.dtype != pool.dtype or staging.numel() < n * pool[0].numel() or not staging.is_contiguous():
+        raise ValueError("staging must be a contiguous buffer of n blocks in the pool dtype")
+    st = _lib.lib().tb_block_gather(pool.data_ptr(), nb, b_t.data_ptr(), n, staging.data_ptr(),
+                                    pool[0].numel() * pool.element_size(), _lib.stream_handle(pool.device))
+    _lib.check(st, "tb_block_gather")
+
+
+def block_scatter(staging: torch.Tensor, pool: torch.Tensor, blocks) -> None:
+    """pool[blocks[i]] <- staging[i] (swap in)."""
+    nb, _, _, _ = _check_pool(pool)
+    b_t = _block_ids("blocks", blocks, nb, pool.device)
+    n = b_t.numel()
+    if staging.dtype != pool.dtype or staging.numel() < n * pool[0].numel() or not staging.is_contiguous():
+        raise ValueError("staging must be a contiguous buffer of n blocks in the pool dtype")
+    if b_t.numel() != torch.unique(b_t).numel():
+        raise ValueError("blocks must be distinct")
+    st = _lib.lib().tb_block_scatter(staging.data_ptr(), pool.data_ptr(), nb, b_t.data_ptr(), n,
+                                     pool[0].numel() * pool.element_size(), _lib.stream_handle(pool.device))
+    _lib.check(st, "tb_block_scatter")

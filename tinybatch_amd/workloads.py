@@ -1,0 +1,135 @@
+"""Seeded synthetic workloads of the paged data path (bench and tests).
+
+Shapes follow the layer geometries the data path is measured on:
+* ``qwen-fp32-b8``    Qwen2.5-0.5B layer (14 query / 2 KV heads, head_dim 64),
+  block 16, fp32, 8 sequences with U{16..256} cached tokens, 512-block pool.
+* ``qwen-fp16-b64``   same geometry in fp16, 64 sequences with U{512..4096}
+  cached tokens, 32768-block pool.
+* ``llama-bf16-b256`` Llama-3-8B layer (32 / 8 heads, head_dim 128), bf16, 256
+  sequences with log-normal cached lengths (median 8192, sigma 0.5) clipped to
+  [1024, 32768], pool sized to fit every sequence.
+Each decode step appends one token per sequence at position L (the cached
+length) and then attends over ctx = L + 1 positions, as LLMEngine.step does
+for running sequences (reference src/tinybatch/engine.py:114-120).
+
+Draw order from one CPU torch.Generator seeded per workload: cached lengths,
+block permutation, q, new k, new v, then the pool (N(0,1), drawn in fp32 and
+cast). A pool too large to draw on the CPU in reasonable time is drawn on the
+GPU from its own seeded generator instead (``pool_device``).
+Block tables are consecutive chunks of one random permutation of the pool.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+
+@dataclass
+class DecodeWorkload:
+    name: str
+    num_heads: int
+    num_kv_heads: int
+    head_dim: int
+    block_size: int
+    dtype: torch.dtype
+    num_blocks: int
+    cached_lens: list[int]
+    block_tables: list[list[int]]
+    q: torch.Tensor          # [B, Hq, D]
+    k_new: torch.Tensor      # [B, Hkv, D]
+    v_new: torch.Tensor      # [B, Hkv, D]
+    pool: torch.Tensor       # [NB, 2, Hkv, BS, D]
+    seed: int
+
+    @property
+    def batch(self) -> int:
+        return len(self.cached_lens)
+
+    @property
+    def context_lens(self) -> list[int]:
+        return [c + 1 for c in self.cached_lens]
+
+    @property
+    def positions(self) -> list[int]:
+        return list(self.cached_lens)
+
+    @property
+    def seq_slices(self) -> list[tuple[int, int]]:
+        return [(b, b + 1) for b in range(self.batch)]
+
+    def algorithmic_bytes(self) -> dict:
+        """Logical bytes of one append + decode-attention layer step (no cache credit).
+
+        append: read k,v + write the pool rows + 4 B slot per token;
+        attention: every visible K and V row once, q and out once, the block-table
+        entries used and the context lengths.
+        """
+        b = torch.tensor([], dtype=self.dtype).element_size()
+        B, Hq, Hkv, D, BS = self.batch, self.num_heads, self.num_kv_heads, self.head_dim, self.block_size
+        ctx = self.context_lens
+        append = B * 2 * Hkv * D * b * 2 + 4 * B
+        attn = (sum(ctx) * 2 * Hkv * D * b + 2 * B * Hq * D * b
+                + 4 * sum((c + BS - 1) // BS for c in ctx) + 4 * B)
+        return {"append": append, "attention": attn, "total": append + attn}
+
+    def flops(self) -> int:
+        return 4 * self.num_heads * self.head_dim * sum(self.context_lens)
+
+
+SPECS = {
+    "qwen-fp32-b8": dict(Hq=14, Hkv=2, D=64, BS=16, dtype=torch.float32, B=8, lens=("uniform", 16, 256),
+                         num_blocks=512, seed=1),
+    "qwen-fp16-b64": dict(Hq=14, Hkv=2, D=64, BS=16, dtype=torch.float16, B=64, lens=("uniform", 512, 4096),
+                          num_blocks=32768, seed=2),
+    "llama-bf16-b256": dict(Hq=32, Hkv=8, D=128, BS=16, dtype=torch.bfloat16, B=256,
+                            lens=("lognormal", 8192, 0.5, 1024, 32768), num_blocks=None, seed=3),
+}
+
+
+def _cached_lengths(gen: torch.Generator, B: int, spec) -> list[int]:
+    if spec[0] == "uniform":
+        lo, hi = spec[1], spec[2]
+        return torch.randint(lo, hi + 1, (B,), generator=gen).tolist()
+    median, sigma, lo, hi = spec[1:]
+    z = torch.randn(B, generator=gen, dtype=torch.float64)
+    vals = torch.exp(math.log(median) + sigma * z).round().clamp(lo, hi)
+    return [int(x) for x in vals.tolist()]
+
+
+def make_decode_workload(name: str, *, pool_device: str | torch.device = "cpu", seed: int | None = None,
+                         batch: int | None = None) -> DecodeWorkload:
+    spec = SPECS[name]
+    seed = spec["seed"] if seed is None else seed
+    gen = torch.Generator().manual_seed(seed)
+    B = spec["B"] if batch is None else batch
+    Hq, Hkv, D, BS, dt = spec["Hq"], spec["Hkv"], spec["D"], spec["BS"], spec["dtype"]
+    cached = _cached_lengths(gen, B, spec["lens"])
+    need = [(c + 1 + BS - 1) // BS for c in cached]      # blocks for ctx = L + 1
+    NB = spec["num_blocks"] or sum(need)
+    if sum(need) > NB:
+        raise ValueError(f"{name}: sequences need {sum(need)} blocks, pool has {NB}")
+    perm = torch.randperm(NB, generator=gen).tolist()
+    tables, at = [], 0
+    for n in need:
+        tables.append(perm[at:at + n])
+        at += n
+    q = torch.randn(B, Hq, D, generator=gen).to(dt)
+    k_new = torch.randn(B, Hkv, D, generator=gen).to(dt)
+    v_new = torch.randn(B, Hkv, D, generator=gen).to(dt)
+    shape = (NB, 2, Hkv, BS, D)
+    pool_device = torch.device(pool_device)
+    if pool_device.type == "cpu":
+        pool = torch.randn(*shape, generator=gen).to(dt)
+    else:
+        g2 = torch.Generator(device=pool_device).manual_seed(seed + 1000)
+        pool = torch.empty(shape, dtype=dt, device=pool_device)
+        flat = pool.view(-1)
+        step = 1 << 28
+        for s in range(0, flat.numel(), step):
+            n = min(step, flat.numel() - s)
+            flat[s:s + n] = torch.randn(n, generator=g2, device=pool_device, dtype=torch.float32).to(dt)
+    return DecodeWorkload(name=name, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, block_size=BS, dtype=dt,
+                          num_blocks=NB, cached_lens=cached, block_tables=tables, q=q, k_new=k_new,
+                          v_new=v_new, pool=pool, seed=seed)
