@@ -98,6 +98,8 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (profiling runs)")
     ap.add_argument("--partition", type=int, default=0)
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB five times (HBM counter calibration)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -119,20 +121,32 @@ def main() -> int:
     torch.cuda.set_device(dev)
     _lib.lib()
 
+    if args.calibrate_copy:
+        n = args.calibrate_copy << 20
+        a_buf = torch.ones(n // 4, dtype=torch.float32, device=dev)
+        b_buf = torch.empty_like(a_buf)
+        for _ in range(5):
+            b_buf.copy_(a_buf)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration": "device copy", "bytes_read_per_launch": n,
+                          "bytes_written_per_launch": n, "launches": 5}), flush=True)
+        return 0
+
     big = args.workload == "llama-bf16-b256"
     t0 = time.perf_counter()
     wl = make_decode_workload(args.workload, pool_device=(dev if big else "cpu"))
     _log(f"workload {wl.name}: B={wl.batch} NB={wl.num_blocks} mean ctx={sum(wl.context_lens)/wl.batch:.0f} "
          f"({time.perf_counter() - t0:.1f}s)")
     pool_bytes = wl.pool.numel() * wl.pool.element_size()
-    L = args.layers or max(2, min(24, int((2 << 30) // pool_bytes) or 2))
+    # 24 layer pools (a Qwen2.5-0.5B model's worth) unless one pool alone dwarfs the Infinity Cache
+    L = args.layers or (24 if pool_bytes * 24 <= (64 << 30) else 2)
     storage = torch.empty((L,) + tuple(wl.pool.shape), dtype=wl.dtype, device=dev)
     src = wl.pool if wl.pool.is_cuda else wl.pool.to(dev)
     for l in range(L):
         storage[l].copy_(src)
     del src
     pools = [storage[l] for l in range(L)]
-    P = args.partition or int(_lib.lib().tb_attention_partition_tokens())
+    P = args.partition or ops.partition_tokens(wl.dtype, wl.head_dim)
     meta = build_step_metadata(wl.positions, wl.seq_slices, wl.block_tables, wl.context_lens,
                                block_size=wl.block_size, num_blocks=wl.num_blocks, partition_tokens=P).to(dev)
     q = wl.q.to(dev)
@@ -163,10 +177,11 @@ def main() -> int:
         torch.cuda.synchronize()
 
     def run_once():
-        if graph is not None:
-            graph.replay()
-        else:
-            with torch.cuda.stream(stream):
+        # replays and eager launches both go to `stream`, the stream the events are recorded on
+        with torch.cuda.stream(stream):
+            if graph is not None:
+                graph.replay()
+            else:
                 step()
 
     for _ in range(args.warmup):

@@ -72,7 +72,7 @@ int32_t tb_kv_gather(const void* pool, int64_t num_blocks,
                      int32_t dtype, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
- * K2 — fused paged attention (decode rows and prefill rows on the VALU path).
+ * K2 — fused paged attention (any query rows: decode, prefill, cached-prefix tail).
  * Replaces the per-sequence loop of Qwen2Paged.forward
  * (src/tinybatch/model.py:130-147: gather, GQA repeat_interleave, offset-causal
  * mask, scaled_dot_product_attention, attn_out assembly).
@@ -87,21 +87,25 @@ int32_t tb_kv_gather(const void* pool, int64_t num_blocks,
  *   block_tables: [num_seqs][max_blocks_per_seq] int32 physical block ids
  *   work_items: [num_work_items][4] int32 = (row, seq, partition, row_ctx);
  *     partition p covers positions [p*P, min((p+1)*P, row_ctx)) with
- *     P = partition_tokens (a multiple of 64 and of block_size, at most
- *     64 blocks; tb_attention_partition_tokens() is the default). Every row
+ *     P = partition_tokens (a multiple of block_size spanning at most 64
+ *     blocks; fp16/bf16 require tb_attention_partition_tokens(dtype, D),
+ *     fp32 accepts any multiple of its 8-load chunk). Every row
  *     lists partitions 0 .. ceil(row_ctx/P)-1, row_part_offsets[num_rows+1]
  *     is their running count (row r owns partial slots
  *     row_part_offsets[r] ..), total_partitions = row_part_offsets[num_rows]
  *     and max_parts_per_row is the largest per-row count.
  *   workspace: >= tb_paged_attention_workspace_bytes(total_partitions, ...)
- *     bytes of device memory; only touched when a row has > 1 partition.
+ *     bytes of device memory (16-byte aligned) for the split-row partials;
+ *     only used when a row has > 1 partition (max_parts_per_row > 1), which
+ *     also launches a second (combine) kernel. Calls that may overlap in time
+ *     need their own workspace.
  * Fused decode append (k_new != NULL): each row's own newest position
  * row_ctx-1 is read from k_new/v_new ([num_rows][num_kv_heads][head_dim]) and
  * written to its slot in the pool by the same kernel, replacing a separate
  * tb_kv_append. Valid only when no row reads another row's newest slot, which
  * holds for a batch of decode rows (one new token per sequence).
  */
-int32_t tb_attention_partition_tokens(void);
+int32_t tb_attention_partition_tokens(int32_t dtype, int32_t head_dim);
 
 size_t tb_paged_attention_workspace_bytes(int32_t total_partitions, int32_t num_heads,
                                           int32_t head_dim);

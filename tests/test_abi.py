@@ -75,6 +75,8 @@ def test_attention_rejects_bad_arguments_without_launching():
     assert call(pt=100) == _lib.TB_ERR_INVALID_ARG             # partition not a whole number of chunks
     assert call(bs=2048, pt=256) == _lib.TB_ERR_INVALID_ARG    # partition shorter than a block
     assert call(mpr=3, ws=None) == _lib.TB_ERR_INVALID_ARG     # split rows need a workspace
+    assert call(mpr=3, ws=f, wsb=100) == _lib.TB_ERR_INVALID_ARG   # ... of the right size
+    assert call(pt=512) == _lib.TB_ERR_INVALID_ARG             # 16-bit kernel has a fixed partition
     assert call(kn=f, vn=None) == _lib.TB_ERR_INVALID_ARG      # fused append needs both k and v
     assert call(nw=0) == _lib.TB_OK                            # empty step: nothing to launch
 
@@ -83,6 +85,7 @@ def test_workspace_size_formula():
     L = _lib.lib()
     assert L.tb_paged_attention_workspace_bytes(10, 14, 64) == 10 * 14 * 66 * 4
     assert L.tb_paged_attention_workspace_bytes(0, 14, 64) == 0
+    assert L.tb_attention_partition_tokens(1, 64) == 256          # 16-bit kernel: fixed partition
 
 
 def test_copy_rejects_bad_arguments_without_launching():

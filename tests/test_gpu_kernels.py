@@ -242,3 +242,22 @@ def test_swap_out_swap_in_roundtrip_pinned_host():
     torch.cuda.synchronize()
     for layer in range(2):
         assert torch.equal(_bits(cache.storage[layer, :3].cpu()), _bits(host[layer, blocks]))
+
+
+def test_consecutive_calls_of_different_shapes_share_workspace():
+    """Split rows of one call must not be disturbed by an earlier call of another
+    shape that used the same partials buffer."""
+    cases = [(14, 2, 64, torch.bfloat16), (32, 8, 128, torch.float32), (14, 2, 64, torch.float16),
+             (32, 8, 128, torch.bfloat16), (8, 1, 128, torch.float16)]
+    for i, (Hq, Hkv, D, dt) in enumerate(cases * 2):
+        c = _mixed_case(20 + i, Hq, Hkv, D, 16, dt, qlens=[1, 3, 9, 1], cached=[700, 260, 300, 40])
+        _attention_vs_oracle(c, Hq, Hkv, dt)
+
+
+@pytest.mark.parametrize("BS", [4, 8, 32, 64])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_block_sizes_16bit(BS, dtype):
+    c = _mixed_case(9, 14, 2, 64, BS, dtype, qlens=[1, 3, 1], cached=[700, 90, 2])
+    _attention_vs_oracle(c, 14, 2, dtype)
+    c = _mixed_case(10, 16, 4, 128, BS, dtype, qlens=[1, 2], cached=[333, 1000])
+    _attention_vs_oracle(c, 16, 4, dtype)

@@ -29,7 +29,7 @@ SIGNATURES = {
     "tb_status_string": (ctypes.c_char_p, [c_i32]),
     "tb_kv_append": (c_i32, [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp]),
     "tb_kv_gather": (c_i32, [c_vp, c_i64, c_vp, c_i32, c_vp, c_vp, c_i32, c_i32, c_i32, c_i32, c_vp]),
-    "tb_attention_partition_tokens": (c_i32, []),
+    "tb_attention_partition_tokens": (c_i32, [c_i32, c_i32]),
     "tb_paged_attention_workspace_bytes": (c_sz, [c_i32, c_i32, c_i32]),
     "tb_paged_attention": (c_i32, [
         c_vp, c_i64,            # q, q_row_stride

@@ -1,4 +1,4 @@
-// K2 — fused paged attention on the VALU path (decode rows; any query row).
+// K2 — fused paged attention (decode rows and any other query row).
 //
 // Replaces the per-sequence loop of Qwen2Paged.forward
 // (reference src/tinybatch/model.py:130-147): gather of the sequence's blocks
@@ -6,78 +6,58 @@
 // offset-causal mask j <= ctx - q_len + i (model.py:139-145) and
 // scaled_dot_product_attention with scale 1/sqrt(D) (model.py:140,146).
 //
-// Mapping onto CDNA4 (wave64):
-// * One wave = one work item = (query row, kv head, head group, partition of
-//   P tokens). The wave reads each K/V token row once, through the block table
-//   in place, and serves all REP query heads of the GQA group from registers
-//   (no repeat_interleave, no gather copy).
-// * A K or V tile [BS][D] of one (block, kv head) is contiguous. The wave
-//   splits a token row into LPT lanes of 16 bytes (D=64 fp16: 8 lanes), so one
-//   wave load instruction moves 1 KiB of consecutive bytes (TPL = 64/LPT
-//   tokens).
-// * q.k: v_dot2_f32_{f16,bf16} over the lane's 8 elements, then a DPP
-//   butterfly over the LPT lanes of the token (fp32 accumulation).
-// * p.V: tokens are paired across two consecutive loads and packed with
-//   v_perm so that one v_dot2 applies (p_a, p_b) to (v_a[d], v_b[d]); the
-//   softmax denominator uses the same rounded p, so numerator and denominator
-//   agree.
-// * Online softmax over chunks in the base-2 domain (scores pre-scaled by
-//   scale*log2(e)), wave-wide max by DPP/ds_bpermute.
-// * Split-K: a row longer than P tokens is cut into partitions whose
-//   (max, sum, unnormalised acc) partials are merged by a log-sum-exp combine
-//   kernel. Rows of one partition write the output directly.
-// * Positions >= the row's context are never loaded (stale slots may hold
-//   anything, including NaN): their V registers are zero and their scores -inf.
+// Work decomposition: one wave64 = one work item = (query row, kv head, head
+// group, partition of P positions). The wave reads each visible K/V row of its
+// partition once, in place through the block table, and serves every query
+// head of its GQA group from that one read (no repeat_interleave, no gathered
+// copy). A row longer than P is split over several waves that write
+// (max, sum, unnormalised acc) partials; combine_partials_kernel merges them
+// with a log-sum-exp (kernel boundaries make the partials visible across XCDs).
+//
+// fp16 / bf16 (the hot path): paged_attn_mfma_kernel. The GQA group (up to 16
+// heads, padded) is one MFMA operand, so q.K^T and p.V are
+// v_mfma_f32_16x16x32_{f16,bf16} over 16-position tiles:
+//   S^T[pos][head] = K[pos][:] . Q[head][:]   A = K rows straight from the pool
+//                                              B = q (registers, loaded once)
+//   O[head][dv]   += P[head][pos] . V[pos][dv] A = p (the S^T tile registers,
+//                                              repacked in place), B = V read
+//                                              column-wise from an LDS copy
+// The online softmax runs per 64-position chunk on the S^T tiles (max / sum
+// across the four 16-lane groups by shuffles); loads of chunk c+1 are in
+// flight while chunk c is computed.
+// fp32: paged_attn_valu_kernel, fp32 FMAs on the VALU (no fp32 MFMA of the
+// needed precision on CDNA4), same decomposition.
+// Positions >= the row's context are never loaded (stale slots may hold any
+// bits, NaN included): their scores are -inf and their V rows zero.
 #include "tb_common.h"
 
 namespace tb {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf168_t __attribute__((ext_vector_type(8)));
 
 template <typename Tag>
 struct math;
 
 template <>
 struct math<f16_t> {
-  typedef half2_t pair_t;
-  static __device__ __forceinline__ pair_t as_pair(uint32_t w) { return __builtin_bit_cast(pair_t, w); }
-  static __device__ __forceinline__ float dot2(pair_t a, pair_t b, float c) {
-    return __builtin_amdgcn_fdot2(a, b, c, false);
-  }
-  static __device__ __forceinline__ pair_t pack(float a, float b) {
-    pair_t r = {(_Float16)a, (_Float16)b};
-    return r;
-  }
-  static __device__ __forceinline__ uint32_t pack_bits(float a, float b) {
-    return __builtin_bit_cast(uint32_t, pack(a, b));
+  typedef _Float16 scalar_t;
+  typedef half8_t vec8_t;
+  static __device__ __forceinline__ float4_t mfma(vec8_t a, vec8_t b, float4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
   }
 };
 
 template <>
 struct math<bf16_t> {
-  typedef bf162_t pair_t;
-  static __device__ __forceinline__ pair_t as_pair(uint32_t w) { return __builtin_bit_cast(pair_t, w); }
-  static __device__ __forceinline__ float dot2(pair_t a, pair_t b, float c) {
-    return __builtin_amdgcn_fdot2_f32_bf16(a, b, c, false);
-  }
-  static __device__ __forceinline__ pair_t pack(float a, float b) {
-    pair_t r = {(__bf16)a, (__bf16)b};
-    return r;
-  }
-  static __device__ __forceinline__ uint32_t pack_bits(float a, float b) {
-    return __builtin_bit_cast(uint32_t, pack(a, b));
+  typedef __bf16 scalar_t;
+  typedef bf168_t vec8_t;
+  static __device__ __forceinline__ float4_t mfma(vec8_t a, vec8_t b, float4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
   }
 };
 
-// Shape constants of the VALU kernel for element type Tag and head_dim D.
-template <typename Tag, int D>
-struct valu_shape {
-  static constexpr int EB = elem<Tag>::bytes;
-  static constexpr int EPL = 16 / EB;     // elements per lane per load
-  static constexpr int LPT = D / EPL;     // lanes per token row
-  static constexpr int TPL = 64 / LPT;    // tokens per wave load
-  static constexpr int CH_LOADS = 8;      // wave loads of K (and of V) per chunk
-  static constexpr int CH = CH_LOADS * TPL;  // tokens per chunk
-  static_assert(LPT >= 1 && LPT <= 64 && (64 % LPT) == 0, "lane split");
-};
+constexpr int PART16 = 256;   // partition length of the 16-bit kernel (positions)
 
 struct attn_args {
   const char* q;          // [rows][Hq][D]
@@ -95,6 +75,7 @@ struct attn_args {
   int32_t num_heads;
   int32_t num_kv_heads;
   int32_t rep;            // num_heads / num_kv_heads
+  int32_t group;          // heads per wave (grid z = rep / group)
   int32_t log2_bs;
   int32_t part_tokens;
   float scale_log2e;
@@ -104,12 +85,64 @@ struct attn_args {
   int64_t v_new_row_bytes;
 };
 
+// ---------------------------------------------------------------------------
+// fp32 path: single pass, online softmax per chunk, fp32 FMAs.
+template <typename Tag, int D>
+struct valu_shape {
+  static constexpr int EB = elem<Tag>::bytes;
+  static constexpr int EPL = 16 / EB;     // elements per lane per load
+  static constexpr int LPT = D / EPL;     // lanes per token row
+  static constexpr int TPL = 64 / LPT;    // tokens per wave load
+  static constexpr int CH_LOADS = 8;      // wave loads of K (and of V) per chunk
+  static constexpr int CH = CH_LOADS * TPL;  // tokens per chunk
+  static_assert(LPT >= 1 && LPT <= 64 && (64 % LPT) == 0, "lane split");
+};
+
+// End of a VALU work item. acc[h][e] holds, in lanes 0..LPT-1 (column j = lane),
+// the unnormalised output of head h over the partition for dims j*EPL..;
+// m[h] / l[h] (wave-uniform) are its max (base-2 domain) and sum. One
+// partition: write the output. Several: write the partial for the combine.
+template <typename Tag, int D, int REP, int EPL, int LPT>
+__device__ __forceinline__ void finish_valu(const attn_args& a, int row, int part, int head0, int lane,
+                                            float (&acc)[REP][EPL], const float (&m)[REP],
+                                            const float (&l)[REP]) {
+  const int j = lane % LPT;
+  if (lane >= LPT) return;
+  const int pbeg = a.row_part_off[row];
+  const int nparts = a.row_part_off[row + 1] - pbeg;
+  if (nparts == 1) {
+    char* orow = a.out + row * a.out_row_bytes + j * 16;
+#pragma unroll
+    for (int h = 0; h < REP; ++h) {
+      const float inv = 1.f / l[h];
+      vec16 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o.w[e] = __float_as_uint(acc[h][e] * inv);
+      st16(orow + (int64_t)(head0 + h) * D * 4, o);
+    }
+    return;
+  }
+  const int64_t pidx = pbeg + part;
+#pragma unroll
+  for (int h = 0; h < REP; ++h) {
+    float* dst = a.ws_acc + (pidx * a.num_heads + head0 + h) * D + j * EPL;
+#pragma unroll
+    for (int e = 0; e < EPL; e += 4)
+      *reinterpret_cast<float4*>(dst + e) = make_float4(acc[h][e], acc[h][e + 1], acc[h][e + 2], acc[h][e + 3]);
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int h = 0; h < REP; ++h)
+      *reinterpret_cast<float2*>(a.ws_ml + (pidx * a.num_heads + head0 + h) * 2) = make_float2(m[h], l[h]);
+  }
+}
+
 template <typename Tag, int D, int REP>
 __global__ __launch_bounds__(64) void paged_attn_valu_kernel(const attn_args a) {
   using S = valu_shape<Tag, D>;
   constexpr int EB = S::EB, EPL = S::EPL, LPT = S::LPT, TPL = S::TPL;
   constexpr int CH_LOADS = S::CH_LOADS, CH = S::CH;
-  constexpr bool F32 = (EB == 4);
+  static_assert(EB == 4, "the 16-bit types use paged_attn_mfma_kernel");
 
   const int lane = threadIdx.x;
   const int j = lane % LPT;  // 16-byte column of the token row
@@ -133,7 +166,7 @@ __global__ __launch_bounds__(64) void paged_attn_valu_kernel(const attn_args a) 
     if (my_blk < 0 || my_blk >= a.num_blocks) my_blk = 0;  // host validates; stay inside the pool
   }
 
-  const int64_t tile_bytes = (int64_t)bs * D * EB;              // one [BS][D] tile
+  const int64_t tile_bytes = (int64_t)bs * D * EB;
   const int64_t blk_bytes = 2 * (int64_t)a.num_kv_heads * tile_bytes;
   const int64_t v_off = (int64_t)a.num_kv_heads * tile_bytes;
   const char* pool_kvh = a.pool + kvh * tile_bytes + j * 16;
@@ -142,7 +175,6 @@ __global__ __launch_bounds__(64) void paged_attn_valu_kernel(const attn_args a) 
   const char* k_new_row = fused ? a.k_new + row * a.k_new_row_bytes + (int64_t)kvh * D * EB + j * 16 : nullptr;
   const char* v_new_row = fused ? a.v_new + row * a.v_new_row_bytes + (int64_t)kvh * D * EB + j * 16 : nullptr;
 
-  // Query registers: REP heads x this lane's EPL elements.
   vec16 qv[REP];
   {
     const char* qrow = a.q + row * a.q_row_bytes + j * 16;
@@ -159,54 +191,35 @@ __global__ __launch_bounds__(64) void paged_attn_valu_kernel(const attn_args a) 
     for (int e = 0; e < EPL; ++e) acc[h][e] = 0.f;
   }
 
-  // Pool offset of the row's newest position (fused append only). Every lane
-  // runs the shuffle; the partition may not contain new_pos, then it is unused.
   int64_t new_off = 0;
   if (fused) {
     const int nb = __shfl(my_blk, ((new_pos - p0) >> a.log2_bs) & 63);
     new_off = (int64_t)nb * blk_bytes + (int64_t)(new_pos & (bs - 1)) * (D * EB);
   }
 
-  vec16 kbuf[CH_LOADS], vbuf[CH_LOADS];
-
-  auto issue = [&](int c0, vec16* kd, vec16* vd) {
+  for (int c0 = p0; c0 < p1; c0 += CH) {
+    vec16 kbuf[CH_LOADS], vbuf[CH_LOADS];
 #pragma unroll
     for (int i = 0; i < CH_LOADS; ++i) {
       const int tau = c0 + i * TPL + g;
-      const int bidx = (tau - p0) >> a.log2_bs;
-      const int blk = __shfl(my_blk, bidx & 63);
+      const int blk = __shfl(my_blk, ((tau - p0) >> a.log2_bs) & 63);
       const int64_t off = (int64_t)blk * blk_bytes + (int64_t)(tau & (bs - 1)) * (D * EB);
       const char* kp = pool_kvh + off;
       const char* vp = kp + v_off;
-      if (fused && tau == new_pos) {
-        kp = k_new_row;
-        vp = v_new_row;
-      }
-      if (tau < p1) {
-        kd[i] = ld16(kp);
-        vd[i] = ld16(vp);
-      } else {
-        kd[i] = zero16();
-        vd[i] = zero16();
-      }
+      if (fused && tau == new_pos) { kp = k_new_row; vp = v_new_row; }
+      if (tau < p1) { kbuf[i] = ld16(kp); vbuf[i] = ld16(vp); }
+      else { kbuf[i] = zero16(); vbuf[i] = zero16(); }
     }
-  };
-
-  for (int c0 = p0; c0 < p1; c0 += CH) {
-    issue(c0, kbuf, vbuf);
     if (fused) {
 #pragma unroll
       for (int i = 0; i < CH_LOADS; ++i) {
-        const int tau = c0 + i * TPL + g;
-        if (tau == new_pos) {
+        if (c0 + i * TPL + g == new_pos) {
           char* kp = const_cast<char*>(pool_kvh) + new_off;
           st16(kp, kbuf[i]);
           st16(kp + v_off, vbuf[i]);
         }
       }
     }
-
-    // ---- scores (base-2 domain) ----
     float s[CH_LOADS][REP];
 #pragma unroll
     for (int i = 0; i < CH_LOADS; ++i) {
@@ -214,20 +227,12 @@ __global__ __launch_bounds__(64) void paged_attn_valu_kernel(const attn_args a) 
 #pragma unroll
       for (int h = 0; h < REP; ++h) {
         float d = 0.f;
-        if constexpr (F32) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) d = fmaf(bits_to_f32(qv[h].w[e]), bits_to_f32(kbuf[i].w[e]), d);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            d = math<Tag>::dot2(math<Tag>::as_pair(qv[h].w[e]), math<Tag>::as_pair(kbuf[i].w[e]), d);
-        }
+        for (int e = 0; e < 4; ++e) d = fmaf(bits_to_f32(qv[h].w[e]), bits_to_f32(kbuf[i].w[e]), d);
         d = group_sum<LPT>(d);
         s[i][h] = valid ? d * a.scale_log2e : -INFINITY;
       }
     }
-
-    // ---- online-softmax rescale ----
 #pragma unroll
     for (int h = 0; h < REP; ++h) {
       float cm = s[0][h];
@@ -241,162 +246,347 @@ __global__ __launch_bounds__(64) void paged_attn_valu_kernel(const attn_args a) 
 #pragma unroll
       for (int e = 0; e < EPL; ++e) acc[h][e] *= alpha;
     }
-
-    // ---- p.V over token pairs (i, i+1) ----
 #pragma unroll
-    for (int i = 0; i < CH_LOADS; i += 2) {
-      if constexpr (F32) {
+    for (int i = 0; i < CH_LOADS; ++i) {
 #pragma unroll
-        for (int h = 0; h < REP; ++h) {
-          const float pa = fast_exp2(s[i][h] - m_run[h]);
-          const float pb = fast_exp2(s[i + 1][h] - m_run[h]);
-          l_run[h] += pa + pb;
+      for (int h = 0; h < REP; ++h) {
+        const float p = fast_exp2(s[i][h] - m_run[h]);
+        l_run[h] += p;
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            acc[h][e] = fmaf(pb, bits_to_f32(vbuf[i + 1].w[e]), fmaf(pa, bits_to_f32(vbuf[i].w[e]), acc[h][e]));
-        }
-      } else {
-        typedef typename math<Tag>::pair_t pair_t;
-        pair_t lo[4], hi[4];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          lo[c] = math<Tag>::as_pair(__builtin_amdgcn_perm(vbuf[i + 1].w[c], vbuf[i].w[c], 0x05040100u));
-          hi[c] = math<Tag>::as_pair(__builtin_amdgcn_perm(vbuf[i + 1].w[c], vbuf[i].w[c], 0x07060302u));
-        }
-        const pair_t ones = math<Tag>::pack(1.f, 1.f);
-#pragma unroll
-        for (int h = 0; h < REP; ++h) {
-          const pair_t p2 = math<Tag>::pack(fast_exp2(s[i][h] - m_run[h]), fast_exp2(s[i + 1][h] - m_run[h]));
-          l_run[h] = math<Tag>::dot2(p2, ones, l_run[h]);
-#pragma unroll
-          for (int c = 0; c < 4; ++c) {
-            acc[h][2 * c] = math<Tag>::dot2(p2, lo[c], acc[h][2 * c]);
-            acc[h][2 * c + 1] = math<Tag>::dot2(p2, hi[c], acc[h][2 * c + 1]);
-          }
-        }
+        for (int e = 0; e < 4; ++e) acc[h][e] = fmaf(p, bits_to_f32(vbuf[i].w[e]), acc[h][e]);
       }
     }
   }
 
-  // ---- reduce over the token slots g of the wave ----
+  // l was accumulated per token slot; sum over the slots like acc
 #pragma unroll
   for (int h = 0; h < REP; ++h) {
     l_run[h] = cross_group_sum<LPT>(l_run[h]);
 #pragma unroll
     for (int e = 0; e < EPL; ++e) acc[h][e] = cross_group_sum<LPT>(acc[h][e]);
   }
-
-  const int pbeg = a.row_part_off[row];
-  const int nparts = a.row_part_off[row + 1] - pbeg;
-  if (nparts == 1) {
-    if (g == 0) {
-      char* orow = a.out + row * a.out_row_bytes + j * 16;
-#pragma unroll
-      for (int h = 0; h < REP; ++h) {
-        const float inv = 1.f / l_run[h];
-        vec16 o;
-        if constexpr (F32) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) o.w[e] = __float_as_uint(acc[h][e] * inv);
-        } else {
-#pragma unroll
-          for (int c = 0; c < 4; ++c) o.w[c] = math<Tag>::pack_bits(acc[h][2 * c] * inv, acc[h][2 * c + 1] * inv);
-        }
-        st16(orow + (int64_t)(head0 + h) * D * EB, o);
-      }
-    }
-  } else {
-    const int64_t pidx = pbeg + part;
-    if (g == 0) {
-#pragma unroll
-      for (int h = 0; h < REP; ++h) {
-        float* dst = a.ws_acc + (pidx * a.num_heads + head0 + h) * D + j * EPL;
-#pragma unroll
-        for (int e = 0; e < EPL; e += 4) {
-          float4 v4 = make_float4(acc[h][e], acc[h][e + 1], acc[h][e + 2], acc[h][e + 3]);
-          *reinterpret_cast<float4*>(dst + e) = v4;
-        }
-      }
-    }
-    if (lane < REP) {
-      // lane h publishes head h's running max and sum (uniform across the wave)
-      float mh = m_run[0], lh = l_run[0];
-#pragma unroll
-      for (int h = 1; h < REP; ++h) {
-        if (lane == h) { mh = m_run[h]; lh = l_run[h]; }
-      }
-      float* ml = a.ws_ml + (pidx * a.num_heads + head0 + lane) * 2;
-      ml[0] = mh;
-      ml[1] = lh;
-    }
-  }
+  finish_valu<Tag, D, REP, EPL, LPT>(a, row, part, head0, lane, acc, m_run, l_run);
 }
 
-// Log-sum-exp merge of the partition partials of one (row, head).
-// Grid: (rows, heads); block: D threads, thread d owns output column d.
+// ---------------------------------------------------------------------------
+// 16-bit kernel (see the file header). Lane l = 16*lg + lc.
+// MFMA 16x16x32 operand layouts (gfx950): A lane l holds A[l%16][8*(l/16)+j],
+// B lane l holds B[8*(l/16)+j][l%16], C/D lane l holds D[4*(l/16)+j][l%16].
+template <int D>
+struct mfma_shape {
+  static constexpr int RB = D * 2;           // bytes per K or V row
+  static constexpr int KS = D / 32;          // q.k k-slices (32 dims each)
+  static constexpr int NSL = D / 16;         // p.V output slices (16 dims each)
+  static constexpr int P = PART16;
+  static constexpr int CT = 8192 / RB;       // positions per chunk (8 KB of K, 8 KB of V)
+  static constexpr int TILES = CT / 16;      // 16-position tiles per chunk
+  static constexpr int NCH = P / CT;         // chunks per partition
+  static constexpr int VCOLS = RB / 16;      // 16-byte columns of a row
+  static constexpr int VT = 64 / VCOLS;      // rows per V load instruction
+  static constexpr int VLD = CT / VT;        // V loads per lane per chunk
+  static constexpr int RS = RB + 8;          // LDS row stride: column reads hit 32 distinct banks
+  static_assert(TILES % 2 == 0 && P % CT == 0, "chunk shape");
+};
+
 template <typename Tag, int D>
-__global__ __launch_bounds__(128) void combine_partials_kernel(const attn_args a) {
+__global__ __launch_bounds__(64) void paged_attn_mfma_kernel(const attn_args a) {
+  using S = mfma_shape<D>;
+  using M = math<Tag>;
+  typedef typename M::vec8_t vec8_t;
+  typedef typename M::scalar_t scalar_t;
+  constexpr int RB = S::RB, KS = S::KS, NSL = S::NSL, P = S::P, CT = S::CT, TILES = S::TILES;
+  constexpr int NCH = S::NCH, VCOLS = S::VCOLS, VT = S::VT, VLD = S::VLD, RS = S::RS;
+
+  __shared__ __align__(16) char v_lds[CT * RS];
+
+  const int lane = threadIdx.x;
+  const int lc = lane & 15, lg = lane >> 4;
+  const int4 wi = a.work[blockIdx.x];
+  const int row = wi.x, seq = wi.y, part = wi.z, ctx = wi.w;
+  const int kvh = blockIdx.y;
+  const int R = a.group;                    // heads of this wave (<= 16)
+  const int head0 = kvh * a.rep + blockIdx.z * R;
+  const int p0 = part * P;
+  const int n = min(P, ctx - p0);          // visible positions of this partition (>= 1)
+  const int nch = (n + CT - 1) / CT;
+  const int bs = 1 << a.log2_bs;
+
+  // Block-table entries of this partition: lane l holds entry p0/BS + l.
+  const int blk_count = ((n - 1) >> a.log2_bs) + 1;   // <= 64: BS >= 4
+  int my_blk = 0;
+  if (lane < blk_count) {
+    my_blk = a.block_tables[(int64_t)seq * a.max_nb + (p0 >> a.log2_bs) + lane];
+    if (my_blk < 0 || my_blk >= a.num_blocks) my_blk = 0;  // host validates; stay inside the pool
+  }
+  const int64_t tile_bytes = (int64_t)bs * RB;
+  const int64_t blk_bytes = 2 * (int64_t)a.num_kv_heads * tile_bytes;
+  const int64_t v_off = (int64_t)a.num_kv_heads * tile_bytes;
+  char* const pool_kvh = a.pool + kvh * tile_bytes;
+  const bool fused = (a.k_new != nullptr);
+  const int new_tau = ctx - 1 - p0;         // partition-relative index of the newest position
+  const char* k_new_row = fused ? a.k_new + row * a.k_new_row_bytes + (int64_t)kvh * RB : nullptr;
+  const char* v_new_row = fused ? a.v_new + row * a.v_new_row_bytes + (int64_t)kvh * RB : nullptr;
+  // Pool offset of position p0+tau (this kv head). Shuffles: every lane runs it.
+  auto pos_off = [&](int tau) -> int64_t {
+    const int blk = __shfl(my_blk, (tau >> a.log2_bs) & 63);
+    return (int64_t)blk * blk_bytes + (int64_t)(tau & (bs - 1)) * RB;
+  };
+
+  // q as the B operand of S^T = K.Q^T: lane holds q[head0+lc][32s + 8lg .. +8].
+  vec16 qb[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) qb[s] = zero16();
+  if (lc < R) {
+    const char* qrow = a.q + row * a.q_row_bytes + (int64_t)(head0 + lc) * RB + 16 * lg;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qb[s] = ld16(qrow + 64 * s);
+  }
+
+  // K tiles (A operand: lane holds position 16t+lc, bytes 64s+16lg) and V rows
+  // (16-byte column lane%VCOLS of row VT*i + lane/VCOLS) of chunk c.
+  vec16 kd[2][TILES][KS], vd[2][VLD];
+  auto load_chunk = [&](int c, vec16 (&kk)[TILES][KS], vec16 (&vv)[VLD]) {
+#pragma unroll
+    for (int t = 0; t < TILES; ++t) {
+      const int tau = c * CT + 16 * t + lc;
+      const int64_t off = pos_off(tau);
+      const char* src = pool_kvh + off + 16 * lg;
+      if (fused && tau == new_tau) src = k_new_row + 16 * lg;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) kk[t][s] = (tau < n) ? ld16(src + 64 * s) : zero16();
+    }
+#pragma unroll
+    for (int i = 0; i < VLD; ++i) {
+      const int tau = c * CT + VT * i + lane / VCOLS;
+      const int col = lane % VCOLS;
+      const int64_t off = pos_off(tau);
+      const char* src = pool_kvh + v_off + off + 16 * col;
+      if (fused && tau == new_tau) src = v_new_row + 16 * col;
+      vv[i] = (tau < n) ? ld16(src) : zero16();
+    }
+  };
+
+  float m_run = -INFINITY;   // running max of head lc (base-2 domain), same in all 4 lane groups
+  float l_part = 0.f;        // this lane's share of head lc's running sum
+  float4_t acc[NSL];         // O[head 4lg+j][16n + lc]
+#pragma unroll
+  for (int nn = 0; nn < NSL; ++nn) acc[nn] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  load_chunk(0, kd[0], vd[0]);
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    if (c >= nch) break;
+    if (c + 1 < nch) load_chunk(c + 1, kd[(c + 1) & 1], vd[(c + 1) & 1]);
+    vec16(&ck)[TILES][KS] = kd[c & 1];
+    vec16(&cv)[VLD] = vd[c & 1];
+
+    if (fused) {   // the newest position's K/V rows go to their pool slot
+#pragma unroll
+      for (int t = 0; t < TILES; ++t) {
+        const int tau = c * CT + 16 * t + lc;
+        const int64_t off = pos_off(tau);
+        if (tau == new_tau) {
+#pragma unroll
+          for (int s = 0; s < KS; ++s) st16(pool_kvh + off + 16 * lg + 64 * s, ck[t][s]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < VLD; ++i) {
+        const int tau = c * CT + VT * i + lane / VCOLS;
+        const int64_t off = pos_off(tau);
+        if (tau == new_tau) st16(pool_kvh + v_off + off + 16 * (lane % VCOLS), cv[i]);
+      }
+    }
+
+    // V rows into LDS (8-byte stores: the padded row stride is only 8-byte aligned)
+#pragma unroll
+    for (int i = 0; i < VLD; ++i) {
+      char* dst = v_lds + (VT * i + lane / VCOLS) * RS + 16 * (lane % VCOLS);
+      *reinterpret_cast<uint2*>(dst) = make_uint2(cv[i].w[0], cv[i].w[1]);
+      *reinterpret_cast<uint2*>(dst + 8) = make_uint2(cv[i].w[2], cv[i].w[3]);
+    }
+
+    // S^T tiles: lane holds positions 16t + 4lg + j of head lc
+    float4_t sc[TILES];
+#pragma unroll
+    for (int t = 0; t < TILES; ++t) {
+      sc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+        sc[t] = M::mfma(__builtin_bit_cast(vec8_t, ck[t][s]), __builtin_bit_cast(vec8_t, qb[s]), sc[t]);
+    }
+    float cm = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < TILES; ++t)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int tau = c * CT + 16 * t + 4 * lg + j;
+        const float v = tau < n ? sc[t][j] * a.scale_log2e : -INFINITY;
+        sc[t][j] = v;
+        cm = fmaxf(cm, v);
+      }
+    cm = fmaxf(cm, __shfl_xor(cm, 16));
+    cm = fmaxf(cm, __shfl_xor(cm, 32));
+    const float m_new = fmaxf(m_run, cm);          // finite: the chunk has a visible position
+    const float alpha = fast_exp2(m_run - m_new);
+    m_run = m_new;
+    float psum = 0.f;
+#pragma unroll
+    for (int t = 0; t < TILES; ++t)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        sc[t][j] = fast_exp2(sc[t][j] - m_new);
+        psum += sc[t][j];
+      }
+    l_part = fmaf(l_part, alpha, psum);
+    // acc rows are heads 4lg+j: their factors live in lanes 4lg+j
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float aj = __shfl(alpha, 4 * lg + j);
+#pragma unroll
+      for (int nn = 0; nn < NSL; ++nn) acc[nn][j] *= aj;
+    }
+    __syncthreads();   // V rows visible in LDS
+
+    // O += P.V over 32-position blocks: k index 8lg+j <-> position 32u + 4lg + j (j<4)
+    // or 32u + 16 + 4lg + (j-4): exactly the S^T values this lane holds.
+#pragma unroll
+    for (int u = 0; u < TILES / 2; ++u) {
+      vec8_t pa;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        pa[j] = (scalar_t)sc[2 * u][j];
+        pa[4 + j] = (scalar_t)sc[2 * u + 1][j];
+      }
+      const char* vbase = v_lds + (32 * u + 4 * lg) * RS + 2 * lc;
+#pragma unroll
+      for (int nn = 0; nn < NSL; ++nn) {
+        vec8_t vb;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          vb[j] = *reinterpret_cast<const scalar_t*>(vbase + j * RS + 32 * nn);
+          vb[4 + j] = *reinterpret_cast<const scalar_t*>(vbase + (16 + j) * RS + 32 * nn);
+        }
+        acc[nn] = M::mfma(pa, vb, acc[nn]);
+      }
+    }
+    __syncthreads();   // LDS is rewritten by the next chunk
+  }
+
+  // Sum over the four lane groups, then hand each acc row its head's (m, l).
+  float l_tot = l_part + __shfl_xor(l_part, 16);
+  l_tot += __shfl_xor(l_tot, 32);
+  const int pbeg = a.row_part_off[row];
+  const int nparts = a.row_part_off[row + 1] - pbeg;
+  float lj[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) lj[j] = __shfl(l_tot, 4 * lg + j);
+  if (nparts == 1) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int h = 4 * lg + j;
+      if (h >= R) continue;
+      const float inv = 1.f / lj[j];
+      scalar_t* orow = reinterpret_cast<scalar_t*>(a.out + row * a.out_row_bytes) + (int64_t)(head0 + h) * D + lc;
+#pragma unroll
+      for (int nn = 0; nn < NSL; ++nn) orow[16 * nn] = (scalar_t)(acc[nn][j] * inv);
+    }
+    return;
+  }
+  const int64_t pidx = pbeg + part;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int h = 4 * lg + j;
+    if (h >= R) continue;
+    float* dst = a.ws_acc + (pidx * a.num_heads + head0 + h) * D + lc;
+#pragma unroll
+    for (int nn = 0; nn < NSL; ++nn) dst[16 * nn] = acc[nn][j];
+  }
+  if (lg == 0 && lc < R)
+    *reinterpret_cast<float2*>(a.ws_ml + (pidx * a.num_heads + head0 + lc) * 2) = make_float2(m_run, l_tot);
+}
+
+// ---------------------------------------------------------------------------
+// Log-sum-exp merge of the partials of one (row, head): one wave, lane owns
+// output columns lane, lane + 64, ... Rows of a single partition exit.
+template <typename Tag, int D>
+__global__ __launch_bounds__(64) void combine_partials_kernel(const attn_args a) {
   constexpr int EB = elem<Tag>::bytes;
-  const int row = blockIdx.x, head = blockIdx.y, d = threadIdx.x;
+  __shared__ float w_lds[64];
+  const int row = blockIdx.x, head = blockIdx.y, lane = threadIdx.x;
   const int pbeg = a.row_part_off[row];
   const int n = a.row_part_off[row + 1] - pbeg;
   if (n <= 1) return;
   float M = -INFINITY;
-  for (int p = 0; p < n; ++p) M = fmaxf(M, a.ws_ml[((int64_t)(pbeg + p) * a.num_heads + head) * 2]);
-  float L = 0.f, o = 0.f;
-  for (int p = 0; p < n; ++p) {
-    const int64_t idx = (int64_t)(pbeg + p) * a.num_heads + head;
-    const float w = fast_exp2(a.ws_ml[idx * 2] - M);
-    L = fmaf(a.ws_ml[idx * 2 + 1], w, L);
-    o = fmaf(a.ws_acc[idx * D + d], w, o);
+  for (int p = lane; p < n; p += 64) M = fmaxf(M, a.ws_ml[((int64_t)(pbeg + p) * a.num_heads + head) * 2]);
+  M = cross_group_max<1>(M);
+  float L = 0.f;
+  for (int p = lane; p < n; p += 64) {
+    const float2 ml = *reinterpret_cast<const float2*>(a.ws_ml + ((int64_t)(pbeg + p) * a.num_heads + head) * 2);
+    L = fmaf(ml.y, fast_exp2(ml.x - M), L);
   }
-  o = o / L;
-  char* dst = a.out + row * a.out_row_bytes + ((int64_t)head * D + d) * EB;
-  if constexpr (EB == 4) *reinterpret_cast<float*>(dst) = o;
-  else *reinterpret_cast<typename elem<Tag>::type*>(dst) = (typename elem<Tag>::type)o;
+  L = cross_group_sum<1>(L);
+  const float invL = 1.f / L;
+  float o[D / 64];
+#pragma unroll
+  for (int k = 0; k < D / 64; ++k) o[k] = 0.f;
+  for (int p0 = 0; p0 < n; p0 += 64) {
+    const int cnt = min(64, n - p0);
+    __syncthreads();
+    if (lane < cnt) w_lds[lane] = fast_exp2(a.ws_ml[((int64_t)(pbeg + p0 + lane) * a.num_heads + head) * 2] - M);
+    __syncthreads();
+#pragma unroll 8
+    for (int p = 0; p < cnt; ++p) {
+      const float w = w_lds[p];
+      const float* src = a.ws_acc + ((int64_t)(pbeg + p0 + p) * a.num_heads + head) * D + lane;
+#pragma unroll
+      for (int k = 0; k < D / 64; ++k) o[k] = fmaf(src[64 * k], w, o[k]);
+    }
+  }
+  char* orow = a.out + row * a.out_row_bytes + (int64_t)head * D * EB;
+#pragma unroll
+  for (int k = 0; k < D / 64; ++k) {
+    const float v = o[k] * invL;
+    if constexpr (EB == 4) reinterpret_cast<float*>(orow)[lane + 64 * k] = v;
+    else reinterpret_cast<typename elem<Tag>::type*>(orow)[lane + 64 * k] = (typename elem<Tag>::type)v;
+  }
 }
 
 // ---- dispatch ---------------------------------------------------------------
 template <typename Tag, int D, int REP>
-static void launch_valu(const attn_args& a, int num_work, int head_groups, hipStream_t stream) {
-  hipLaunchKernelGGL((paged_attn_valu_kernel<Tag, D, REP>), dim3(num_work, a.num_kv_heads, head_groups),
+static void launch_valu(const attn_args& a, int num_work, hipStream_t stream) {
+  hipLaunchKernelGGL((paged_attn_valu_kernel<Tag, D, REP>), dim3(num_work, a.num_kv_heads, a.rep / a.group),
                      dim3(64), 0, stream, a);
 }
 
-template <typename Tag, int D>
-static int dispatch_rep(const attn_args& a, int rep_tile, int num_work, int head_groups, hipStream_t s) {
-  switch (rep_tile) {
-    case 1: launch_valu<Tag, D, 1>(a, num_work, head_groups, s); return TB_OK;
-    case 2: launch_valu<Tag, D, 2>(a, num_work, head_groups, s); return TB_OK;
-    case 3: launch_valu<Tag, D, 3>(a, num_work, head_groups, s); return TB_OK;
-    case 4: launch_valu<Tag, D, 4>(a, num_work, head_groups, s); return TB_OK;
-    case 5: launch_valu<Tag, D, 5>(a, num_work, head_groups, s); return TB_OK;
-    case 6: launch_valu<Tag, D, 6>(a, num_work, head_groups, s); return TB_OK;
-    case 7: launch_valu<Tag, D, 7>(a, num_work, head_groups, s); return TB_OK;
-    case 8: launch_valu<Tag, D, 8>(a, num_work, head_groups, s); return TB_OK;
+template <int D>
+static int dispatch_valu_rep(const attn_args& a, int num_work, hipStream_t s) {
+  switch (a.group) {
+    case 1: launch_valu<f32_t, D, 1>(a, num_work, s); return TB_OK;
+    case 2: launch_valu<f32_t, D, 2>(a, num_work, s); return TB_OK;
+    case 3: launch_valu<f32_t, D, 3>(a, num_work, s); return TB_OK;
+    case 4: launch_valu<f32_t, D, 4>(a, num_work, s); return TB_OK;
+    case 5: launch_valu<f32_t, D, 5>(a, num_work, s); return TB_OK;
+    case 6: launch_valu<f32_t, D, 6>(a, num_work, s); return TB_OK;
+    case 7: launch_valu<f32_t, D, 7>(a, num_work, s); return TB_OK;
+    case 8: launch_valu<f32_t, D, 8>(a, num_work, s); return TB_OK;
     default: return TB_ERR_UNSUPPORTED;
   }
 }
 
-template <typename Tag>
-static int dispatch_dim(const attn_args& a, int D, int rep_tile, int num_work, int head_groups,
-                        int num_rows, int max_parts, hipStream_t s) {
-  int st;
-  if (D == 64) st = dispatch_rep<Tag, 64>(a, rep_tile, num_work, head_groups, s);
-  else if (D == 128) st = dispatch_rep<Tag, 128>(a, rep_tile, num_work, head_groups, s);
-  else return TB_ERR_UNSUPPORTED;
-  if (st != TB_OK) return st;
-  if (max_parts > 1) {
-    if (D == 64)
-      hipLaunchKernelGGL((combine_partials_kernel<Tag, 64>), dim3(num_rows, a.num_heads), dim3(64), 0, s, a);
-    else
-      hipLaunchKernelGGL((combine_partials_kernel<Tag, 128>), dim3(num_rows, a.num_heads), dim3(128), 0, s, a);
-  }
-  return TB_OK;
+template <typename Tag, int D>
+static void launch_mfma(const attn_args& a, int num_work, hipStream_t stream) {
+  hipLaunchKernelGGL((paged_attn_mfma_kernel<Tag, D>), dim3(num_work, a.num_kv_heads, a.rep / a.group),
+                     dim3(64), 0, stream, a);
 }
 
-static int largest_rep_tile(int rep) {
-  for (int t = 8; t >= 1; --t)
+template <typename Tag, int D>
+static void launch_combine(const attn_args& a, int num_rows, hipStream_t stream) {
+  hipLaunchKernelGGL((combine_partials_kernel<Tag, D>), dim3(num_rows, a.num_heads), dim3(64), 0, stream, a);
+}
+
+static int largest_divisor_upto(int rep, int cap) {
+  for (int t = cap; t >= 1; --t)
     if (rep % t == 0) return t;
   return 1;
 }
@@ -405,15 +595,21 @@ static int elem_bytes(int32_t dtype) {
   return dtype == TB_DTYPE_F32 ? 4 : (dtype == TB_DTYPE_F16 || dtype == TB_DTYPE_BF16) ? 2 : 0;
 }
 
-static int chunk_tokens(int32_t dtype, int head_dim) {
-  const int eb = elem_bytes(dtype);
-  const int lpt = head_dim * eb / 16;
-  return 8 * (64 / lpt);
+// Partition lengths each kernel accepts.
+static bool partition_ok(int32_t dtype, int head_dim, int block_size, int part) {
+  if (part <= 0 || part % block_size != 0 || part / block_size > 64) return false;
+  if (elem_bytes(dtype) == 2) return part == PART16;
+  const int lpt = head_dim * 4 / 16;
+  const int chunk = 8 * (64 / lpt);
+  return part % chunk == 0;
 }
 
 }  // namespace tb
 
-extern "C" int32_t tb_attention_partition_tokens(void) { return 256; }
+extern "C" int32_t tb_attention_partition_tokens(int32_t dtype, int32_t head_dim) {
+  if (tb::elem_bytes(dtype) == 2) return tb::PART16;
+  return 256;
+}
 
 extern "C" size_t tb_paged_attention_workspace_bytes(int32_t total_partitions, int32_t num_heads,
                                                      int32_t head_dim) {
@@ -441,16 +637,14 @@ extern "C" int32_t tb_paged_attention(const void* q, int64_t q_row_stride, void*
   int log2_bs = 0;
   while ((1 << log2_bs) < block_size) ++log2_bs;
   TB_CHECK_ARG(num_rows >= 0 && num_work_items >= 0 && max_blocks_per_seq > 0 && num_blocks > 0);
-  // A partition is a whole number of chunks and spans at most 64 blocks.
-  TB_CHECK_ARG(partition_tokens > 0 && partition_tokens % chunk_tokens(dtype, head_dim) == 0);
-  TB_CHECK_ARG(partition_tokens % block_size == 0 && partition_tokens / block_size <= 64);
+  TB_CHECK_ARG(partition_ok(dtype, head_dim, block_size, partition_tokens));
   TB_CHECK_ARG(q_row_stride >= (int64_t)num_heads * head_dim);
   TB_CHECK_ARG(out_row_stride >= (int64_t)num_heads * head_dim);
   if (num_work_items == 0) return TB_OK;
   TB_CHECK_ARG(q && pool && out && block_tables && work_items && row_part_offsets);
   TB_CHECK_ARG((((uintptr_t)q | (uintptr_t)pool | (uintptr_t)out) & 15u) == 0);
   TB_CHECK_ARG((q_row_stride * eb) % 16 == 0 && (out_row_stride * eb) % 16 == 0);
-  TB_CHECK_ARG(max_parts_per_row >= 1);
+  TB_CHECK_ARG(max_parts_per_row >= 1 && total_partitions >= num_work_items && num_rows > 0);
   if (max_parts_per_row > 1) {
     TB_CHECK_ARG(workspace != nullptr);
     TB_CHECK_ARG(workspace_bytes >= tb_paged_attention_workspace_bytes(total_partitions, num_heads, head_dim));
@@ -464,9 +658,9 @@ extern "C" int32_t tb_paged_attention(const void* q, int64_t q_row_stride, void*
   }
 
   const int rep = num_heads / num_kv_heads;
-  const int rep_tile = largest_rep_tile(rep);
-  const int head_groups = rep / rep_tile;
-  TB_CHECK_ARG(num_kv_heads <= 65535 && head_groups <= 65535);
+  // heads per wave: the MFMA operand holds 16; the fp32 kernel keeps 8 in registers
+  const int group = largest_divisor_upto(rep, eb == 2 ? 16 : 8);
+  TB_CHECK_ARG(num_kv_heads <= 65535 && rep / group <= 65535);
 
   attn_args a;
   a.q = (const char*)q;
@@ -479,11 +673,13 @@ extern "C" int32_t tb_paged_attention(const void* q, int64_t q_row_stride, void*
   a.max_nb = max_blocks_per_seq;
   a.work = reinterpret_cast<const int4*>(work_items);
   a.row_part_off = row_part_offsets;
+  // workspace: [acc partials: parts x Hq x D][max/sum partials: parts x Hq x 2]
   a.ws_acc = (float*)workspace;
-  a.ws_ml = workspace ? (float*)workspace + (size_t)total_partitions * num_heads * head_dim : nullptr;
+  a.ws_ml = workspace ? a.ws_acc + (size_t)total_partitions * num_heads * head_dim : nullptr;
   a.num_heads = num_heads;
   a.num_kv_heads = num_kv_heads;
   a.rep = rep;
+  a.group = group;
   a.log2_bs = log2_bs;
   a.part_tokens = partition_tokens;
   a.scale_log2e = scale * 1.4426950408889634f;
@@ -492,11 +688,24 @@ extern "C" int32_t tb_paged_attention(const void* q, int64_t q_row_stride, void*
   a.v_new = (const char*)v_new;
   a.v_new_row_bytes = v_row_stride * eb;
 
-  int st;
+  const bool d64 = head_dim == 64;
+  int st = TB_OK;
   switch (dtype) {
-    case TB_DTYPE_F32: st = dispatch_dim<f32_t>(a, head_dim, rep_tile, num_work_items, head_groups, num_rows, max_parts_per_row, stream); break;
-    case TB_DTYPE_F16: st = dispatch_dim<f16_t>(a, head_dim, rep_tile, num_work_items, head_groups, num_rows, max_parts_per_row, stream); break;
-    case TB_DTYPE_BF16: st = dispatch_dim<bf16_t>(a, head_dim, rep_tile, num_work_items, head_groups, num_rows, max_parts_per_row, stream); break;
+    case TB_DTYPE_F32:
+      st = d64 ? dispatch_valu_rep<64>(a, num_work_items, stream) : dispatch_valu_rep<128>(a, num_work_items, stream);
+      if (st == TB_OK && max_parts_per_row > 1)
+        d64 ? launch_combine<f32_t, 64>(a, num_rows, stream) : launch_combine<f32_t, 128>(a, num_rows, stream);
+      break;
+    case TB_DTYPE_F16:
+      d64 ? launch_mfma<f16_t, 64>(a, num_work_items, stream) : launch_mfma<f16_t, 128>(a, num_work_items, stream);
+      if (max_parts_per_row > 1)
+        d64 ? launch_combine<f16_t, 64>(a, num_rows, stream) : launch_combine<f16_t, 128>(a, num_rows, stream);
+      break;
+    case TB_DTYPE_BF16:
+      d64 ? launch_mfma<bf16_t, 64>(a, num_work_items, stream) : launch_mfma<bf16_t, 128>(a, num_work_items, stream);
+      if (max_parts_per_row > 1)
+        d64 ? launch_combine<bf16_t, 64>(a, num_rows, stream) : launch_combine<bf16_t, 128>(a, num_rows, stream);
+      break;
     default: return TB_ERR_INVALID_ARG;
   }
   if (st != TB_OK) return st;

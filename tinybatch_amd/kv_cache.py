@@ -43,7 +43,7 @@ class PagedKVCache:
         self.head_dim = head_dim
         self.dtype = dtype
         self.device = device
-        self.partition_tokens = partition_tokens or int(_lib.lib().tb_attention_partition_tokens())
+        self.partition_tokens = partition_tokens or ops.partition_tokens(dtype, head_dim)
         self.storage = torch.zeros(n_layers, num_blocks, 2, n_kv_heads, block_size, head_dim,
                                    device=device, dtype=dtype)
         self.pools = [self.storage[i] for i in range(n_layers)]

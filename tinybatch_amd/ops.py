@@ -88,8 +88,15 @@ def kv_gather(pool: torch.Tensor, table: torch.Tensor, context_len: int) -> tupl
     return k_out, v_out
 
 
-def workspace_for(meta: StepMetadata, num_heads: int, head_dim: int, device: torch.device) -> torch.Tensor | None:
-    """Split-K partial buffer (grown on demand, cached per device)."""
+def partition_tokens(dtype: torch.dtype, head_dim: int) -> int:
+    """Default attention partition length (positions per wave) for this element type."""
+    return int(_lib.lib().tb_attention_partition_tokens(_lib.DTYPE_CODE[dtype], head_dim))
+
+
+def workspace_for(meta: StepMetadata, num_heads: int, head_dim: int,
+                  device: torch.device) -> torch.Tensor | None:
+    """Split-row partials buffer, grown on demand and cached per device (calls on
+    one stream are ordered, so consecutive calls can share it)."""
     if meta.max_parts_per_row <= 1:
         return None
     need = int(_lib.lib().tb_paged_attention_workspace_bytes(meta.total_partitions, num_heads, head_dim))
@@ -151,7 +158,8 @@ def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, 
         ksp, vsp = k_new.data_ptr(), v_new.data_ptr()
     if workspace is None:
         workspace = workspace_for(meta, num_heads, d, q.device)
-    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    ws = workspace
+    ws_bytes = 0 if ws is None else ws.numel() * ws.element_size()
     st = _lib.lib().tb_paged_attention(
         q.data_ptr(), qs, pool.data_ptr(), nb, out.data_ptr(), os_,
         meta.block_tables.data_ptr(), meta.max_blocks_per_seq,
@@ -159,7 +167,7 @@ def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, 
         meta.row_part_off.data_ptr(), T,
         max(meta.max_parts_per_row, 1), meta.partition_tokens, meta.total_partitions,
         num_heads, hkv, d, bs, float(scale), _lib.DTYPE_CODE[q.dtype],
-        ksp, ks, vsp, vs, _ptr(workspace), ws_bytes, _lib.stream_handle(q.device))
+        ksp, ks, vsp, vs, _ptr(ws), ws_bytes, _lib.stream_handle(q.device))
     _lib.check(st, "tb_paged_attention")
     return out
 
