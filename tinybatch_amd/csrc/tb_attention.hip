@@ -269,7 +269,11 @@ __global__ __launch_bounds__(64) void paged_attn_valu_kernel(const attn_args a) 
 }
 
 // ---------------------------------------------------------------------------
-// 16-bit kernel (see the file header). Lane l = 16*lg + lc.
+// 16-bit kernel (see the file header). A workgroup of NW waves owns one
+// partition of P positions; wave w takes positions [w*CT, (w+1)*CT) and issues
+// all of its K and V loads at once, so a whole partition is in flight. The
+// waves' (max, sum, acc) are merged in LDS; one partial (or the output) leaves
+// the workgroup. Lane l = 16*lg + lc.
 // MFMA 16x16x32 operand layouts (gfx950): A lane l holds A[l%16][8*(l/16)+j],
 // B lane l holds B[8*(l/16)+j][l%16], C/D lane l holds D[4*(l/16)+j][l%16].
 template <int D>
@@ -278,37 +282,46 @@ struct mfma_shape {
   static constexpr int KS = D / 32;          // q.k k-slices (32 dims each)
   static constexpr int NSL = D / 16;         // p.V output slices (16 dims each)
   static constexpr int P = PART16;
-  static constexpr int CT = 8192 / RB;       // positions per chunk (8 KB of K, 8 KB of V)
-  static constexpr int TILES = CT / 16;      // 16-position tiles per chunk
-  static constexpr int NCH = P / CT;         // chunks per partition
+  static constexpr int CT = 8192 / RB;       // positions per wave (8 KB of K, 8 KB of V)
+  static constexpr int NW = P / CT;          // waves per workgroup
+  static constexpr int TILES = CT / 16;      // 16-position tiles per wave
   static constexpr int VCOLS = RB / 16;      // 16-byte columns of a row
   static constexpr int VT = 64 / VCOLS;      // rows per V load instruction
-  static constexpr int VLD = CT / VT;        // V loads per lane per chunk
+  static constexpr int VLD = CT / VT;        // V loads per lane
   static constexpr int RS = RB + 8;          // LDS row stride: column reads hit 32 distinct banks
-  static_assert(TILES % 2 == 0 && P % CT == 0, "chunk shape");
+  static constexpr int HALVES = (TILES % 4 == 0) ? 2 : 1;   // V staged in LDS in HALVES parts
+  static constexpr int HALF = CT / HALVES;   // V positions staged at a time
+  static constexpr int STAGE = HALF * RS;    // V staging bytes per wave
+  static constexpr int MERGE = 16 * D * 4;   // per-wave acc bytes in the merge
+  static constexpr int LDS = NW * (STAGE > MERGE ? STAGE : MERGE);
+  static_assert(TILES % (2 * HALVES) == 0 && P % CT == 0 && VLD % HALVES == 0, "chunk shape");
 };
 
 template <typename Tag, int D>
-__global__ __launch_bounds__(64) void paged_attn_mfma_kernel(const attn_args a) {
+__global__ __launch_bounds__(64 * mfma_shape<D>::NW) __attribute__((amdgpu_waves_per_eu(5)))
+void paged_attn_mfma_kernel(const attn_args a) {
   using S = mfma_shape<D>;
   using M = math<Tag>;
   typedef typename M::vec8_t vec8_t;
   typedef typename M::scalar_t scalar_t;
-  constexpr int RB = S::RB, KS = S::KS, NSL = S::NSL, P = S::P, CT = S::CT, TILES = S::TILES;
-  constexpr int NCH = S::NCH, VCOLS = S::VCOLS, VT = S::VT, VLD = S::VLD, RS = S::RS;
+  constexpr int RB = S::RB, KS = S::KS, NSL = S::NSL, P = S::P, CT = S::CT, NW = S::NW;
+  constexpr int TILES = S::TILES, VCOLS = S::VCOLS, VT = S::VT, VLD = S::VLD, RS = S::RS;
 
-  __shared__ __align__(16) char v_lds[CT * RS];
+  __shared__ __align__(16) char lds[S::LDS];
+  __shared__ float2 ml_lds[NW][16];
 
-  const int lane = threadIdx.x;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
   const int lc = lane & 15, lg = lane >> 4;
   const int4 wi = a.work[blockIdx.x];
   const int row = wi.x, seq = wi.y, part = wi.z, ctx = wi.w;
   const int kvh = blockIdx.y;
-  const int R = a.group;                    // heads of this wave (<= 16)
+  const int R = a.group;                    // heads of this workgroup (<= 16)
   const int head0 = kvh * a.rep + blockIdx.z * R;
   const int p0 = part * P;
   const int n = min(P, ctx - p0);          // visible positions of this partition (>= 1)
-  const int nch = (n + CT - 1) / CT;
+  const int wb = wave * CT;                // this wave's first position (partition-relative)
+  const bool busy = wb < n;                // wave 0 always is
   const int bs = 1 << a.log2_bs;
 
   // Block-table entries of this partition: lane l holds entry p0/BS + l.
@@ -332,6 +345,28 @@ __global__ __launch_bounds__(64) void paged_attn_mfma_kernel(const attn_args a) 
     return (int64_t)blk * blk_bytes + (int64_t)(tau & (bs - 1)) * RB;
   };
 
+  // K tiles (A operand: lane holds position wb+16t+lc, bytes 64s+16lg) and V rows
+  // (16-byte column lane%VCOLS of row VT*i + lane/VCOLS), all issued now.
+  vec16 kd[TILES][KS], vd[VLD];
+  if (busy) {
+#pragma unroll
+    for (int t = 0; t < TILES; ++t) {
+      const int tau = wb + 16 * t + lc;
+      const int64_t off = pos_off(tau);
+      const char* src = pool_kvh + off + 16 * lg;
+      if (fused && tau == new_tau) src = k_new_row + 16 * lg;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) kd[t][s] = (tau < n) ? ld16_stream(src + 64 * s) : zero16();
+    }
+#pragma unroll
+    for (int i = 0; i < VLD; ++i) {
+      const int tau = wb + VT * i + lane / VCOLS;
+      const int64_t off = pos_off(tau);
+      const char* src = pool_kvh + v_off + off + 16 * (lane % VCOLS);
+      if (fused && tau == new_tau) src = v_new_row + 16 * (lane % VCOLS);
+      vd[i] = (tau < n) ? ld16_stream(src) : zero16();
+    }
+  }
   // q as the B operand of S^T = K.Q^T: lane holds q[head0+lc][32s + 8lg .. +8].
   vec16 qb[KS];
 #pragma unroll
@@ -342,123 +377,82 @@ __global__ __launch_bounds__(64) void paged_attn_mfma_kernel(const attn_args a) 
     for (int s = 0; s < KS; ++s) qb[s] = ld16(qrow + 64 * s);
   }
 
-  // K tiles (A operand: lane holds position 16t+lc, bytes 64s+16lg) and V rows
-  // (16-byte column lane%VCOLS of row VT*i + lane/VCOLS) of chunk c.
-  vec16 kd[2][TILES][KS], vd[2][VLD];
-  auto load_chunk = [&](int c, vec16 (&kk)[TILES][KS], vec16 (&vv)[VLD]) {
-#pragma unroll
-    for (int t = 0; t < TILES; ++t) {
-      const int tau = c * CT + 16 * t + lc;
-      const int64_t off = pos_off(tau);
-      const char* src = pool_kvh + off + 16 * lg;
-      if (fused && tau == new_tau) src = k_new_row + 16 * lg;
-#pragma unroll
-      for (int s = 0; s < KS; ++s) kk[t][s] = (tau < n) ? ld16(src + 64 * s) : zero16();
-    }
-#pragma unroll
-    for (int i = 0; i < VLD; ++i) {
-      const int tau = c * CT + VT * i + lane / VCOLS;
-      const int col = lane % VCOLS;
-      const int64_t off = pos_off(tau);
-      const char* src = pool_kvh + v_off + off + 16 * col;
-      if (fused && tau == new_tau) src = v_new_row + 16 * col;
-      vv[i] = (tau < n) ? ld16(src) : zero16();
-    }
-  };
-
-  float m_run = -INFINITY;   // running max of head lc (base-2 domain), same in all 4 lane groups
-  float l_part = 0.f;        // this lane's share of head lc's running sum
+  char* const vl = lds + wave * S::STAGE;
+  float m_w = -INFINITY;     // max of head lc over this wave's positions (base-2 domain)
+  float l_part = 0.f;        // this lane's share of head lc's sum
   float4_t acc[NSL];         // O[head 4lg+j][16n + lc]
 #pragma unroll
   for (int nn = 0; nn < NSL; ++nn) acc[nn] = float4_t{0.f, 0.f, 0.f, 0.f};
+  float4_t sc[TILES];        // S^T, then P: lane holds positions 16t + 4lg + j of head lc
 
-  load_chunk(0, kd[0], vd[0]);
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    if (c >= nch) break;
-    if (c + 1 < nch) load_chunk(c + 1, kd[(c + 1) & 1], vd[(c + 1) & 1]);
-    vec16(&ck)[TILES][KS] = kd[c & 1];
-    vec16(&cv)[VLD] = vd[c & 1];
-
+  if (busy) {
     if (fused) {   // the newest position's K/V rows go to their pool slot
 #pragma unroll
       for (int t = 0; t < TILES; ++t) {
-        const int tau = c * CT + 16 * t + lc;
+        const int tau = wb + 16 * t + lc;
         const int64_t off = pos_off(tau);
         if (tau == new_tau) {
 #pragma unroll
-          for (int s = 0; s < KS; ++s) st16(pool_kvh + off + 16 * lg + 64 * s, ck[t][s]);
+          for (int s = 0; s < KS; ++s) st16(pool_kvh + off + 16 * lg + 64 * s, kd[t][s]);
         }
       }
 #pragma unroll
       for (int i = 0; i < VLD; ++i) {
-        const int tau = c * CT + VT * i + lane / VCOLS;
+        const int tau = wb + VT * i + lane / VCOLS;
         const int64_t off = pos_off(tau);
-        if (tau == new_tau) st16(pool_kvh + v_off + off + 16 * (lane % VCOLS), cv[i]);
+        if (tau == new_tau) st16(pool_kvh + v_off + off + 16 * (lane % VCOLS), vd[i]);
       }
     }
-
-    // V rows into LDS (8-byte stores: the padded row stride is only 8-byte aligned)
-#pragma unroll
-    for (int i = 0; i < VLD; ++i) {
-      char* dst = v_lds + (VT * i + lane / VCOLS) * RS + 16 * (lane % VCOLS);
-      *reinterpret_cast<uint2*>(dst) = make_uint2(cv[i].w[0], cv[i].w[1]);
-      *reinterpret_cast<uint2*>(dst + 8) = make_uint2(cv[i].w[2], cv[i].w[3]);
-    }
-
-    // S^T tiles: lane holds positions 16t + 4lg + j of head lc
-    float4_t sc[TILES];
 #pragma unroll
     for (int t = 0; t < TILES; ++t) {
       sc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < KS; ++s)
-        sc[t] = M::mfma(__builtin_bit_cast(vec8_t, ck[t][s]), __builtin_bit_cast(vec8_t, qb[s]), sc[t]);
+        sc[t] = M::mfma(__builtin_bit_cast(vec8_t, kd[t][s]), __builtin_bit_cast(vec8_t, qb[s]), sc[t]);
     }
     float cm = -INFINITY;
 #pragma unroll
     for (int t = 0; t < TILES; ++t)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int tau = c * CT + 16 * t + 4 * lg + j;
-        const float v = tau < n ? sc[t][j] * a.scale_log2e : -INFINITY;
+        const float v = (wb + 16 * t + 4 * lg + j) < n ? sc[t][j] * a.scale_log2e : -INFINITY;
         sc[t][j] = v;
         cm = fmaxf(cm, v);
       }
     cm = fmaxf(cm, __shfl_xor(cm, 16));
-    cm = fmaxf(cm, __shfl_xor(cm, 32));
-    const float m_new = fmaxf(m_run, cm);          // finite: the chunk has a visible position
-    const float alpha = fast_exp2(m_run - m_new);
-    m_run = m_new;
-    float psum = 0.f;
+    m_w = fmaxf(cm, __shfl_xor(cm, 32));          // finite: the wave has a visible position
 #pragma unroll
     for (int t = 0; t < TILES; ++t)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        sc[t][j] = fast_exp2(sc[t][j] - m_new);
-        psum += sc[t][j];
+        sc[t][j] = fast_exp2(sc[t][j] - m_w);
+        l_part += sc[t][j];
       }
-    l_part = fmaf(l_part, alpha, psum);
-    // acc rows are heads 4lg+j: their factors live in lanes 4lg+j
+  }
+  // O += P.V over 32-position blocks: k index 8lg+j <-> position 32u + 4lg + j (j<4)
+  // or 32u + 16 + 4lg + (j-4): exactly the S^T values this lane holds. V goes
+  // through LDS in two halves of HALF positions (barriers are workgroup-uniform).
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float aj = __shfl(alpha, 4 * lg + j);
+  for (int hf = 0; hf < S::HALVES; ++hf) {
+    if (busy) {   // V rows of this part into the wave's stage (8-byte stores: 8-byte aligned stride)
 #pragma unroll
-      for (int nn = 0; nn < NSL; ++nn) acc[nn][j] *= aj;
+      for (int i = hf * (VLD / S::HALVES); i < (hf + 1) * (VLD / S::HALVES); ++i) {
+        char* dst = vl + (VT * i - hf * S::HALF + lane / VCOLS) * RS + 16 * (lane % VCOLS);
+        *reinterpret_cast<uint2*>(dst) = make_uint2(vd[i].w[0], vd[i].w[1]);
+        *reinterpret_cast<uint2*>(dst + 8) = make_uint2(vd[i].w[2], vd[i].w[3]);
+      }
     }
-    __syncthreads();   // V rows visible in LDS
-
-    // O += P.V over 32-position blocks: k index 8lg+j <-> position 32u + 4lg + j (j<4)
-    // or 32u + 16 + 4lg + (j-4): exactly the S^T values this lane holds.
+    __syncthreads();   // stage visible
+    if (busy) {
 #pragma unroll
-    for (int u = 0; u < TILES / 2; ++u) {
+    for (int u = hf * (TILES / 2 / S::HALVES); u < (hf + 1) * (TILES / 2 / S::HALVES); ++u) {
       vec8_t pa;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         pa[j] = (scalar_t)sc[2 * u][j];
         pa[4 + j] = (scalar_t)sc[2 * u + 1][j];
       }
-      const char* vbase = v_lds + (32 * u + 4 * lg) * RS + 2 * lc;
+      const char* vbase = vl + (32 * u - hf * S::HALF + 4 * lg) * RS + 2 * lc;
 #pragma unroll
       for (int nn = 0; nn < NSL; ++nn) {
         vec8_t vb;
@@ -470,40 +464,51 @@ __global__ __launch_bounds__(64) void paged_attn_mfma_kernel(const attn_args a) 
         acc[nn] = M::mfma(pa, vb, acc[nn]);
       }
     }
-    __syncthreads();   // LDS is rewritten by the next chunk
-  }
-
-  // Sum over the four lane groups, then hand each acc row its head's (m, l).
-  float l_tot = l_part + __shfl_xor(l_part, 16);
-  l_tot += __shfl_xor(l_tot, 32);
-  const int pbeg = a.row_part_off[row];
-  const int nparts = a.row_part_off[row + 1] - pbeg;
-  float lj[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) lj[j] = __shfl(l_tot, 4 * lg + j);
-  if (nparts == 1) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int h = 4 * lg + j;
-      if (h >= R) continue;
-      const float inv = 1.f / lj[j];
-      scalar_t* orow = reinterpret_cast<scalar_t*>(a.out + row * a.out_row_bytes) + (int64_t)(head0 + h) * D + lc;
-#pragma unroll
-      for (int nn = 0; nn < NSL; ++nn) orow[16 * nn] = (scalar_t)(acc[nn][j] * inv);
     }
-    return;
+    __syncthreads();   // stage consumed
   }
-  const int64_t pidx = pbeg + part;
+  float l_w = l_part + __shfl_xor(l_part, 16);
+  l_w += __shfl_xor(l_w, 32);
+  if (lg == 0) ml_lds[wave][lc] = make_float2(m_w, l_w);
+  __syncthreads();   // stats visible
+
+  // ---- merge the waves: acc rows (heads 4lg+j) scaled to the workgroup max ----
+  float* const acc_lds = reinterpret_cast<float*>(lds);   // [wave][16 heads][D]
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int h = 4 * lg + j;
-    if (h >= R) continue;
-    float* dst = a.ws_acc + (pidx * a.num_heads + head0 + h) * D + lc;
+    float Mh = ml_lds[0][h].x;
 #pragma unroll
-    for (int nn = 0; nn < NSL; ++nn) dst[16 * nn] = acc[nn][j];
+    for (int w = 1; w < NW; ++w) Mh = fmaxf(Mh, ml_lds[w][h].x);
+    const float f = busy ? fast_exp2(ml_lds[wave][h].x - Mh) : 0.f;
+    float* dst = acc_lds + ((wave * 16) + h) * D + lc;
+#pragma unroll
+    for (int nn = 0; nn < NSL; ++nn) dst[16 * nn] = acc[nn][j] * f;
   }
-  if (lg == 0 && lc < R)
-    *reinterpret_cast<float2*>(a.ws_ml + (pidx * a.num_heads + head0 + lc) * 2) = make_float2(m_run, l_tot);
+  __syncthreads();
+
+  const int pbeg = a.row_part_off[row];
+  const int nparts = a.row_part_off[row + 1] - pbeg;
+  const int64_t pidx = pbeg + part;
+  for (int idx = threadIdx.x; idx < R * D; idx += 64 * NW) {
+    const int h = idx / D, d = idx - h * D;
+    float Mh = ml_lds[0][h].x;
+#pragma unroll
+    for (int w = 1; w < NW; ++w) Mh = fmaxf(Mh, ml_lds[w][h].x);
+    float L = 0.f, o = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float2 ml = ml_lds[w][h];
+      if (ml.y > 0.f) L = fmaf(ml.y, fast_exp2(ml.x - Mh), L);   // idle waves hold (-inf, 0)
+      o += acc_lds[(w * 16 + h) * D + d];
+    }
+    if (nparts == 1) {
+      reinterpret_cast<scalar_t*>(a.out + row * a.out_row_bytes)[(int64_t)(head0 + h) * D + d] = (scalar_t)(o / L);
+    } else {
+      a.ws_acc[(pidx * a.num_heads + head0 + h) * D + d] = o;
+      if (d == 0) *reinterpret_cast<float2*>(a.ws_ml + (pidx * a.num_heads + head0 + h) * 2) = make_float2(Mh, L);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -577,7 +582,7 @@ static int dispatch_valu_rep(const attn_args& a, int num_work, hipStream_t s) {
 template <typename Tag, int D>
 static void launch_mfma(const attn_args& a, int num_work, hipStream_t stream) {
   hipLaunchKernelGGL((paged_attn_mfma_kernel<Tag, D>), dim3(num_work, a.num_kv_heads, a.rep / a.group),
-                     dim3(64), 0, stream, a);
+                     dim3(64 * mfma_shape<D>::NW), 0, stream, a);
 }
 
 template <typename Tag, int D>

@@ -30,6 +30,15 @@ __device__ __forceinline__ vec16 ld16(const void* p) {
   return r;
 }
 
+// Streamed once (K/V rows): non-temporal hint, the line is not kept in L2.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ vec16 ld16_stream(const void* p) {
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  vec16 r;
+  r.w[0] = v.x; r.w[1] = v.y; r.w[2] = v.z; r.w[3] = v.w;
+  return r;
+}
+
 __device__ __forceinline__ void st16(void* p, const vec16& r) {
   uint4 v;
   v.x = r.w[0]; v.y = r.w[1]; v.z = r.w[2]; v.w = r.w[3];
