@@ -77,12 +77,17 @@ def cpu_baseline(wl, reps: int, budget_s: float) -> dict:
                       f"{med * 1e3:.1f} ms, torch CPU ({cpu_model()})"}
 
 
-def load_traffic(name: str):
-    path = os.path.join(ROOT, "profiles", f"traffic_{name}.json")
+def load_traffic(workload: str, mode: str):
+    """HBM bytes per call measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, calibrated
+    against a plain device copy) in the committed profile summary, or None."""
+    path = os.path.join(ROOT, "profiles", f"paged_decode_{workload}_{mode}.md")
     if not os.path.exists(path):
         return None
     with open(path) as f:
-        return json.load(f).get("bytes_per_launch")
+        for line in f:
+            if line.startswith("traffic_bytes_per_call:"):
+                return int(line.split(":", 1)[1])
+    return None
 
 
 def main() -> int:
@@ -202,9 +207,11 @@ def main() -> int:
     bytes_layer = wl.algorithmic_bytes()
     total_bytes = bytes_layer["total"] * L
     gbs = total_bytes / (ms * 1e-3) / 1e9
-    per_launch_ms = ms / (L if fused else L)   # one attention launch per layer (plus the append in split mode)
+    # one tb_paged_attention call per layer (attention kernel + its combine kernel; plus the
+    # append kernel in split mode): the time per call is the step time over the layers
+    per_launch_ms = ms / L
     achieved = bytes_layer["total"] / (per_launch_ms * 1e-3) / 1e9
-    traffic = load_traffic(f"{wl.name}_{args.mode}")
+    traffic = load_traffic(wl.name, args.mode)
 
     cpu = None
     if not args.no_cpu:
@@ -217,7 +224,8 @@ def main() -> int:
         if big:
             cpu["sample"] += " (first 16 sequences of the workload)"
 
-    kernel = "paged_attn_valu_kernel" + ("" if fused else " + kv_append_kernel")
+    attn = "paged_attn_valu_kernel" if wl.dtype == torch.float32 else "paged_attn_mfma_kernel"
+    kernel = attn + " + combine_partials_kernel" + ("" if fused else " + kv_append_kernel")
     line = {
         "metric": METRIC,
         "value": round(gbs, 2),

@@ -261,3 +261,16 @@ def test_block_sizes_16bit(BS, dtype):
     _attention_vs_oracle(c, 14, 2, dtype)
     c = _mixed_case(10, 16, 4, 128, BS, dtype, qlens=[1, 2], cached=[333, 1000])
     _attention_vs_oracle(c, 16, 4, dtype)
+
+
+def test_golden_fixture_decode_fp32():
+    """GPU decode step of the committed fixture (inputs regenerated from its seed)."""
+    import os
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "qwen_fp32_b8_decode.npz"))
+    wl = make_decode_workload("qwen-fp32-b8")
+    pool = wl.pool.to(DEV)
+    meta = _meta(wl.positions, wl.seq_slices, wl.block_tables, wl.context_lens, 16, wl.num_blocks)
+    out = ops.paged_attention(wl.q.to(DEV), pool, meta, num_heads=14, k_new=wl.k_new.to(DEV), v_new=wl.v_new.to(DEV))
+    torch.cuda.synchronize()
+    assert np.abs(out.cpu().numpy() - g["attn_out_f64"]).max() <= 1e-5
+    assert np.abs(out.cpu().numpy() - g["attn_out"]).max() <= 1e-5
