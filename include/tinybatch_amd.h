@@ -85,7 +85,10 @@ int32_t tb_kv_gather(const void* pool, int64_t num_blocks,
  *   q:   [num_rows][num_heads][head_dim], row stride q_row_stride (elements)
  *   out: [num_rows][num_heads * head_dim], row stride out_row_stride
  *   block_tables: [num_seqs][max_blocks_per_seq] int32 physical block ids
- *   work_items: [num_work_items][4] int32 = (row, seq, partition, row_ctx);
+ *   work_items: [num_work_items][4] int32 = (row, seq, partition | (rows-1) << 24,
+ *     row_ctx): rows row .. row+rows-1 of sequence seq (fp16/bf16 only: up to
+ *     16 / heads-per-group consecutive query rows whose partition counts are
+ *     equal; the later rows see one more position each; fp32: rows = 1);
  *     partition p covers positions [p*P, min((p+1)*P, row_ctx)) with
  *     P = partition_tokens (a multiple of block_size spanning at most 64
  *     blocks; fp16/bf16 require tb_attention_partition_tokens(dtype, D),

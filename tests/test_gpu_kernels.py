@@ -25,9 +25,9 @@ def _bits(t: torch.Tensor) -> torch.Tensor:
     return t.contiguous().view(torch.int32 if t.element_size() == 4 else torch.int16)
 
 
-def _meta(positions, slices, tables, ctx, BS, NB, P=256):
+def _meta(positions, slices, tables, ctx, BS, NB, P=256, rows=1):
     return build_step_metadata(positions, slices, tables, ctx, block_size=BS, num_blocks=NB,
-                               partition_tokens=P).to(DEV)
+                               partition_tokens=P, rows_per_item=rows).to(DEV)
 
 
 def _mixed_case(seed, Hq, Hkv, D, BS, dtype, qlens, cached, NB=None, nan_tail=False):
@@ -110,14 +110,17 @@ def test_gather_bit_exact(dtype):
 
 
 # ---------------------------------------------------------------- K2 attention
-def _attention_vs_oracle(c, Hq, Hkv, dtype, P=256):
+def _attention_vs_oracle(c, Hq, Hkv, dtype, P=256, rows=None):
+    """Both work-item shapes: one row per item and (16-bit) the widest row group."""
     want = ref.attention(c["q"], c["pool"], c["slices"], c["tables"], c["ctx"], Hq, Hkv)
-    meta = _meta(c["pos"], c["slices"], c["tables"], c["ctx"], c["pool"].shape[3], c["NB"], P=P)
-    out = ops.paged_attention(c["q"].to(DEV), c["pool"].to(DEV), meta, num_heads=Hq)
-    torch.cuda.synchronize()
-    got = out.cpu()
-    assert torch.isfinite(got).all()
-    torch.testing.assert_close(got.float(), want.float(), **TOL[dtype])
+    shapes = [1, ops.rows_per_item(dtype, Hq, Hkv)] if rows is None else [rows]
+    for r in sorted(set(shapes)):
+        meta = _meta(c["pos"], c["slices"], c["tables"], c["ctx"], c["pool"].shape[3], c["NB"], P=P, rows=r)
+        out = ops.paged_attention(c["q"].to(DEV), c["pool"].to(DEV), meta, num_heads=Hq)
+        torch.cuda.synchronize()
+        got = out.cpu()
+        assert torch.isfinite(got).all(), f"rows per item {r}"
+        torch.testing.assert_close(got.float(), want.float(), **TOL[dtype], msg=lambda m: f"rows per item {r}: {m}")
     return got, want
 
 
@@ -274,3 +277,21 @@ def test_golden_fixture_decode_fp32():
     torch.cuda.synchronize()
     assert np.abs(out.cpu().numpy() - g["attn_out_f64"]).max() <= 1e-5
     assert np.abs(out.cpu().numpy() - g["attn_out"]).max() <= 1e-5
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("Hq,Hkv,D", [(14, 2, 64), (32, 8, 128), (8, 8, 64)])
+def test_prefill_rows_grouped(dtype, Hq, Hkv, D):
+    """Full prefills (q_len == ctx, the is_causal branch), a cached-prefix tail
+    (1 < q_len < ctx) and decodes in one batch; rows straddle partition edges."""
+    c = _mixed_case(11, Hq, Hkv, D, 16, dtype, qlens=[300, 1, 37, 260, 1, 3], cached=[0, 700, 220, 0, 40, 509])
+    _attention_vs_oracle(c, Hq, Hkv, dtype)
+
+
+def test_prefill_config4_shape_bf16():
+    """Eight 512-token prefills next to 56 decodes, Qwen geometry, bf16."""
+    qlens = [512] * 8 + [1] * 56
+    g = torch.Generator().manual_seed(12)
+    cached = [0] * 8 + torch.randint(256, 2049, (56,), generator=g).tolist()
+    c = _mixed_case(12, 14, 2, 64, 16, torch.bfloat16, qlens=qlens, cached=cached)
+    _attention_vs_oracle(c, 14, 2, torch.bfloat16)

@@ -80,3 +80,30 @@ def test_off_by_one_of_block_multiple_prompt_is_refused():
     position 16, which needs a second block (the engine must reserve it)."""
     with pytest.raises(IndexError):
         build_step_metadata([16], [(0, 1)], [[3]], [17], block_size=16, num_blocks=8, partition_tokens=256)
+
+
+def test_row_groups_cover_each_row_partition_once():
+    # seq0: 40-row prefill (ctx 40); seq1: decode; seq2: 9-row tail of ctx 70
+    q = [40, 1, 9]
+    ctx = [40, 77, 70]
+    positions, slices, t = [], [], 0
+    for n, c in zip(q, ctx):
+        positions += list(range(c - n, c))
+        slices.append((t, t + n)); t += n
+    tables = [list(range(0, 3)), list(range(3, 8)), list(range(8, 13))]
+    m = build_step_metadata(positions, slices, tables, ctx, block_size=16, num_blocks=16,
+                            partition_tokens=32, rows_per_item=4)
+    seen = {}
+    for row0, seq, z, rc in m.work_np.tolist():
+        part, nrows = z & 0xFFFFFF, (z >> 24) + 1
+        assert 1 <= nrows <= 4
+        s, e = slices[seq]
+        assert s <= row0 and row0 + nrows <= e
+        parts = {-(-(m.row_ctx_np[r]) // 32) for r in range(row0, row0 + nrows)}
+        assert len(parts) == 1                               # equal partition counts in a group
+        for i in range(nrows):
+            assert m.row_ctx_np[row0 + i] == rc + i
+            seen[(row0 + i, part)] = seen.get((row0 + i, part), 0) + 1
+    want = {(r, p) for r in range(t) for p in range(-(-int(m.row_ctx_np[r]) // 32))}
+    assert set(seen) == want and all(v == 1 for v in seen.values())
+    assert m.total_partitions == len(want)

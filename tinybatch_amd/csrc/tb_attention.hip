@@ -148,8 +148,8 @@ __global__ __launch_bounds__(64) void paged_attn_valu_kernel(const attn_args a) 
   const int j = lane % LPT;  // 16-byte column of the token row
   const int g = lane / LPT;  // token slot inside one wave load
 
-  const int4 wi = a.work[blockIdx.x];
-  const int row = wi.x, seq = wi.y, part = wi.z, ctx = wi.w;
+  const int4 wi = a.work[blockIdx.x];   // one row per item on this path
+  const int row = wi.x, seq = wi.y, part = wi.z & 0xFFFFFF, ctx = wi.w;
   const int kvh = blockIdx.y;
   const int head0 = kvh * a.rep + blockIdx.z * REP;
 
@@ -313,13 +313,20 @@ void paged_attn_mfma_kernel(const attn_args a) {
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int lc = lane & 15, lg = lane >> 4;
+  // Work item: rows row0 .. row0+nrows-1 of one sequence (consecutive query
+  // rows, row_ctx ctx0, ctx0+1, ...), one partition. The 16 MFMA columns are
+  // (row, head) pairs: column c = qi*R + h. Decode rows come one per item.
   const int4 wi = a.work[blockIdx.x];
-  const int row = wi.x, seq = wi.y, part = wi.z, ctx = wi.w;
+  const int row0 = wi.x, seq = wi.y, part = wi.z & 0xFFFFFF, nrows = (wi.z >> 24) + 1, ctx0 = wi.w;
   const int kvh = blockIdx.y;
-  const int R = a.group;                    // heads of this workgroup (<= 16)
+  const int R = a.group;                    // heads of this workgroup; nrows * R <= 16
   const int head0 = kvh * a.rep + blockIdx.z * R;
   const int p0 = part * P;
-  const int n = min(P, ctx - p0);          // visible positions of this partition (>= 1)
+  const int n = min(P, ctx0 + nrows - 1 - p0);   // positions visible to the last row (>= 1)
+  const int ctx = ctx0;                     // the single decode row's context (fused append)
+  const int ncols = nrows * R;
+  const int qi = lc / R;                    // this lane's column: row qi, head lc - qi*R
+  const int n_col = lc < ncols ? min(P, ctx0 + qi - p0) : n;   // positions visible to the column
   const int wb = wave * CT;                // this wave's first position (partition-relative)
   const bool busy = wb < n;                // wave 0 always is
   const int bs = 1 << a.log2_bs;
@@ -337,8 +344,8 @@ void paged_attn_mfma_kernel(const attn_args a) {
   char* const pool_kvh = a.pool + kvh * tile_bytes;
   const bool fused = (a.k_new != nullptr);
   const int new_tau = ctx - 1 - p0;         // partition-relative index of the newest position
-  const char* k_new_row = fused ? a.k_new + row * a.k_new_row_bytes + (int64_t)kvh * RB : nullptr;
-  const char* v_new_row = fused ? a.v_new + row * a.v_new_row_bytes + (int64_t)kvh * RB : nullptr;
+  const char* k_new_row = fused ? a.k_new + row0 * a.k_new_row_bytes + (int64_t)kvh * RB : nullptr;
+  const char* v_new_row = fused ? a.v_new + row0 * a.v_new_row_bytes + (int64_t)kvh * RB : nullptr;
   // Pool offset of position p0+tau (this kv head). Shuffles: every lane runs it.
   auto pos_off = [&](int tau) -> int64_t {
     const int blk = __shfl(my_blk, (tau >> a.log2_bs) & 63);
@@ -367,12 +374,12 @@ void paged_attn_mfma_kernel(const attn_args a) {
       vd[i] = (tau < n) ? ld16_stream(src) : zero16();
     }
   }
-  // q as the B operand of S^T = K.Q^T: lane holds q[head0+lc][32s + 8lg .. +8].
+  // q as the B operand of S^T = K.Q^T: lane holds q[row0+qi][head0+h][32s + 8lg .. +8].
   vec16 qb[KS];
 #pragma unroll
   for (int s = 0; s < KS; ++s) qb[s] = zero16();
-  if (lc < R) {
-    const char* qrow = a.q + row * a.q_row_bytes + (int64_t)(head0 + lc) * RB + 16 * lg;
+  if (lc < ncols) {
+    const char* qrow = a.q + (row0 + qi) * a.q_row_bytes + (int64_t)(head0 + lc - qi * R) * RB + 16 * lg;
 #pragma unroll
     for (int s = 0; s < KS; ++s) qb[s] = ld16(qrow + 64 * s);
   }
@@ -415,17 +422,19 @@ void paged_attn_mfma_kernel(const attn_args a) {
     for (int t = 0; t < TILES; ++t)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float v = (wb + 16 * t + 4 * lg + j) < n ? sc[t][j] * a.scale_log2e : -INFINITY;
+        const float v = (wb + 16 * t + 4 * lg + j) < n_col ? sc[t][j] * a.scale_log2e : -INFINITY;
         sc[t][j] = v;
         cm = fmaxf(cm, v);
       }
     cm = fmaxf(cm, __shfl_xor(cm, 16));
-    m_w = fmaxf(cm, __shfl_xor(cm, 32));          // finite: the wave has a visible position
+    m_w = fmaxf(cm, __shfl_xor(cm, 32));
+    // a column whose visible positions all lie before this wave's range gets p = 0
+    const float m_safe = m_w == -INFINITY ? 0.f : m_w;
 #pragma unroll
     for (int t = 0; t < TILES; ++t)
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        sc[t][j] = fast_exp2(sc[t][j] - m_w);
+        sc[t][j] = fast_exp2(sc[t][j] - m_safe);
         l_part += sc[t][j];
       }
   }
@@ -472,26 +481,28 @@ void paged_attn_mfma_kernel(const attn_args a) {
   if (lg == 0) ml_lds[wave][lc] = make_float2(m_w, l_w);
   __syncthreads();   // stats visible
 
-  // ---- merge the waves: acc rows (heads 4lg+j) scaled to the workgroup max ----
-  float* const acc_lds = reinterpret_cast<float*>(lds);   // [wave][16 heads][D]
+  // ---- merge the waves: acc rows (columns 4lg+j) scaled to the workgroup max ----
+  float* const acc_lds = reinterpret_cast<float*>(lds);   // [wave][16 columns][D]
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int h = 4 * lg + j;
     float Mh = ml_lds[0][h].x;
 #pragma unroll
     for (int w = 1; w < NW; ++w) Mh = fmaxf(Mh, ml_lds[w][h].x);
-    const float f = busy ? fast_exp2(ml_lds[wave][h].x - Mh) : 0.f;
+    const float mw = ml_lds[wave][h].x;
+    const float f = (busy && mw != -INFINITY) ? fast_exp2(mw - Mh) : 0.f;
     float* dst = acc_lds + ((wave * 16) + h) * D + lc;
 #pragma unroll
     for (int nn = 0; nn < NSL; ++nn) dst[16 * nn] = acc[nn][j] * f;
   }
   __syncthreads();
 
-  const int pbeg = a.row_part_off[row];
-  const int nparts = a.row_part_off[row + 1] - pbeg;
-  const int64_t pidx = pbeg + part;
-  for (int idx = threadIdx.x; idx < R * D; idx += 64 * NW) {
-    const int h = idx / D, d = idx - h * D;
+  for (int idx = threadIdx.x; idx < ncols * D; idx += 64 * NW) {
+    const int h = idx / D, d = idx - h * D;          // h: column
+    const int row = row0 + h / R, head = head0 + h - (h / R) * R;
+    const int pbeg = a.row_part_off[row];
+    const int nparts = a.row_part_off[row + 1] - pbeg;   // the same for every row of the item
+    const int64_t pidx = pbeg + part;
     float Mh = ml_lds[0][h].x;
 #pragma unroll
     for (int w = 1; w < NW; ++w) Mh = fmaxf(Mh, ml_lds[w][h].x);
@@ -503,10 +514,10 @@ void paged_attn_mfma_kernel(const attn_args a) {
       o += acc_lds[(w * 16 + h) * D + d];
     }
     if (nparts == 1) {
-      reinterpret_cast<scalar_t*>(a.out + row * a.out_row_bytes)[(int64_t)(head0 + h) * D + d] = (scalar_t)(o / L);
+      reinterpret_cast<scalar_t*>(a.out + row * a.out_row_bytes)[(int64_t)head * D + d] = (scalar_t)(o / L);
     } else {
-      a.ws_acc[(pidx * a.num_heads + head0 + h) * D + d] = o;
-      if (d == 0) *reinterpret_cast<float2*>(a.ws_ml + (pidx * a.num_heads + head0 + h) * 2) = make_float2(Mh, L);
+      a.ws_acc[(pidx * a.num_heads + head) * D + d] = o;
+      if (d == 0) *reinterpret_cast<float2*>(a.ws_ml + (pidx * a.num_heads + head) * 2) = make_float2(Mh, L);
     }
   }
 }

@@ -53,7 +53,8 @@ class PagedKVCache:
         return sum(p.numel() * p.element_size() for p in self.pools)
 
     # ---- per-step metadata -------------------------------------------------
-    def step_metadata(self, positions, seq_slices, block_tables, context_lens=None) -> StepMetadata:
+    def step_metadata(self, positions, seq_slices, block_tables, context_lens=None,
+                      rows_per_item: int = 1) -> StepMetadata:
         """Build (or reuse) the step's device metadata.
 
         Every layer of a forward pass passes the same argument objects, so the
@@ -67,15 +68,16 @@ class PagedKVCache:
         for e in self._meta_cache:
             if (_same_positions(e["pos"], pos_key) and e["slices"] == [tuple(x) for x in seq_slices]
                     and e["tables"] == block_tables
-                    and (context_lens is None or e["ctx"] == context_lens)):
+                    and (context_lens is None or (e["ctx"] == context_lens and e["rows"] == rows_per_item))):
                 return e["meta"]
         meta = build_step_metadata(positions, seq_slices, block_tables, context_lens,
                                    block_size=self.block_size, num_blocks=self.num_blocks,
-                                   partition_tokens=self.partition_tokens)
+                                   partition_tokens=self.partition_tokens, rows_per_item=rows_per_item)
         meta.to(self.device)
         entry = {"pos": pos_key, "slices": [tuple(x) for x in seq_slices],
                  "tables": [list(t) for t in block_tables],
-                 "ctx": None if context_lens is None else list(context_lens), "meta": meta}
+                 "ctx": None if context_lens is None else list(context_lens), "rows": rows_per_item,
+                 "meta": meta}
         self._meta_cache = [entry] + self._meta_cache[:1]
         return meta
 
@@ -104,7 +106,8 @@ class PagedKVCache:
                   out: torch.Tensor | None = None) -> torch.Tensor:
         """attn_out [T, Hq*D] for the whole flat batch (reference model.py:130-147)."""
         hq = num_heads if num_heads is not None else q.shape[1]
-        meta = self._lookup_or_build(positions, seq_slices, block_tables, context_lens, q.shape[0])
+        rows = ops.rows_per_item(q.dtype, hq, self.n_kv_heads)
+        meta = self._lookup_or_build(positions, seq_slices, block_tables, context_lens, q.shape[0], rows)
         return ops.paged_attention(q, self.pools[layer], meta, num_heads=hq, scale=scale, out=out)
 
     def decode_step(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, meta: StepMetadata,
@@ -128,8 +131,9 @@ class PagedKVCache:
         for pool, st in zip(self.pools, staging):
             ops.block_scatter(st, pool, blocks)
 
-    def _lookup_or_build(self, positions, seq_slices, block_tables, context_lens, num_tokens) -> StepMetadata:
-        meta = self.step_metadata(positions, seq_slices, block_tables, context_lens)
+    def _lookup_or_build(self, positions, seq_slices, block_tables, context_lens, num_tokens,
+                         rows_per_item: int = 1) -> StepMetadata:
+        meta = self.step_metadata(positions, seq_slices, block_tables, context_lens, rows_per_item)
         if meta.num_tokens != num_tokens:
             raise ValueError(f"{num_tokens} tokens given, positions describe {meta.num_tokens}")
         return meta

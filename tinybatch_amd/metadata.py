@@ -12,9 +12,12 @@ step and uploaded in a single host-to-device copy:
   every slice and for all but the last writer of a duplicated slot, so the
   parallel append equals the reference's sequential "last in batch order wins".
 * ``block_tables[B, max_nb]`` - tables padded with 0 (padding is never read).
-* ``work[W, 4]`` - (row, seq, partition, row_ctx) for the attention kernel, where
-  row_ctx = ctx - q_len + i + 1 is the number of positions query row i may see
-  (the mask rule j <= ctx - q_len + i of model.py:139-145).
+* ``work[W, 4]`` - (row, seq, partition | (rows-1) << 24, row_ctx) for the
+  attention kernel: rows row .. row+rows-1 of one sequence (rows = 1 unless
+  ``rows_per_item`` > 1 groups consecutive prefill rows, never across a change
+  of partition count), where row_ctx = ctx - q_len + i + 1 is the number of
+  positions query row i may see (the mask rule j <= ctx - q_len + i of
+  model.py:139-145) and the group's later rows see one more position each.
 * ``row_part_off[T + 1]`` - running count of partitions per row.
 
 Errors mirror the reference: a table too short for a position raises
@@ -40,6 +43,7 @@ class StepMetadata:
     total_partitions: int
     max_parts_per_row: int
     decode_only: bool            # every sequence has exactly one query row
+    rows_per_item: int
     # host copies
     slot_mapping_np: np.ndarray
     block_tables_np: np.ndarray
@@ -86,7 +90,7 @@ def _host_positions(positions) -> np.ndarray:
 
 def build_step_metadata(positions, seq_slices, block_tables, context_lens, *, block_size: int,
                         num_blocks: int, partition_tokens: int, num_tokens: int | None = None,
-                        validate_attention: bool = True) -> StepMetadata:
+                        validate_attention: bool = True, rows_per_item: int = 1) -> StepMetadata:
     """Build the per-step arrays (host side). See the module docstring."""
     if block_size <= 0 or block_size & (block_size - 1):
         raise ValueError(f"block_size must be a power of two, got {block_size}")
@@ -167,27 +171,50 @@ def build_step_metadata(positions, seq_slices, block_tables, context_lens, *, bl
         nparts_by_row[row_ids] = (row_ctx + P - 1) // P
     row_part_off = np.zeros(T + 1, dtype=np.int64)
     np.cumsum(nparts_by_row, out=row_part_off[1:])
-    W = int(row_part_off[-1])
+    if not 1 <= rows_per_item <= 16:
+        raise ValueError("rows_per_item must be in [1, 16]")
+    total_parts = int(row_part_off[-1])
+    # groups of consecutive rows of one sequence with equal partition counts
+    grp_row, grp_len = row_ids, np.ones(tot, dtype=np.int64)
+    if rows_per_item > 1 and tot:
+        starts_l, lens_l = [], []
+        for b in range(B):
+            s0, e0 = int(starts[b]), int(ends[b])
+            i = s0
+            while i < e0:
+                j = min(e0, i + rows_per_item)
+                k = i + 1
+                while k < j and nparts_by_row[k] == nparts_by_row[i]:
+                    k += 1
+                starts_l.append(i)
+                lens_l.append(k - i)
+                i = k
+        grp_row = np.asarray(starts_l, dtype=np.int64)
+        grp_len = np.asarray(lens_l, dtype=np.int64)
+    grp_parts = nparts_by_row[grp_row] if tot else np.zeros(0, np.int64)
+    keep = grp_parts > 0
+    grp_row, grp_len, grp_parts = grp_row[keep], grp_len[keep], grp_parts[keep]
+    W = int(grp_parts.sum())
     work = np.zeros((W, 4), dtype=np.int64)
     if W:
-        has = nparts_by_row > 0
-        rows = np.nonzero(has)[0]
-        np_r = nparts_by_row[rows]
-        rep_rows = np.repeat(rows, np_r)
-        work[:, 0] = rep_rows
+        rep_rows = np.repeat(grp_row, grp_parts)
         seq_of_row = np.zeros(T, dtype=np.int64)
         seq_of_row[row_ids] = row_seq
+        item_off = np.concatenate([[0], np.cumsum(grp_parts)[:-1]])
+        part = np.arange(W) - np.repeat(item_off, grp_parts)
+        work[:, 0] = rep_rows
         work[:, 1] = seq_of_row[rep_rows]
-        work[:, 2] = np.arange(W) - np.repeat(row_part_off[rows], np_r)
+        work[:, 2] = part | ((np.repeat(grp_len, grp_parts) - 1) << 24)
         work[:, 3] = row_ctx_by_row[rep_rows]
-    if max(T, W, max_nb, int(row_part_off[-1])) >= 2**31:
+    if max(T, W, max_nb, total_parts) >= 2**24 - 1:
         raise ValueError("step too large for int32 metadata")
 
     return StepMetadata(
         num_tokens=T, num_seqs=B, block_size=block_size, partition_tokens=P,
-        max_blocks_per_seq=max_nb, num_work_items=W, total_partitions=W,
+        max_blocks_per_seq=max_nb, num_work_items=W, total_partitions=total_parts,
         max_parts_per_row=int(nparts_by_row.max()) if T else 0,
         decode_only=bool(B) and bool(np.all(qlens == 1)),
+        rows_per_item=int(rows_per_item),
         slot_mapping_np=slots.astype(np.int32),
         block_tables_np=tables[:max(B, 1)].astype(np.int32),
         work_np=work.astype(np.int32),

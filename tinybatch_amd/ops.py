@@ -88,6 +88,21 @@ def kv_gather(pool: torch.Tensor, table: torch.Tensor, context_len: int) -> tupl
     return k_out, v_out
 
 
+def heads_per_group(dtype: torch.dtype, num_heads: int, num_kv_heads: int) -> int:
+    """Query heads one work item serves (the C dispatch uses the same rule)."""
+    rep = num_heads // num_kv_heads
+    cap = 16 if dtype in (torch.float16, torch.bfloat16) else 8
+    return max(t for t in range(1, cap + 1) if rep % t == 0)
+
+
+def rows_per_item(dtype: torch.dtype, num_heads: int, num_kv_heads: int) -> int:
+    """Consecutive query rows one 16-bit work item serves: its MFMA operand holds
+    16 (row, head) columns. fp32 items serve one row."""
+    if dtype not in (torch.float16, torch.bfloat16):
+        return 1
+    return max(1, 16 // heads_per_group(dtype, num_heads, num_kv_heads))
+
+
 def partition_tokens(dtype: torch.dtype, head_dim: int) -> int:
     """Default attention partition length (positions per wave) for this element type."""
     return int(_lib.lib().tb_attention_partition_tokens(_lib.DTYPE_CODE[dtype], head_dim))
@@ -140,6 +155,9 @@ def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, 
     os_ = _rows_view("out", out, num_heads, d)
     if meta.work is None:
         raise ValueError("metadata has not been uploaded (call meta.to(device))")
+    if meta.rows_per_item > rows_per_item(q.dtype, num_heads, hkv):
+        raise ValueError(f"metadata groups {meta.rows_per_item} rows per item; this geometry allows "
+                         f"{rows_per_item(q.dtype, num_heads, hkv)}")
     if scale is None:
         scale = 1.0 / math.sqrt(d)   # scaled_dot_product_attention's default (model.py:140,146)
     ksp = vsp = None
