@@ -90,6 +90,136 @@ def load_traffic(workload: str, mode: str):
     return None
 
 
+def time_step(step, dev, args) -> tuple[float, bool]:
+    """ms per call of ``step``: one eager warm-up, capture into a HIP graph (unless
+    --no-graph), W untimed and K timed replays bracketed by events on the stream
+    the work runs on."""
+    import torch
+
+    stream = torch.cuda.Stream(device=dev)
+    stream.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(stream):
+        step()                                   # eager warm-up (also exercises every launch)
+    torch.cuda.synchronize()
+    graph = None
+    if not args.no_graph:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            step()
+        torch.cuda.synchronize()
+
+    def run_once():
+        # replays and eager launches both go to `stream`, the stream the events are recorded on
+        with torch.cuda.stream(stream):
+            if graph is not None:
+                graph.replay()
+            else:
+                step()
+
+    for _ in range(args.warmup):
+        run_once()
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        ev0.record(stream)
+    for _ in range(args.steps):
+        run_once()
+    with torch.cuda.stream(stream):
+        ev1.record(stream)
+    torch.cuda.synchronize()
+    return ev0.elapsed_time(ev1) / args.steps, graph is not None
+
+
+MFMA_PEAK_TFLOPS_16 = 2500.0
+
+
+def bench_mixed(args, dev) -> int:
+    """Mixed engine step (8 x 512-token prefills + 56 decodes, shared prefix) and a
+    1024-block compaction round, on rotating layer pools. Times the whole layer
+    step (append + attention), the prefill rows alone (MFMA-bound: reported in
+    TFLOP/s against the dense 16-bit MFMA peak), the decode rows alone (GB/s)
+    and the block copy over every layer pool in one launch (GB/s)."""
+    import torch
+
+    from tinybatch_amd import ops
+    from tinybatch_amd.metadata import build_step_metadata
+    from tinybatch_amd.workloads import make_mixed_workload
+
+    t0 = time.perf_counter()
+    wl = make_mixed_workload()
+    _log(f"workload {wl.name}: T={wl.num_tokens} seqs={wl.batch} ({time.perf_counter() - t0:.1f}s)")
+    L = args.layers or 24
+    storage = torch.empty((L,) + tuple(wl.pool.shape), dtype=wl.dtype, device=dev)
+    src = wl.pool.to(dev)
+    for l in range(L):
+        storage[l].copy_(src)
+    del src
+    pools = [storage[l] for l in range(L)]
+    P = args.partition or ops.partition_tokens(wl.dtype, wl.head_dim)
+    rows = ops.rows_per_item(wl.dtype, wl.num_heads, wl.num_kv_heads)
+    Hq = wl.num_heads
+    results = {}
+    for which, w in (("step", wl), ("prefill", wl.part("prefill")), ("decode", wl.part("decode"))):
+        meta = build_step_metadata(w.positions, w.seq_slices, w.block_tables, w.context_lens,
+                                   block_size=w.block_size, num_blocks=w.num_blocks, partition_tokens=P,
+                                   rows_per_item=rows).to(dev)
+        q, k, v = w.q.to(dev), w.k_new.to(dev), w.v_new.to(dev)
+        out = torch.empty(w.num_tokens, Hq * w.head_dim, dtype=w.dtype, device=dev)
+        ws = ops.workspace_for(meta, Hq, w.head_dim, dev)
+        append = which == "step"
+
+        def step(meta=meta, q=q, k=k, v=v, out=out, ws=ws, append=append):
+            for pool in pools:
+                if append:
+                    ops.kv_append(pool, k, v, meta.slot_mapping)
+                ops.paged_attention(q, pool, meta, num_heads=Hq, out=out, workspace=ws)
+
+        ms, graph = time_step(step, dev, args)
+        results[which] = (ms / L, w)
+        _log(f"{which}: {ms / L * 1e3:.2f} us per layer")
+    plan = ops.BlockCopyPlan(pools, wl.copy_src, wl.copy_dst)
+    ms_copy, _ = time_step(plan.launch, dev, args)
+    _log(f"copy: {ms_copy * 1e3:.2f} us for {L} layer pools")
+
+    step_ms, _ = results["step"]
+    b = wl.algorithmic_bytes()
+    step_gbs = (b["append"] + b["attention"]) / (step_ms * 1e-3) / 1e9
+    pre_ms, pre = results["prefill"]
+    pre_tflops = pre.flops() / (pre_ms * 1e-3) / 1e12
+    dec_ms, dec = results["decode"]
+    dec_gbs = dec.algorithmic_bytes()["attention"] / (dec_ms * 1e-3) / 1e9
+    copy_gbs = b["copy"] * L / (ms_copy * 1e-3) / 1e9
+    line = {
+        "metric": "mixed step: prefill attention TFLOP/s (MFMA), decode attention and block copy GB/s",
+        "value": round(pre_tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(step_ms * L, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) pool, q, k, v; seeded random block tables, one shared prefix)",
+        "config": {"workload": f"{wl.name}: 8 x 512-token prefills + 56 decodes (24 share a 32-block "
+                               f"prefix) per layer, {L} layer pools; 1024-block copy over all pools",
+                   "tokens": wl.num_tokens, "layers": L, "partition_tokens": P, "rows_per_item": rows,
+                   "graph": graph},
+        "step_us_per_layer": round(step_ms * 1e3, 3),
+        "step_algorithmic_GBps": round(step_gbs, 2),
+        "prefill_us_per_layer": round(pre_ms * 1e3, 3),
+        "decode_us_per_layer": round(dec_ms * 1e3, 3),
+        "decode_kv_bytes_logical": dec.algorithmic_bytes()["attention"],
+        "decode_kv_bytes_unique": dec.unique_kv_bytes(),
+        "copy_us_all_layers": round(ms_copy * 1e3, 3),
+        "roofline": {"bound": "mfma", "achieved": round(pre_tflops, 2), "peak": MFMA_PEAK_TFLOPS_16,
+                     "unit": "TFLOP/s", "frac": round(pre_tflops / MFMA_PEAK_TFLOPS_16, 4), "traffic": None,
+                     "kernel": "paged_attn_mfma_kernel + combine_partials_kernel (prefill rows)"},
+        "decode_roofline": {"bound": "hbm", "achieved": round(dec_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                            "frac": round(dec_gbs / HBM_PEAK_GBS, 4)},
+        "copy_roofline": {"bound": "hbm", "achieved": round(copy_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                          "frac": round(copy_gbs / HBM_PEAK_GBS, 4), "kernel": "block_copy_kernel"},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -137,6 +267,9 @@ def main() -> int:
                           "bytes_written_per_launch": n, "launches": 5}), flush=True)
         return 0
 
+    if args.workload == "qwen-bf16-mixed":
+        return bench_mixed(args, dev)
+
     big = args.workload == "llama-bf16-b256"
     t0 = time.perf_counter()
     wl = make_decode_workload(args.workload, pool_device=(dev if big else "cpu"))
@@ -169,39 +302,7 @@ def main() -> int:
                 ops.kv_append(pool, k, v, meta.slot_mapping)
                 ops.paged_attention(q, pool, meta, num_heads=wl.num_heads, out=out, workspace=ws)
 
-    stream = torch.cuda.Stream(device=dev)
-    stream.wait_stream(torch.cuda.current_stream(dev))
-    with torch.cuda.stream(stream):
-        step()                                   # eager warm-up (also exercises every launch)
-    torch.cuda.synchronize()
-    graph = None
-    if not args.no_graph:
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=stream):
-            step()
-        torch.cuda.synchronize()
-
-    def run_once():
-        # replays and eager launches both go to `stream`, the stream the events are recorded on
-        with torch.cuda.stream(stream):
-            if graph is not None:
-                graph.replay()
-            else:
-                step()
-
-    for _ in range(args.warmup):
-        run_once()
-    torch.cuda.synchronize()
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    with torch.cuda.stream(stream):
-        ev0.record(stream)
-    for _ in range(args.steps):
-        run_once()
-    with torch.cuda.stream(stream):
-        ev1.record(stream)
-    torch.cuda.synchronize()
-    ms = ev0.elapsed_time(ev1) / args.steps
+    ms, graph = time_step(step, dev, args)
     _log(f"{L} layers x {args.steps} steps: {ms:.4f} ms/step")
 
     bytes_layer = wl.algorithmic_bytes()
@@ -244,7 +345,7 @@ def main() -> int:
             "batch": wl.batch, "num_heads": wl.num_heads, "num_kv_heads": wl.num_kv_heads,
             "head_dim": wl.head_dim, "block_size": wl.block_size, "num_blocks": wl.num_blocks,
             "mean_context": round(sum(wl.context_lens) / wl.batch, 1), "layers": L,
-            "mode": args.mode, "graph": graph is not None, "partition_tokens": P,
+            "mode": args.mode, "graph": graph, "partition_tokens": P,
             "bytes_per_layer_step": bytes_layer["total"],
         },
         "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),

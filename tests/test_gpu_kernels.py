@@ -295,3 +295,31 @@ def test_prefill_config4_shape_bf16():
     cached = [0] * 8 + torch.randint(256, 2049, (56,), generator=g).tolist()
     c = _mixed_case(12, 14, 2, 64, 16, torch.bfloat16, qlens=qlens, cached=cached)
     _attention_vs_oracle(c, 14, 2, torch.bfloat16)
+
+
+def test_mixed_step_config4_append_attention_copy():
+    """The mixed engine step at full size: 8 x 512-token prefills + 56 decodes
+    (24 share a 32-block prefix) in bf16 — append bit-exact, attention within
+    2e-2 with grouped prefill rows, then the 1024-block compaction copy bit-exact."""
+    from tinybatch_amd.workloads import make_mixed_workload
+    wl = make_mixed_workload()
+    BS = wl.block_size
+    pos = torch.tensor(wl.positions, dtype=torch.int64)
+    want_pool = wl.pool.clone()
+    ref.kv_write(want_pool, wl.k_new, wl.v_new, pos, wl.seq_slices, wl.block_tables, BS)
+    want = ref.attention(wl.q, want_pool, wl.seq_slices, wl.block_tables, wl.context_lens,
+                         wl.num_heads, wl.num_kv_heads)
+    rows = ops.rows_per_item(wl.dtype, wl.num_heads, wl.num_kv_heads)
+    assert rows == 2
+    meta = _meta(wl.positions, wl.seq_slices, wl.block_tables, wl.context_lens, BS, wl.num_blocks, rows=rows)
+    pool = wl.pool.to(DEV)
+    ops.kv_append(pool, wl.k_new.to(DEV), wl.v_new.to(DEV), meta.slot_mapping)
+    out = ops.paged_attention(wl.q.to(DEV), pool, meta, num_heads=wl.num_heads)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(pool.cpu()), _bits(want_pool))
+    torch.testing.assert_close(out.cpu().float(), want.float(), **TOL[torch.bfloat16])
+    # compaction round: live blocks move to free ids
+    ops.block_copy([pool], wl.copy_src, wl.copy_dst)
+    torch.cuda.synchronize()
+    want_pool[wl.copy_dst] = want_pool[wl.copy_src]
+    assert torch.equal(_bits(pool.cpu()), _bits(want_pool))

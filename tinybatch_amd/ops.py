@@ -197,31 +197,48 @@ def _block_ids(name: str, ids, num_blocks: int, device) -> torch.Tensor:
     return torch.from_numpy(arr.astype(np.int32)).to(device)
 
 
+class BlockCopyPlan:
+    """A validated copy round over a fixed set of layer pools: ids and pool pointers
+    live on the device, so ``launch`` makes no host round trip and can be
+    captured in a HIP graph (the pools must stay allocated while it is in use)."""
+
+    def __init__(self, pools: list[torch.Tensor], src, dst):
+        if not pools:
+            raise ValueError("no layer pools")
+        nb = pools[0].shape[0]
+        for p in pools:
+            _check_pool(p)
+            if p.shape != pools[0].shape or p.dtype != pools[0].dtype or p.device != pools[0].device:
+                raise ValueError("all layer pools must share shape, dtype and device")
+        s_np = np.asarray(src.cpu() if isinstance(src, torch.Tensor) else src, dtype=np.int64).reshape(-1)
+        d_np = np.asarray(dst.cpu() if isinstance(dst, torch.Tensor) else dst, dtype=np.int64).reshape(-1)
+        if s_np.size != d_np.size:
+            raise ValueError("src and dst differ in length")
+        if d_np.size != np.unique(d_np).size:
+            raise ValueError("dst block ids must be distinct")
+        if np.intersect1d(s_np, d_np).size:
+            raise ValueError("a dst block is also a src block; split the copy into rounds")
+        self.device = pools[0].device
+        self.num_blocks = nb
+        self.num_layers = len(pools)
+        self.num_pairs = int(s_np.size)
+        self.block_bytes = pools[0][0].numel() * pools[0].element_size()
+        self.src = _block_ids("src", s_np, nb, self.device)
+        self.dst = _block_ids("dst", d_np, nb, self.device)
+        self.ptrs = torch.tensor([p.data_ptr() for p in pools], dtype=torch.int64).to(self.device)
+
+    def launch(self) -> None:
+        st = _lib.lib().tb_block_copy(self.ptrs.data_ptr(), self.num_layers, self.num_blocks, self.src.data_ptr(),
+                                      self.dst.data_ptr(), self.num_pairs, self.block_bytes,
+                                      _lib.stream_handle(self.device))
+        _lib.check(st, "tb_block_copy")
+
+
 def block_copy(pools: list[torch.Tensor], src, dst) -> None:
     """K3: pool_l[dst[i]] <- pool_l[src[i]] for every layer pool l, one launch."""
     if not pools:
         return
-    nb = pools[0].shape[0]
-    block_bytes = pools[0][0].numel() * pools[0].element_size()
-    for p in pools:
-        _check_pool(p)
-        if p.shape != pools[0].shape or p.dtype != pools[0].dtype or p.device != pools[0].device:
-            raise ValueError("all layer pools must share shape, dtype and device")
-    s_np = np.asarray(src.cpu() if isinstance(src, torch.Tensor) else src, dtype=np.int64).reshape(-1)
-    d_np = np.asarray(dst.cpu() if isinstance(dst, torch.Tensor) else dst, dtype=np.int64).reshape(-1)
-    if s_np.size != d_np.size:
-        raise ValueError("src and dst differ in length")
-    if d_np.size != np.unique(d_np).size:
-        raise ValueError("dst block ids must be distinct")
-    if np.intersect1d(s_np, d_np).size:
-        raise ValueError("a dst block is also a src block; split the copy into rounds")
-    dev = pools[0].device
-    s_t = _block_ids("src", s_np, nb, dev)
-    d_t = _block_ids("dst", d_np, nb, dev)
-    ptrs = torch.tensor([p.data_ptr() for p in pools], dtype=torch.int64).to(dev)
-    st = _lib.lib().tb_block_copy(ptrs.data_ptr(), len(pools), nb, s_t.data_ptr(), d_t.data_ptr(), int(s_np.size),
-                                  block_bytes, _lib.stream_handle(dev))
-    _lib.check(st, "tb_block_copy")
+    BlockCopyPlan(pools, src, dst).launch()
 
 
 def block_gather(pool: torch.Tensor, blocks, staging: torch.Tensor) -> None:

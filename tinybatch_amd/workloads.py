@@ -17,6 +17,15 @@ block permutation, q, new k, new v, then the pool (N(0,1), drawn in fp32 and
 cast). A pool too large to draw on the CPU in reasonable time is drawn on the
 GPU from its own seeded generator instead (``pool_device``).
 Block tables are consecutive chunks of one random permutation of the pool.
+
+``qwen-bf16-mixed`` is one mixed engine step (``make_mixed_workload``): Qwen
+geometry in bf16, eight fresh 512-token prefills (q_len = ctx = 512, the
+is_causal branch) scheduled before 56 decodes (the engine's token order,
+reference src/tinybatch/engine.py:104-120). 32 decodes have U{256..2048}
+cached tokens; 24 share one 32-block (512-token) prompt prefix, as prefix-cache
+hits do (reference src/tinybatch/block_manager.py:94-104), and have
+U{512..2048} cached tokens so that the prefix fits. Plus a compaction round of
+1024 block copies (distinct sources in use, destinations free).
 """
 from __future__ import annotations
 
@@ -133,3 +142,142 @@ def make_decode_workload(name: str, *, pool_device: str | torch.device = "cpu", 
     return DecodeWorkload(name=name, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, block_size=BS, dtype=dt,
                           num_blocks=NB, cached_lens=cached, block_tables=tables, q=q, k_new=k_new,
                           v_new=v_new, pool=pool, seed=seed)
+
+
+@dataclass
+class MixedWorkload:
+    name: str
+    num_heads: int
+    num_kv_heads: int
+    head_dim: int
+    block_size: int
+    dtype: torch.dtype
+    num_blocks: int
+    q_lens: list[int]
+    context_lens: list[int]
+    block_tables: list[list[int]]
+    q: torch.Tensor          # [T, Hq, D]
+    k_new: torch.Tensor      # [T, Hkv, D]
+    v_new: torch.Tensor      # [T, Hkv, D]
+    pool: torch.Tensor       # [NB, 2, Hkv, BS, D]
+    copy_src: list[int]
+    copy_dst: list[int]
+    shared_prefix: list[int]
+    num_prefill: int
+    seed: int
+
+    @property
+    def batch(self) -> int:
+        return len(self.q_lens)
+
+    @property
+    def num_tokens(self) -> int:
+        return sum(self.q_lens)
+
+    @property
+    def seq_slices(self) -> list[tuple[int, int]]:
+        out, at = [], 0
+        for n in self.q_lens:
+            out.append((at, at + n))
+            at += n
+        return out
+
+    @property
+    def positions(self) -> list[int]:
+        pos = []
+        for n, c in zip(self.q_lens, self.context_lens):
+            pos.extend(range(c - n, c))
+        return pos
+
+    def part(self, which: str) -> "MixedWorkload":
+        """The prefill-only or decode-only sub-batch (same pool, same tables)."""
+        sel = range(self.num_prefill) if which == "prefill" else range(self.num_prefill, self.batch)
+        sl = self.seq_slices
+        rows = torch.cat([torch.arange(sl[i][0], sl[i][1]) for i in sel])
+        return MixedWorkload(
+            name=f"{self.name}:{which}", num_heads=self.num_heads, num_kv_heads=self.num_kv_heads,
+            head_dim=self.head_dim, block_size=self.block_size, dtype=self.dtype, num_blocks=self.num_blocks,
+            q_lens=[self.q_lens[i] for i in sel], context_lens=[self.context_lens[i] for i in sel],
+            block_tables=[self.block_tables[i] for i in sel], q=self.q[rows], k_new=self.k_new[rows],
+            v_new=self.v_new[rows], pool=self.pool, copy_src=self.copy_src, copy_dst=self.copy_dst,
+            shared_prefix=self.shared_prefix, num_prefill=self.num_prefill if which == "prefill" else 0,
+            seed=self.seed)
+
+    def algorithmic_bytes(self) -> dict:
+        """append: read k,v + write the pool rows + slots; attention: every visible
+        K/V row of every sequence once (shared prefix counted per sequence, as
+        logical bytes), q and out of every row, block-table entries, context
+        lengths; copy: read + write of every copied block."""
+        b = torch.tensor([], dtype=self.dtype).element_size()
+        Hq, Hkv, D, BS = self.num_heads, self.num_kv_heads, self.head_dim, self.block_size
+        T = self.num_tokens
+        append = T * 2 * Hkv * D * b * 2 + 4 * T
+        attn = (sum(self.context_lens) * 2 * Hkv * D * b + 2 * T * Hq * D * b
+                + 4 * sum((c + BS - 1) // BS for c in self.context_lens) + 4 * self.batch)
+        copy = 2 * len(self.copy_src) * 2 * Hkv * BS * D * b
+        return {"append": append, "attention": attn, "copy": copy}
+
+    def unique_kv_bytes(self) -> int:
+        """K/V bytes of distinct blocks the attention reads (shared prefix once)."""
+        b = torch.tensor([], dtype=self.dtype).element_size()
+        used = set()
+        for t, c in zip(self.block_tables, self.context_lens):
+            used.update(t[:(c + self.block_size - 1) // self.block_size])
+        return len(used) * 2 * self.num_kv_heads * self.block_size * self.head_dim * b
+
+    def flops(self) -> int:
+        """Attention flops: 2 (QK) + 2 (PV) per head, dim and visible (row, key) pair."""
+        pairs = 0
+        for n, c in zip(self.q_lens, self.context_lens):
+            first = c - n
+            pairs += sum(first + i + 1 for i in range(n))
+        return 4 * self.num_heads * self.head_dim * pairs
+
+
+def make_mixed_workload(name: str = "qwen-bf16-mixed", *, seed: int = 4, num_blocks: int = 32768,
+                        num_copies: int = 1024) -> MixedWorkload:
+    if name != "qwen-bf16-mixed":
+        raise KeyError(name)
+    gen = torch.Generator().manual_seed(seed)
+    Hq, Hkv, D, BS, dt = 14, 2, 64, 16, torch.bfloat16
+    n_pre, pre_len, n_dec, n_share, prefix_blocks = 8, 512, 32, 24, 32
+    cached_dec = torch.randint(256, 2049, (n_dec,), generator=gen).tolist()
+    cached_share = torch.randint(prefix_blocks * BS, 2049, (n_share,), generator=gen).tolist()
+    perm = torch.randperm(num_blocks, generator=gen).tolist()
+    at = 0
+
+    def take(n):
+        nonlocal at
+        ids = perm[at:at + n]
+        at += n
+        return ids
+
+    tables, q_lens, ctx = [], [], []
+    for _ in range(n_pre):
+        tables.append(take(pre_len // BS))
+        q_lens.append(pre_len)
+        ctx.append(pre_len)
+    for c in cached_dec:
+        tables.append(take((c + 1 + BS - 1) // BS))
+        q_lens.append(1)
+        ctx.append(c + 1)
+    prefix = take(prefix_blocks)
+    for c in cached_share:
+        tables.append(prefix + take((c + 1 + BS - 1) // BS - prefix_blocks))
+        q_lens.append(1)
+        ctx.append(c + 1)
+    in_use = perm[:at]
+    if at + num_copies > num_blocks:
+        raise ValueError("pool too small for the copy round")
+    dst = take(num_copies)
+    src_idx = torch.randperm(len(in_use), generator=gen)[:num_copies].tolist()
+    src = [in_use[i] for i in src_idx]
+    T = sum(q_lens)
+    q = torch.randn(T, Hq, D, generator=gen).to(dt)
+    k_new = torch.randn(T, Hkv, D, generator=gen).to(dt)
+    v_new = torch.randn(T, Hkv, D, generator=gen).to(dt)
+    pool = torch.randn(num_blocks, 2, Hkv, BS, D, generator=gen).to(dt)
+    return MixedWorkload(name=name, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, block_size=BS, dtype=dt,
+                         num_blocks=num_blocks, q_lens=q_lens, context_lens=ctx, block_tables=tables, q=q,
+                         k_new=k_new, v_new=v_new, pool=pool, copy_src=src, copy_dst=dst,
+                         shared_prefix=prefix, num_prefill=n_pre, seed=seed)
