@@ -163,7 +163,7 @@ def bench_mixed(args, dev) -> int:
     for which, w in (("step", wl), ("prefill", wl.part("prefill")), ("decode", wl.part("decode"))):
         meta = build_step_metadata(w.positions, w.seq_slices, w.block_tables, w.context_lens,
                                    block_size=w.block_size, num_blocks=w.num_blocks, partition_tokens=P,
-                                   rows_per_item=rows).to(dev)
+                                   rows_per_item=rows, tile_prefill=not args.no_tiles).to(dev)
         q, k, v = w.q.to(dev), w.k_new.to(dev), w.v_new.to(dev)
         out = torch.empty(w.num_tokens, Hq * w.head_dim, dtype=w.dtype, device=dev)
         ws = ops.workspace_for(meta, Hq, w.head_dim, dev)
@@ -199,7 +199,7 @@ def bench_mixed(args, dev) -> int:
         "config": {"workload": f"{wl.name}: 8 x 512-token prefills + 56 decodes (24 share a 32-block "
                                f"prefix) per layer, {L} layer pools; 1024-block copy over all pools",
                    "tokens": wl.num_tokens, "layers": L, "partition_tokens": P, "rows_per_item": rows,
-                   "graph": graph},
+                   "prefill_tiles": not args.no_tiles, "graph": graph},
         "step_us_per_layer": round(step_ms * 1e3, 3),
         "step_algorithmic_GBps": round(step_gbs, 2),
         "prefill_us_per_layer": round(pre_ms * 1e3, 3),
@@ -209,7 +209,8 @@ def bench_mixed(args, dev) -> int:
         "copy_us_all_layers": round(ms_copy * 1e3, 3),
         "roofline": {"bound": "mfma", "achieved": round(pre_tflops, 2), "peak": MFMA_PEAK_TFLOPS_16,
                      "unit": "TFLOP/s", "frac": round(pre_tflops / MFMA_PEAK_TFLOPS_16, 4), "traffic": None,
-                     "kernel": "paged_attn_mfma_kernel + combine_partials_kernel (prefill rows)"},
+                     "kernel": ("paged_attn_mfma_kernel + combine_partials_kernel" if args.no_tiles
+                                else "paged_prefill_mfma_kernel") + " (prefill rows)"},
         "decode_roofline": {"bound": "hbm", "achieved": round(dec_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                             "frac": round(dec_gbs / HBM_PEAK_GBS, 4)},
         "copy_roofline": {"bound": "hbm", "achieved": round(copy_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -233,6 +234,7 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (profiling runs)")
     ap.add_argument("--partition", type=int, default=0)
+    ap.add_argument("--no-tiles", action="store_true", help="mixed step: prefill rows as row groups, not tiles")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB five times (HBM counter calibration)")
     args = ap.parse_args()

@@ -92,11 +92,22 @@ int32_t tb_kv_gather(const void* pool, int64_t num_blocks,
  *     partition p covers positions [p*P, min((p+1)*P, row_ctx)) with
  *     P = partition_tokens (a multiple of block_size spanning at most 64
  *     blocks; fp16/bf16 require tb_attention_partition_tokens(dtype, D),
- *     fp32 accepts any multiple of its 8-load chunk). Every row
- *     lists partitions 0 .. ceil(row_ctx/P)-1, row_part_offsets[num_rows+1]
- *     is their running count (row r owns partial slots
- *     row_part_offsets[r] ..), total_partitions = row_part_offsets[num_rows]
- *     and max_parts_per_row is the largest per-row count.
+ *     fp32 accepts any multiple of its 8-load chunk). Every row served by
+ *     work items lists partitions 0 .. ceil(row_ctx/P)-1,
+ *     row_part_offsets[num_rows+1] is their running count (row r owns
+ *     partial slots row_part_offsets[r] ..; rows served by tiles count 0),
+ *     total_partitions = row_part_offsets[num_rows] and max_parts_per_row is
+ *     the largest per-row count.
+ *   prefill_tiles: [num_prefill_tiles][4] int32 = (row0, seq,
+ *     rows | part << 8, pos0), fp16/bf16 only: query rows row0 .. row0+rows-1
+ *     (rows <= TB_PREFILL_TILE_ROWS) of sequence seq at positions
+ *     pos0 .. pos0+rows-1, positions [part*T, (part+1)*T) of their range with
+ *     T = TB_PREFILL_TILE_PARTITION (one workgroup per item and query head).
+ *     A tile row counts ceil(row_ctx/T) partitions in row_part_offsets; one
+ *     item per partition its tile's last row reaches. Rows in tiles must not
+ *     also appear in work items.
+ *   split_rows: [num_split_rows] int32, the rows with more than one partition;
+ *     their partials are merged by a combine kernel.
  *   workspace: >= tb_paged_attention_workspace_bytes(total_partitions, ...)
  *     bytes of device memory (16-byte aligned) for the split-row partials;
  *     only used when a row has > 1 partition (max_parts_per_row > 1), which
@@ -110,6 +121,10 @@ int32_t tb_kv_gather(const void* pool, int64_t num_blocks,
  */
 int32_t tb_attention_partition_tokens(int32_t dtype, int32_t head_dim);
 
+/* Prefill tile shape: rows per tile, positions per tile partition. */
+#define TB_PREFILL_TILE_ROWS 64
+#define TB_PREFILL_TILE_PARTITION 1024
+
 size_t tb_paged_attention_workspace_bytes(int32_t total_partitions, int32_t num_heads,
                                           int32_t head_dim);
 
@@ -118,7 +133,9 @@ int32_t tb_paged_attention(const void* q, int64_t q_row_stride,
                            void* out, int64_t out_row_stride,
                            const int32_t* block_tables, int32_t max_blocks_per_seq,
                            const int32_t* work_items, int32_t num_work_items,
+                           const int32_t* prefill_tiles, int32_t num_prefill_tiles,
                            const int32_t* row_part_offsets, int32_t num_rows,
+                           const int32_t* split_rows, int32_t num_split_rows,
                            int32_t max_parts_per_row, int32_t partition_tokens,
                            int32_t total_partitions,
                            int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,

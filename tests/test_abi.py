@@ -61,14 +61,14 @@ def test_attention_rejects_bad_arguments_without_launching():
     f = ctypes.c_void_p(4096)
 
     def call(**kw):
-        a = dict(q=f, qs=896, pool=f, nb=64, out=f, os=896, bt=f, mnb=4, work=f, nw=2, rpo=f, nr=2,
-                 mpr=1, pt=256, tp=2, hq=14, hkv=2, d=64, bs=16, scale=0.125, dt=1,
-                 kn=None, ks=0, vn=None, vs=0, ws=None, wsb=0)
+        a = dict(q=f, qs=896, pool=f, nb=64, out=f, os=896, bt=f, mnb=4, work=f, nw=2, tiles=None, nt=0,
+                 rpo=f, nr=2, split=None, ns=0, mpr=1, pt=256, tp=2, hq=14, hkv=2, d=64, bs=16, scale=0.125,
+                 dt=1, kn=None, ks=0, vn=None, vs=0, ws=None, wsb=0)
         a.update(kw)
         return L.tb_paged_attention(a["q"], a["qs"], a["pool"], a["nb"], a["out"], a["os"], a["bt"], a["mnb"],
-                                    a["work"], a["nw"], a["rpo"], a["nr"], a["mpr"], a["pt"], a["tp"], a["hq"],
-                                    a["hkv"], a["d"], a["bs"], a["scale"], a["dt"], a["kn"], a["ks"], a["vn"],
-                                    a["vs"], a["ws"], a["wsb"], None)
+                                    a["work"], a["nw"], a["tiles"], a["nt"], a["rpo"], a["nr"], a["split"], a["ns"],
+                                    a["mpr"], a["pt"], a["tp"], a["hq"], a["hkv"], a["d"], a["bs"], a["scale"],
+                                    a["dt"], a["kn"], a["ks"], a["vn"], a["vs"], a["ws"], a["wsb"], None)
 
     assert call(d=96) == _lib.TB_ERR_UNSUPPORTED               # no kernel for head_dim 96
     assert call(hq=13) == _lib.TB_ERR_INVALID_ARG              # heads not a multiple of kv heads
@@ -79,6 +79,11 @@ def test_attention_rejects_bad_arguments_without_launching():
     assert call(pt=512) == _lib.TB_ERR_INVALID_ARG             # 16-bit kernel has a fixed partition
     assert call(kn=f, vn=None) == _lib.TB_ERR_INVALID_ARG      # fused append needs both k and v
     assert call(nw=0) == _lib.TB_OK                            # empty step: nothing to launch
+    assert call(dt=0, pt=256, tiles=f, nt=1) == _lib.TB_ERR_UNSUPPORTED   # prefill tiles are 16-bit only
+    assert call(tiles=None, nt=1) == _lib.TB_ERR_INVALID_ARG   # tiles announced, none given
+    assert call(tiles=f, nt=1, kn=f, vn=f, ks=128, vs=128) == _lib.TB_ERR_INVALID_ARG   # fused append: decode only
+    assert call(split=f, ns=1, mpr=1) == _lib.TB_ERR_INVALID_ARG   # split rows imply > 1 partition
+    assert call(split=f, ns=3, nr=2, mpr=2, ws=f, wsb=1 << 20) == _lib.TB_ERR_INVALID_ARG   # more split rows than rows
 
 
 def test_workspace_size_formula():

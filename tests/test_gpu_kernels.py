@@ -25,9 +25,9 @@ def _bits(t: torch.Tensor) -> torch.Tensor:
     return t.contiguous().view(torch.int32 if t.element_size() == 4 else torch.int16)
 
 
-def _meta(positions, slices, tables, ctx, BS, NB, P=256, rows=1):
+def _meta(positions, slices, tables, ctx, BS, NB, P=256, rows=1, tiles=False):
     return build_step_metadata(positions, slices, tables, ctx, block_size=BS, num_blocks=NB,
-                               partition_tokens=P, rows_per_item=rows).to(DEV)
+                               partition_tokens=P, rows_per_item=rows, tile_prefill=tiles).to(DEV)
 
 
 def _mixed_case(seed, Hq, Hkv, D, BS, dtype, qlens, cached, NB=None, nan_tail=False):
@@ -111,16 +111,22 @@ def test_gather_bit_exact(dtype):
 
 # ---------------------------------------------------------------- K2 attention
 def _attention_vs_oracle(c, Hq, Hkv, dtype, P=256, rows=None):
-    """Both work-item shapes: one row per item and (16-bit) the widest row group."""
+    """Every work shape: one row per item, (16-bit) the widest row group, and
+    (16-bit) prefill tiles for sequences with many new rows."""
     want = ref.attention(c["q"], c["pool"], c["slices"], c["tables"], c["ctx"], Hq, Hkv)
-    shapes = [1, ops.rows_per_item(dtype, Hq, Hkv)] if rows is None else [rows]
-    for r in sorted(set(shapes)):
-        meta = _meta(c["pos"], c["slices"], c["tables"], c["ctx"], c["pool"].shape[3], c["NB"], P=P, rows=r)
+    widest = ops.rows_per_item(dtype, Hq, Hkv)
+    shapes = [(1, False), (widest, False)] if rows is None else [(rows, False)]
+    if rows is None and dtype != torch.float32:
+        shapes.append((widest, True))
+    for r, tiles in sorted(set(shapes)):
+        meta = _meta(c["pos"], c["slices"], c["tables"], c["ctx"], c["pool"].shape[3], c["NB"], P=P, rows=r,
+                     tiles=tiles)
         out = ops.paged_attention(c["q"].to(DEV), c["pool"].to(DEV), meta, num_heads=Hq)
         torch.cuda.synchronize()
         got = out.cpu()
-        assert torch.isfinite(got).all(), f"rows per item {r}"
-        torch.testing.assert_close(got.float(), want.float(), **TOL[dtype], msg=lambda m: f"rows per item {r}: {m}")
+        case = f"rows per item {r}, tiles {tiles} ({meta.num_prefill_tiles})"
+        assert torch.isfinite(got).all(), case
+        torch.testing.assert_close(got.float(), want.float(), **TOL[dtype], msg=lambda m: f"{case}: {m}")
     return got, want
 
 
@@ -311,7 +317,9 @@ def test_mixed_step_config4_append_attention_copy():
                          wl.num_heads, wl.num_kv_heads)
     rows = ops.rows_per_item(wl.dtype, wl.num_heads, wl.num_kv_heads)
     assert rows == 2
-    meta = _meta(wl.positions, wl.seq_slices, wl.block_tables, wl.context_lens, BS, wl.num_blocks, rows=rows)
+    meta = _meta(wl.positions, wl.seq_slices, wl.block_tables, wl.context_lens, BS, wl.num_blocks, rows=rows,
+                 tiles=True)
+    assert meta.num_prefill_tiles == 8 * 512 // 64            # one 1024-position partition each
     pool = wl.pool.to(DEV)
     ops.kv_append(pool, wl.k_new.to(DEV), wl.v_new.to(DEV), meta.slot_mapping)
     out = ops.paged_attention(wl.q.to(DEV), pool, meta, num_heads=wl.num_heads)
@@ -323,3 +331,46 @@ def test_mixed_step_config4_append_attention_copy():
     torch.cuda.synchronize()
     want_pool[wl.copy_dst] = want_pool[wl.copy_src]
     assert torch.equal(_bits(pool.cpu()), _bits(want_pool))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("Hq,Hkv,D", [(14, 2, 64), (32, 8, 128), (4, 4, 64)])
+def test_prefill_tiles_ragged_and_tails(dtype, Hq, Hkv, D):
+    """Tiles with partial last tiles (q_len not a multiple of 64), prefill tails
+    after a cached prefix (pos0 > 0, chunks straddling the diagonal), block
+    sizes other than 16 through the chunk walk, next to decode rows."""
+    for BS, seed in ((16, 21), (4, 22), (64, 23)):
+        c = _mixed_case(seed, Hq, Hkv, D, BS, dtype, qlens=[16, 1, 130, 64, 77, 1, 200],
+                        cached=[0, 300, 0, 5, 600, 17, 2000])
+        meta = _meta(c["pos"], c["slices"], c["tables"], c["ctx"], BS, c["NB"], tiles=True)
+        # one item per (tile of 64 rows, 1024-position partition its last row reaches)
+        assert meta.num_prefill_tiles == 1 + 3 + 1 + (1 + 1) + 4 * 3
+        _attention_vs_oracle(c, Hq, Hkv, dtype)
+
+
+def test_prefill_tiles_through_the_drop_in_cache():
+    """PagedKVCache.write + attention (16-bit pools use tiles for prefills)."""
+    Hq, Hkv, D, BS = 14, 2, 64, 16
+    c = _mixed_case(24, Hq, Hkv, D, BS, torch.bfloat16, qlens=[96, 1, 40], cached=[0, 70, 400])
+    cache = PagedKVCache(1, c["NB"], BS, Hkv, D, DEV, torch.bfloat16)
+    cache.pools[0].copy_(c["pool"])
+    pos = torch.tensor(c["pos"], device=DEV)
+    cache.write(0, c["k"].to(DEV), c["v"].to(DEV), pos, c["slices"], c["tables"])
+    out = cache.attention(0, c["q"].to(DEV), pos, c["slices"], c["tables"], c["ctx"])
+    torch.cuda.synchronize()
+    want_pool = c["pool"].clone()
+    ref.kv_write(want_pool, c["k"], c["v"], torch.tensor(c["pos"]), c["slices"], c["tables"], BS)
+    want = ref.attention(c["q"], want_pool, c["slices"], c["tables"], c["ctx"], Hq, Hkv)
+    assert cache.step_metadata(pos, c["slices"], c["tables"], c["ctx"], 2).num_prefill_tiles == 2 + 1
+    torch.testing.assert_close(out.cpu().float(), want.float(), **TOL[torch.bfloat16])
+
+
+def test_prefill_tiles_split_over_tile_partitions_bf16():
+    """A 1500-row prefill and a 300-row tail at positions 2000..2299: tile rows
+    reach several 1024-position partitions and merge through the combine pass."""
+    c = _mixed_case(25, 14, 2, 64, 16, torch.bfloat16, qlens=[1500, 1, 300], cached=[0, 3000, 2000])
+    meta = _meta(c["pos"], c["slices"], c["tables"], c["ctx"], 16, c["NB"], rows=2, tiles=True)
+    counts = np.diff(meta.row_part_off_np)
+    assert counts[1500] == 12                       # the decode row: 256-position partitions
+    assert counts[1501:].max() == 3 and counts[:1500].max() == 2   # tile rows: 1024-position ones
+    _attention_vs_oracle(c, 14, 2, torch.bfloat16)

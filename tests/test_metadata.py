@@ -3,7 +3,7 @@ import numpy as np
 import pytest
 import torch
 
-from tinybatch_amd.metadata import build_step_metadata
+from tinybatch_amd.metadata import TILE_PARTITION, TILE_ROWS, build_step_metadata
 
 
 def _mixed():
@@ -107,3 +107,58 @@ def test_row_groups_cover_each_row_partition_once():
     want = {(r, p) for r in range(t) for p in range(-(-int(m.row_ctx_np[r]) // 32))}
     assert set(seen) == want and all(v == 1 for v in seen.values())
     assert m.total_partitions == len(want)
+
+
+def test_prefill_tiles_cover_tiled_rows_most_positions_first():
+    # seq0: prefill 150 (tiles 64, 64, 22); seq1: decode; seq2: tail 20 of ctx 520; seq3: tail 8 (row groups)
+    q = [150, 1, 20, 8]
+    ctx = [150, 33, 520, 300]
+    positions, slices, t = [], [], 0
+    for n, c in zip(q, ctx):
+        positions += list(range(c - n, c))
+        slices.append((t, t + n)); t += n
+    need = [(c + 15) // 16 for c in ctx]
+    tables, at = [], 0
+    for n in need:
+        tables.append(list(range(at, at + n))); at += n
+    P, TP = 256, TILE_PARTITION
+    m = build_step_metadata(positions, slices, tables, ctx, block_size=16, num_blocks=at,
+                            partition_tokens=P, rows_per_item=2, tile_prefill=True)
+    items = [tuple(x) for x in m.prefill_tiles_np.tolist()]
+    want = [(0, 0, 64, 0), (64, 0, 64, 64), (128, 0, 22, 128), (151, 2, 20, 500)]
+    assert sorted(items) == sorted(want)
+    covered = [min(TP, p0 + (z & 0xFF) - (z >> 8) * TP) for _, _, z, p0 in items]
+    assert covered == sorted(covered, reverse=True)
+    tiled = {r for r0, _, z, _ in items for r in range(r0, r0 + (z & 0xFF))}
+    worked = {int(r) + i for r, _, z, _ in m.work_np.tolist() for i in range((z >> 24) + 1)}
+    assert tiled.isdisjoint(worked) and tiled | worked == set(range(t))
+    counts = np.diff(m.row_part_off_np)
+    for r in range(t):   # tile rows count tile partitions, work-item rows count P-position ones
+        assert counts[r] == -(-int(m.row_ctx_np[r]) // (TP if r in tiled else P))
+    assert m.total_partitions == int(counts.sum())
+    assert m.split_rows_np.tolist() == [r for r in range(t) if counts[r] > 1]
+    # fp32 metadata (no tiles) keeps every row in work items
+    m32 = build_step_metadata(positions, slices, tables, ctx, block_size=16, num_blocks=at,
+                              partition_tokens=P)
+    assert m32.num_prefill_tiles == 0 and m32.num_work_items == m32.total_partitions
+
+
+def test_tile_constants_match_the_header():
+    import os
+    import re
+    hdr = open(os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include",
+                            "tinybatch_amd.h")).read()
+    assert int(re.search(r"#define TB_PREFILL_TILE_ROWS (\d+)", hdr).group(1)) == TILE_ROWS
+    assert int(re.search(r"#define TB_PREFILL_TILE_PARTITION (\d+)", hdr).group(1)) == TILE_PARTITION
+
+
+def test_long_prefill_tiles_span_tile_partitions():
+    n = 2100
+    m = build_step_metadata(list(range(n)), [(0, n)], [list(range((n + 15) // 16))], [n], block_size=16,
+                            num_blocks=200, partition_tokens=256, rows_per_item=2, tile_prefill=True)
+    items = m.prefill_tiles_np.tolist()
+    ntiles = -(-n // TILE_ROWS)
+    want = sum(-(-min(n, 64 * (t + 1)) // TILE_PARTITION) for t in range(ntiles))
+    assert len(items) == want
+    assert m.max_parts_per_row == 3
+    assert m.split_rows_np.tolist() == [r for r in range(n) if r + 1 > TILE_PARTITION]

@@ -37,7 +37,9 @@ SIGNATURES = {
         c_vp, c_i64,            # out, out_row_stride
         c_vp, c_i32,            # block_tables, max_blocks_per_seq
         c_vp, c_i32,            # work_items, num_work_items
+        c_vp, c_i32,            # prefill_tiles, num_prefill_tiles
         c_vp, c_i32,            # row_part_offsets, num_rows
+        c_vp, c_i32,            # split_rows, num_split_rows
         c_i32, c_i32, c_i32,    # max_parts_per_row, partition_tokens, total_partitions
         c_i32, c_i32, c_i32, c_i32,  # num_heads, num_kv_heads, head_dim, block_size
         c_f32, c_i32,           # scale, dtype

@@ -25,6 +25,9 @@
 // The online softmax runs per 64-position chunk on the S^T tiles (max / sum
 // across the four 16-lane groups by shuffles); loads of chunk c+1 are in
 // flight while chunk c is computed.
+// Prefill tiles (fp16 / bf16): paged_prefill_mfma_kernel, a flash-style
+// workgroup per (64 query rows of one sequence, query head) that walks the
+// causal range in 64-position chunks staged in LDS (see the kernel).
 // fp32: paged_attn_valu_kernel, fp32 FMAs on the VALU (no fp32 MFMA of the
 // needed precision on CDNA4), same decomposition.
 // Positions >= the row's context are never loaded (stale slots may hold any
@@ -70,6 +73,8 @@ struct attn_args {
   int32_t max_nb;
   const int4* work;       // (row, seq, part, row_ctx)
   const int32_t* row_part_off;
+  const int4* tiles;      // prefill tiles (row0, seq, rows, pos0)
+  const int32_t* split_rows;
   float* ws_acc;          // [parts][Hq][D]
   float* ws_ml;           // [parts][Hq][2]
   int32_t num_heads;
@@ -523,48 +528,301 @@ void paged_attn_mfma_kernel(const attn_args a) {
 }
 
 // ---------------------------------------------------------------------------
-// Log-sum-exp merge of the partials of one (row, head): one wave, lane owns
-// output columns lane, lane + 64, ... Rows of a single partition exit.
+// Prefill tiles (16-bit). A workgroup of 4 waves owns up to 64 consecutive
+// query rows of one sequence (wave w: rows 16w .. 16w+15; lane column lc is
+// the row), one query head and one tile partition of PART_TILE positions (a
+// row longer than that leaves partials for the combine kernel, like a split
+// decode row). It walks its partition in chunks of 64 positions: each chunk's
+// K and V rows are loaded once per workgroup (coalesced 16-byte loads through
+// the block table) and staged in LDS for the four waves, K as rows and V
+// transposed (one LDS row per head dim); the next chunk's loads are in flight
+// while a chunk is computed.
+//   S^T[pos][row] = K[pos][:] . Q[row][:]         A = K rows (LDS), B = q (registers)
+//   O^T[dv][row] += V^T[dv][pos] . P^T[pos][row]  A = V^T rows (LDS, 8-byte reads),
+//                                                 B = P (the S^T registers, repacked)
+// Every operand a lane holds belongs to its own row, so the softmax state
+// stays in the lane; row max / sum reduce across the four 16-lane groups with
+// permlane swaps. The softmax is VALU-bound on CDNA (16-lane SIMDs), so per
+// score it costs one max, one FMA (scale and max folded) and one exp2; the
+// reference max m moves only when a row's max grows past m + 8, so p <= 2^8
+// and the accumulator rescale is rare (m, l and the accumulator always refer
+// to the same m, which is what the partials record). Only chunks that cross a
+// row's diagonal are masked. Row i (position pos0 + i) sees positions
+// 0 .. pos0 + i: the mask of model.py:139-146 for both the causal prefill and
+// a prefill tail.
+constexpr int PART_TILE = TB_PREFILL_TILE_PARTITION;   // positions per tile partition
+static_assert(TB_PREFILL_TILE_ROWS == 64, "four waves of 16 rows");
+
+template <int D>
+struct prefill_shape {
+  static constexpr int RB = 2 * D;             // bytes per K or V row
+  static constexpr int KS = D / 32;            // q.k k-slices
+  static constexpr int NSL = D / 16;           // O^T slices of 16 dims
+  static constexpr int RS = RB + 16;           // LDS row stride: 16-byte aligned, K-row and V-column reads conflict-free
+  static constexpr int CK = 64;                // positions per chunk
+  static constexpr int NCH = PART_TILE / CK;   // chunks per partition
+  static constexpr int VCOLS = RB / 16;        // 16-byte pieces of a row
+  static constexpr int LPT = CK * VCOLS / 256; // 16-byte loads per thread per chunk, of K and of V each
+  static constexpr int VTS = 2 * CK + 8;       // V^T row stride (bytes): 8-byte aligned rows
+  static constexpr int LDS = CK * RS + D * VTS;
+  static_assert(LPT >= 1 && (CK * VCOLS) % 256 == 0 && PART_TILE % CK == 0, "chunk split");
+};
+
 template <typename Tag, int D>
-__global__ __launch_bounds__(64) void combine_partials_kernel(const attn_args a) {
-  constexpr int EB = elem<Tag>::bytes;
-  __shared__ float w_lds[64];
-  const int row = blockIdx.x, head = blockIdx.y, lane = threadIdx.x;
-  const int pbeg = a.row_part_off[row];
-  const int n = a.row_part_off[row + 1] - pbeg;
-  if (n <= 1) return;
-  float M = -INFINITY;
-  for (int p = lane; p < n; p += 64) M = fmaxf(M, a.ws_ml[((int64_t)(pbeg + p) * a.num_heads + head) * 2]);
-  M = cross_group_max<1>(M);
-  float L = 0.f;
-  for (int p = lane; p < n; p += 64) {
-    const float2 ml = *reinterpret_cast<const float2*>(a.ws_ml + ((int64_t)(pbeg + p) * a.num_heads + head) * 2);
-    L = fmaf(ml.y, fast_exp2(ml.x - M), L);
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
+void paged_prefill_mfma_kernel(const attn_args a) {
+  using S = prefill_shape<D>;
+  using M = math<Tag>;
+  typedef typename M::vec8_t vec8_t;
+  typedef typename M::scalar_t scalar_t;
+  constexpr int RB = S::RB, KS = S::KS, NSL = S::NSL, RS = S::RS, CK = S::CK, NCH = S::NCH;
+  constexpr int VCOLS = S::VCOLS, LPT = S::LPT, VTS = S::VTS, EB = 2;
+  __shared__ __align__(16) char lds[S::LDS];
+  char* const k_lds = lds;
+  char* const vt_lds = lds + CK * RS;
+
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lc = lane & 15, lg = lane >> 4;
+  const int item = blockIdx.x / a.num_heads;
+  const int head = blockIdx.x - item * a.num_heads;
+  const int4 ti = a.tiles[item];
+  const int row0 = ti.x, seq = ti.y, nrows = ti.z & 0xFF, part = ti.z >> 8, pos0 = ti.w;
+  const int kvh = head / a.rep;
+  const int limit = pos0 + nrows;                  // positions the tile's last row sees
+  const int c0 = part * NCH;                       // first chunk of the partition
+  const int c_end = min(c0 + NCH, (limit + CK - 1) / CK);
+  const int my_row = 16 * wave + lc;               // tile-relative row of this lane
+  const int my_pos = pos0 + my_row;                // sees positions 0 .. my_pos
+  const int wave_first = pos0 + 16 * wave;         // smallest position a row of this wave has
+  const int wave_last = pos0 + min(nrows, 16 * wave + 16) - 1;
+  const bool wave_busy = 16 * wave < nrows;
+
+  const int bs = 1 << a.log2_bs;
+  const int64_t tile_bytes = (int64_t)bs * RB;
+  const int64_t blk_bytes = 2 * (int64_t)a.num_kv_heads * tile_bytes;
+  const int64_t v_off = (int64_t)a.num_kv_heads * tile_bytes;
+  const char* const pool_kvh = a.pool + kvh * tile_bytes;
+  const int32_t* const table = a.block_tables + (int64_t)seq * a.max_nb;
+
+  // the row's partition count decides between final output and a partial slot
+  int pbeg = 0, nparts = 0;
+  if (my_row < nrows) {
+    pbeg = a.row_part_off[row0 + my_row];
+    nparts = a.row_part_off[row0 + my_row + 1] - pbeg;
   }
-  L = cross_group_sum<1>(L);
-  const float invL = 1.f / L;
-  float o[D / 64];
+
+  // Thread t, load i: row (t + 256 i) / VCOLS of the chunk, 16-byte piece (t + 256 i) % VCOLS.
+  auto load_ids = [&](int c, int (&ids)[LPT]) {
 #pragma unroll
-  for (int k = 0; k < D / 64; ++k) o[k] = 0.f;
-  for (int p0 = 0; p0 < n; p0 += 64) {
-    const int cnt = min(64, n - p0);
-    __syncthreads();
-    if (lane < cnt) w_lds[lane] = fast_exp2(a.ws_ml[((int64_t)(pbeg + p0 + lane) * a.num_heads + head) * 2] - M);
-    __syncthreads();
-#pragma unroll 8
-    for (int p = 0; p < cnt; ++p) {
-      const float w = w_lds[p];
-      const float* src = a.ws_acc + ((int64_t)(pbeg + p0 + p) * a.num_heads + head) * D + lane;
+    for (int i = 0; i < LPT; ++i) {
+      const int p = c * CK + (threadIdx.x + 256 * i) / VCOLS;
+      int b = -1;
+      if (c < c_end && p < limit) {
+        b = table[p >> a.log2_bs];
+        if (b < 0 || b >= a.num_blocks) b = 0;   // host validates; stay inside the pool
+      }
+      ids[i] = b;
+    }
+  };
+  auto load_kv = [&](int c, const int (&ids)[LPT], vec16 (&kr)[LPT], vec16 (&vr)[LPT]) {
 #pragma unroll
-      for (int k = 0; k < D / 64; ++k) o[k] = fmaf(src[64 * k], w, o[k]);
+    for (int i = 0; i < LPT; ++i) {
+      const int f = threadIdx.x + 256 * i;
+      const int p = c * CK + f / VCOLS;
+      if (ids[i] >= 0) {
+        const int64_t off = (int64_t)ids[i] * blk_bytes + (int64_t)(p & (bs - 1)) * RB + 16 * (f % VCOLS);
+        kr[i] = ld16(pool_kvh + off);
+        vr[i] = ld16(pool_kvh + v_off + off);
+      } else {
+        kr[i] = zero16();   // positions past the tile's range: zero K and V
+        vr[i] = zero16();
+      }
+    }
+  };
+
+  vec16 qb[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) qb[s] = zero16();
+  if (my_row < nrows) {
+    const char* qrow = a.q + (row0 + my_row) * a.q_row_bytes + (int64_t)head * RB + 16 * lg;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qb[s] = ld16(qrow + 64 * s);
+  }
+
+  float m = -INFINITY;       // reference max of row lc (scaled, base-2 domain)
+  float l_part = 0.f;        // this lane's share of row lc's sum, relative to m
+  float4_t acc[NSL];         // O^T[16n + 4lg + j][row lc], relative to m
+#pragma unroll
+  for (int nn = 0; nn < NSL; ++nn) acc[nn] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  // stage one chunk (already in registers) in LDS
+  auto stage = [&](const vec16 (&kr)[LPT], const vec16 (&vr)[LPT]) {
+    __syncthreads();   // the previous chunk's LDS reads are done
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      const int f = threadIdx.x + 256 * i;
+      const int r = f / VCOLS, d0 = 8 * (f % VCOLS);
+      st16(k_lds + r * RS + 2 * d0, kr[i]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e)   // V^T[d0 + e][r]
+        *reinterpret_cast<uint16_t*>(vt_lds + (d0 + e) * VTS + 2 * r) = (uint16_t)(vr[i].w[e >> 1] >> (16 * (e & 1)));
+    }
+    __syncthreads();   // chunk staged
+  };
+  // fold the staged chunk c into the row state
+  auto compute = [&](int c) {
+    const int cb = c * CK;
+    if (!(wave_busy && cb <= wave_last)) return;
+    float4_t sc[4];   // S^T (raw): lane holds positions cb + 16t + 4lg + j of row lc
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      sc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+      const char* krow = k_lds + (16 * t + lc) * RS + 16 * lg;
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+        sc[t] = M::mfma(__builtin_bit_cast(vec8_t, ld16(krow + 64 * s)), __builtin_bit_cast(vec8_t, qb[s]), sc[t]);
+    }
+    if (cb + CK - 1 > wave_first) {   // the chunk crosses the diagonal of some row of this wave
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (cb + 16 * t + 4 * lg + j > my_pos) sc[t][j] = -INFINITY;
+    }
+    float cm = fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3]));
+#pragma unroll
+    for (int t = 1; t < 4; ++t) cm = fmaxf(cm, fmaxf(fmaxf(sc[t][0], sc[t][1]), fmaxf(sc[t][2], sc[t][3])));
+    cm = max_xor32(max_xor16(cm)) * a.scale_log2e;   // the row's chunk max, scaled (-inf if all masked)
+    if (__any(cm > m + 8.f)) {   // some row outgrew its reference: move every row's reference up
+      const float m_new = fmaxf(m, cm);
+      const float alpha = fast_exp2(m - (m_new == -INFINITY ? 0.f : m_new));   // 0 while m = -inf
+      m = m_new;
+      l_part *= alpha;
+#pragma unroll
+      for (int nn = 0; nn < NSL; ++nn) acc[nn] *= alpha;
+    }
+    const float neg_m = m == -INFINITY ? 0.f : -m;   // a row that has seen nothing keeps p = 0
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        sc[t][j] = fast_exp2(fmaf(sc[t][j], a.scale_log2e, neg_m));
+        l_part += sc[t][j];
+      }
+    // k index 8lg+j <-> position 32u + 4lg + j (j < 4) or 32u + 16 + 4lg + (j-4)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      vec8_t pb;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        pb[j] = (scalar_t)sc[2 * u][j];
+        pb[4 + j] = (scalar_t)sc[2 * u + 1][j];
+      }
+      const char* vrow = vt_lds + lc * VTS + 2 * (32 * u + 4 * lg);
+#pragma unroll
+      for (int nn = 0; nn < NSL; ++nn) {
+        const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 16 * nn * VTS);
+        const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16 * nn * VTS + 32);
+        vec16 va;
+        va.w[0] = lo.x; va.w[1] = lo.y; va.w[2] = hi.x; va.w[3] = hi.y;
+        acc[nn] = M::mfma(__builtin_bit_cast(vec8_t, va), pb, acc[nn]);
+      }
+    }
+  };
+
+  int ids[LPT];
+  vec16 kr[LPT], vr[LPT];
+  load_ids(c0, ids);
+  load_kv(c0, ids, kr, vr);
+  load_ids(c0 + 1, ids);
+  for (int c = c0; c < c_end; ++c) {   // workgroup-uniform trip count
+    stage(kr, vr);
+    if (c + 1 < c_end) {   // the next chunk's loads are in flight during the compute
+      load_kv(c + 1, ids, kr, vr);
+      load_ids(c + 2, ids);
+    }
+    compute(c);
+  }
+
+  const float l = sum_xor32(sum_xor16(l_part));
+  if (my_row < nrows && part < nparts) {   // rows that end before this partition own no slot here
+    const int row = row0 + my_row;
+    if (nparts == 1) {           // the whole row: final output
+      const float inv = 1.f / l;
+      char* orow = a.out + row * a.out_row_bytes + (int64_t)head * D * EB;
+#pragma unroll
+      for (int nn = 0; nn < NSL; ++nn) {
+        typedef scalar_t s4_t __attribute__((ext_vector_type(4)));
+        s4_t o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = (scalar_t)(acc[nn][j] * inv);
+        *reinterpret_cast<s4_t*>(orow + (16 * nn + 4 * lg) * EB) = o;
+      }
+    } else {                     // partial of a split row
+      const int64_t pidx = pbeg + part;
+      float* dst = a.ws_acc + (pidx * a.num_heads + head) * D;
+#pragma unroll
+      for (int nn = 0; nn < NSL; ++nn) *reinterpret_cast<float4_t*>(dst + 16 * nn + 4 * lg) = acc[nn];
+      if (lg == 0) *reinterpret_cast<float2*>(a.ws_ml + (pidx * a.num_heads + head) * 2) = make_float2(m, l);
     }
   }
-  char* orow = a.out + row * a.out_row_bytes + (int64_t)head * D * EB;
+}
+
+// ---------------------------------------------------------------------------
+// Log-sum-exp merge of the partials of one split row, all heads: one
+// workgroup of 256 threads, thread t owns 4 consecutive output dims (head
+// (t + 256 k) / (D/4)); every partial of the row is read once, in parallel.
+template <typename Tag, int D>
+__global__ __launch_bounds__(256) void combine_partials_kernel(const attn_args a) {
+  constexpr int EB = elem<Tag>::bytes;
+  constexpr int QPH = D / 4;                       // float4 columns per head
+  const int row = a.split_rows[blockIdx.x];
+  const int pbeg = a.row_part_off[row];
+  const int n = a.row_part_off[row + 1] - pbeg;
+  char* orow = a.out + row * a.out_row_bytes;
+  for (int col = threadIdx.x; col < a.num_heads * QPH; col += 256) {
+    const int head = col / QPH, d4 = col - head * QPH;
+    // batches of 8 partials, all loads of a batch in flight, merged online
+    float M = -INFINITY, L = 0.f;
+    float4_t o = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int p0 = 0; p0 < n; p0 += 8) {
+      float2 ml[8];
+      float4_t av[8];
 #pragma unroll
-  for (int k = 0; k < D / 64; ++k) {
-    const float v = o[k] * invL;
-    if constexpr (EB == 4) reinterpret_cast<float*>(orow)[lane + 64 * k] = v;
-    else reinterpret_cast<typename elem<Tag>::type*>(orow)[lane + 64 * k] = (typename elem<Tag>::type)v;
+      for (int k = 0; k < 8; ++k) {
+        if (p0 + k < n) {
+          const int64_t slot = (int64_t)(pbeg + p0 + k) * a.num_heads + head;
+          ml[k] = *reinterpret_cast<const float2*>(a.ws_ml + slot * 2);
+          av[k] = *reinterpret_cast<const float4_t*>(a.ws_acc + slot * D + 4 * d4);
+        } else {
+          ml[k] = make_float2(-INFINITY, 0.f);
+          av[k] = float4_t{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+      float mb = M;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) mb = fmaxf(mb, ml[k].x);   // finite: every partial saw a position
+      const float keep = fast_exp2(M - mb);                    // 0 while M = -inf
+      L *= keep;
+      o *= keep;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float w = ml[k].y > 0.f ? fast_exp2(ml[k].x - mb) : 0.f;
+        L = fmaf(ml[k].y, w, L);
+        o += av[k] * w;
+      }
+      M = mb;
+    }
+    const float inv = 1.f / L;
+    if constexpr (EB == 4) {
+      *reinterpret_cast<float4_t*>(orow + ((int64_t)head * D + 4 * d4) * 4) = o * inv;
+    } else {
+      typedef typename elem<Tag>::type s_t;
+      typedef s_t s4_t __attribute__((ext_vector_type(4)));
+      s4_t r;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) r[j] = (s_t)(o[j] * inv);
+      *reinterpret_cast<s4_t*>(orow + ((int64_t)head * D + 4 * d4) * EB) = r;
+    }
   }
 }
 
@@ -597,8 +855,29 @@ static void launch_mfma(const attn_args& a, int num_work, hipStream_t stream) {
 }
 
 template <typename Tag, int D>
-static void launch_combine(const attn_args& a, int num_rows, hipStream_t stream) {
-  hipLaunchKernelGGL((combine_partials_kernel<Tag, D>), dim3(num_rows, a.num_heads), dim3(64), 0, stream, a);
+static void launch_combine(const attn_args& a, int num_split_rows, hipStream_t stream) {
+  if (num_split_rows > 0)
+    hipLaunchKernelGGL((combine_partials_kernel<Tag, D>), dim3(num_split_rows), dim3(256), 0, stream, a);
+}
+
+template <typename Tag, int D>
+static void launch_prefill(const attn_args& a, int num_tiles, hipStream_t stream) {
+  if (num_tiles > 0)
+    hipLaunchKernelGGL((paged_prefill_mfma_kernel<Tag, D>), dim3(num_tiles * a.num_heads), dim3(256), 0, stream, a);
+}
+
+template <typename Tag>
+static void launch_16bit(const attn_args& a, bool d64, int num_work, int num_tiles, int num_split_rows,
+                         hipStream_t stream) {
+  if (d64) {
+    if (num_work > 0) launch_mfma<Tag, 64>(a, num_work, stream);
+    launch_prefill<Tag, 64>(a, num_tiles, stream);
+    launch_combine<Tag, 64>(a, num_split_rows, stream);
+  } else {
+    if (num_work > 0) launch_mfma<Tag, 128>(a, num_work, stream);
+    launch_prefill<Tag, 128>(a, num_tiles, stream);
+    launch_combine<Tag, 128>(a, num_split_rows, stream);
+  }
 }
 
 static int largest_divisor_upto(int rep, int cap) {
@@ -637,7 +916,9 @@ extern "C" int32_t tb_paged_attention(const void* q, int64_t q_row_stride, void*
                                       int64_t num_blocks, void* out, int64_t out_row_stride,
                                       const int32_t* block_tables, int32_t max_blocks_per_seq,
                                       const int32_t* work_items, int32_t num_work_items,
+                                      const int32_t* prefill_tiles, int32_t num_prefill_tiles,
                                       const int32_t* row_part_offsets, int32_t num_rows,
+                                      const int32_t* split_rows, int32_t num_split_rows,
                                       int32_t max_parts_per_row, int32_t partition_tokens,
                                       int32_t total_partitions, int32_t num_heads,
                                       int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
@@ -652,22 +933,27 @@ extern "C" int32_t tb_paged_attention(const void* q, int64_t q_row_stride, void*
   TB_CHECK_ARG(block_size >= 4 && (block_size & (block_size - 1)) == 0);
   int log2_bs = 0;
   while ((1 << log2_bs) < block_size) ++log2_bs;
-  TB_CHECK_ARG(num_rows >= 0 && num_work_items >= 0 && max_blocks_per_seq > 0 && num_blocks > 0);
+  TB_CHECK_ARG(num_rows >= 0 && num_work_items >= 0 && num_prefill_tiles >= 0 && num_split_rows >= 0);
+  TB_CHECK_ARG(max_blocks_per_seq > 0 && num_blocks > 0);
   TB_CHECK_ARG(partition_ok(dtype, head_dim, block_size, partition_tokens));
   TB_CHECK_ARG(q_row_stride >= (int64_t)num_heads * head_dim);
   TB_CHECK_ARG(out_row_stride >= (int64_t)num_heads * head_dim);
-  if (num_work_items == 0) return TB_OK;
-  TB_CHECK_ARG(q && pool && out && block_tables && work_items && row_part_offsets);
+  if (num_prefill_tiles > 0 && eb != 2) return TB_ERR_UNSUPPORTED;   // fp32 rows go to work items
+  if (num_work_items == 0 && num_prefill_tiles == 0) return TB_OK;
+  TB_CHECK_ARG(q && pool && out && block_tables && num_rows > 0);
+  TB_CHECK_ARG(num_work_items == 0 || (work_items && row_part_offsets));
+  TB_CHECK_ARG(num_prefill_tiles == 0 || prefill_tiles);
   TB_CHECK_ARG((((uintptr_t)q | (uintptr_t)pool | (uintptr_t)out) & 15u) == 0);
   TB_CHECK_ARG((q_row_stride * eb) % 16 == 0 && (out_row_stride * eb) % 16 == 0);
-  TB_CHECK_ARG(max_parts_per_row >= 1 && total_partitions >= num_work_items && num_rows > 0);
+  TB_CHECK_ARG(max_parts_per_row >= (num_work_items > 0 ? 1 : 0) && total_partitions >= num_work_items);
+  TB_CHECK_ARG(num_split_rows <= num_rows && (num_split_rows == 0 || (split_rows && max_parts_per_row > 1)));
   if (max_parts_per_row > 1) {
     TB_CHECK_ARG(workspace != nullptr);
     TB_CHECK_ARG(workspace_bytes >= tb_paged_attention_workspace_bytes(total_partitions, num_heads, head_dim));
     TB_CHECK_ARG(((uintptr_t)workspace & 15u) == 0);
   }
   if (k_new || v_new) {
-    TB_CHECK_ARG(k_new && v_new);
+    TB_CHECK_ARG(k_new && v_new && num_prefill_tiles == 0);
     TB_CHECK_ARG(k_row_stride >= (int64_t)num_kv_heads * head_dim && v_row_stride >= (int64_t)num_kv_heads * head_dim);
     TB_CHECK_ARG((((uintptr_t)k_new | (uintptr_t)v_new) & 15u) == 0);
     TB_CHECK_ARG((k_row_stride * eb) % 16 == 0 && (v_row_stride * eb) % 16 == 0);
@@ -689,6 +975,8 @@ extern "C" int32_t tb_paged_attention(const void* q, int64_t q_row_stride, void*
   a.max_nb = max_blocks_per_seq;
   a.work = reinterpret_cast<const int4*>(work_items);
   a.row_part_off = row_part_offsets;
+  a.tiles = reinterpret_cast<const int4*>(prefill_tiles);
+  a.split_rows = split_rows;
   // workspace: [acc partials: parts x Hq x D][max/sum partials: parts x Hq x 2]
   a.ws_acc = (float*)workspace;
   a.ws_ml = workspace ? a.ws_acc + (size_t)total_partitions * num_heads * head_dim : nullptr;
@@ -709,18 +997,14 @@ extern "C" int32_t tb_paged_attention(const void* q, int64_t q_row_stride, void*
   switch (dtype) {
     case TB_DTYPE_F32:
       st = d64 ? dispatch_valu_rep<64>(a, num_work_items, stream) : dispatch_valu_rep<128>(a, num_work_items, stream);
-      if (st == TB_OK && max_parts_per_row > 1)
-        d64 ? launch_combine<f32_t, 64>(a, num_rows, stream) : launch_combine<f32_t, 128>(a, num_rows, stream);
+      if (st == TB_OK)
+        d64 ? launch_combine<f32_t, 64>(a, num_split_rows, stream) : launch_combine<f32_t, 128>(a, num_split_rows, stream);
       break;
     case TB_DTYPE_F16:
-      d64 ? launch_mfma<f16_t, 64>(a, num_work_items, stream) : launch_mfma<f16_t, 128>(a, num_work_items, stream);
-      if (max_parts_per_row > 1)
-        d64 ? launch_combine<f16_t, 64>(a, num_rows, stream) : launch_combine<f16_t, 128>(a, num_rows, stream);
+      launch_16bit<f16_t>(a, d64, num_work_items, num_prefill_tiles, num_split_rows, stream);
       break;
     case TB_DTYPE_BF16:
-      d64 ? launch_mfma<bf16_t, 64>(a, num_work_items, stream) : launch_mfma<bf16_t, 128>(a, num_work_items, stream);
-      if (max_parts_per_row > 1)
-        d64 ? launch_combine<bf16_t, 64>(a, num_rows, stream) : launch_combine<bf16_t, 128>(a, num_rows, stream);
+      launch_16bit<bf16_t>(a, d64, num_work_items, num_prefill_tiles, num_split_rows, stream);
       break;
     default: return TB_ERR_INVALID_ARG;
   }

@@ -70,9 +70,12 @@ class PagedKVCache:
                     and e["tables"] == block_tables
                     and (context_lens is None or (e["ctx"] == context_lens and e["rows"] == rows_per_item))):
                 return e["meta"]
+        # 16-bit pools serve long runs of new rows (prefills) with the tile kernel
+        tile = self.pools[0].dtype in (torch.float16, torch.bfloat16)
         meta = build_step_metadata(positions, seq_slices, block_tables, context_lens,
                                    block_size=self.block_size, num_blocks=self.num_blocks,
-                                   partition_tokens=self.partition_tokens, rows_per_item=rows_per_item)
+                                   partition_tokens=self.partition_tokens, rows_per_item=rows_per_item,
+                                   tile_prefill=tile)
         meta.to(self.device)
         entry = {"pos": pos_key, "slices": [tuple(x) for x in seq_slices],
                  "tables": [list(t) for t in block_tables],

@@ -19,6 +19,16 @@ step and uploaded in a single host-to-device copy:
   positions query row i may see (the mask rule j <= ctx - q_len + i of
   model.py:139-145) and the group's later rows see one more position each.
 * ``row_part_off[T + 1]`` - running count of partitions per row.
+* ``split_rows[S]`` - rows whose work spans more than one partition (their
+  partials are merged by the combine pass).
+* ``prefill_tiles[N, 4]`` - (row0, seq, rows | partition << 8, pos0) when
+  ``tile_prefill``: sequences with many new rows (full prefills and long
+  prefill tails) are cut into tiles of up to TILE_ROWS consecutive rows (row0
+  at position pos0), one item per tile and TILE_PARTITION-position partition
+  its last row reaches; the prefill kernel serves them and their rows get no
+  work items. A tile row counts ceil(row_ctx / TILE_PARTITION) partitions in
+  row_part_off (a split tile row leaves partials like any split row). Items
+  are ordered by the positions they cover, most first.
 
 Errors mirror the reference: a table too short for a position raises
 IndexError (kv_cache.py:35), a block id outside the pool raises IndexError
@@ -44,23 +54,29 @@ class StepMetadata:
     max_parts_per_row: int
     decode_only: bool            # every sequence has exactly one query row
     rows_per_item: int
+    num_prefill_tiles: int
+    num_split_rows: int
     # host copies
     slot_mapping_np: np.ndarray
     block_tables_np: np.ndarray
     work_np: np.ndarray
     row_part_off_np: np.ndarray
     row_ctx_np: np.ndarray       # [T] visible positions per row (0 for rows outside slices)
+    prefill_tiles_np: np.ndarray  # [N, 4]
+    split_rows_np: np.ndarray     # [S]
     # device views (int32, one backing buffer)
     device_buffer: torch.Tensor | None = None
     slot_mapping: torch.Tensor | None = None
     block_tables: torch.Tensor | None = None
     work: torch.Tensor | None = None
     row_part_off: torch.Tensor | None = None
+    prefill_tiles: torch.Tensor | None = None
+    split_rows: torch.Tensor | None = None
 
     def to(self, device: torch.device) -> "StepMetadata":
         """Upload every array with one host-to-device copy (views into one buffer)."""
         parts = [self.slot_mapping_np, self.block_tables_np.reshape(-1), self.work_np.reshape(-1),
-                 self.row_part_off_np]
+                 self.row_part_off_np, self.prefill_tiles_np.reshape(-1), self.split_rows_np]
         sizes = [_pad4(p.size) for p in parts]
         host = np.zeros(sum(sizes), dtype=np.int32)
         offs = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
@@ -75,7 +91,23 @@ class StepMetadata:
         self.block_tables = buf.narrow(0, int(offs[1]), parts[1].size).view(-1, self.max_blocks_per_seq)
         self.work = buf.narrow(0, int(offs[2]), parts[2].size).view(-1, 4)
         self.row_part_off = buf.narrow(0, int(offs[3]), parts[3].size)
+        self.prefill_tiles = buf.narrow(0, int(offs[4]), parts[4].size).view(-1, 4)
+        self.split_rows = buf.narrow(0, int(offs[5]), parts[5].size)
         return self
+
+
+# The prefill kernel's tile shape (TB_PREFILL_TILE_ROWS / TB_PREFILL_TILE_PARTITION
+# in include/tinybatch_amd.h): query rows per tile, positions per tile partition.
+TILE_ROWS = 64
+TILE_PARTITION = 1024
+
+
+def tiles_sequence(q_len: int, ctx: int, min_rows: int = 16, max_ctx: int = 4096) -> bool:
+    """Whether a sequence's rows go to prefill tiles: many new rows, and a context
+    short enough (or a tail long enough) that one workgroup's serial walk over it
+    is not the critical path. Short tails of long contexts stay with the split
+    row groups, which spread the context over partitions."""
+    return q_len >= min_rows and (ctx <= max_ctx or ctx <= 16 * q_len)
 
 
 def _pad4(n: int) -> int:
@@ -90,7 +122,8 @@ def _host_positions(positions) -> np.ndarray:
 
 def build_step_metadata(positions, seq_slices, block_tables, context_lens, *, block_size: int,
                         num_blocks: int, partition_tokens: int, num_tokens: int | None = None,
-                        validate_attention: bool = True, rows_per_item: int = 1) -> StepMetadata:
+                        validate_attention: bool = True, rows_per_item: int = 1,
+                        tile_prefill: bool = False) -> StepMetadata:
     """Build the per-step arrays (host side). See the module docstring."""
     if block_size <= 0 or block_size & (block_size - 1):
         raise ValueError(f"block_size must be a power of two, got {block_size}")
@@ -153,6 +186,8 @@ def build_step_metadata(positions, seq_slices, block_tables, context_lens, *, bl
     # ---- attention work items ----
     P = int(partition_tokens)
     row_ctx_by_row = np.zeros(T, dtype=np.int64)
+    tiles: list[tuple[int, int, int, int, int]] = []
+    tiled = np.zeros(T, dtype=bool)
     nparts_by_row = np.zeros(T, dtype=np.int64)
     if tot and context_lens is not None:
         ctx = np.asarray(context_lens, dtype=np.int64)
@@ -169,6 +204,21 @@ def build_step_metadata(positions, seq_slices, block_tables, context_lens, *, bl
         row_ctx = np.repeat(ctx - qlens, qlens) + row_i + 1
         row_ctx_by_row[row_ids] = row_ctx
         nparts_by_row[row_ids] = (row_ctx + P - 1) // P
+        if tile_prefill:
+            for b in range(B):
+                n, c = int(qlens[b]), int(ctx[b])
+                if n and tiles_sequence(n, c):
+                    s0 = int(starts[b])
+                    tiled[s0:s0 + n] = True               # served by tiles, not work items
+                    rc = row_ctx_by_row[s0:s0 + n]
+                    nparts_by_row[s0:s0 + n] = (rc + TILE_PARTITION - 1) // TILE_PARTITION
+                    for r in range(0, n, TILE_ROWS):
+                        rows = min(TILE_ROWS, n - r)
+                        pos0 = c - n + r
+                        end = pos0 + rows                 # positions the tile's last row sees
+                        for part in range((end + TILE_PARTITION - 1) // TILE_PARTITION):
+                            tiles.append((s0 + r, b, rows | (part << 8), pos0,
+                                          min(TILE_PARTITION, end - part * TILE_PARTITION)))
     row_part_off = np.zeros(T + 1, dtype=np.int64)
     np.cumsum(nparts_by_row, out=row_part_off[1:])
     if not 1 <= rows_per_item <= 16:
@@ -192,7 +242,7 @@ def build_step_metadata(positions, seq_slices, block_tables, context_lens, *, bl
         grp_row = np.asarray(starts_l, dtype=np.int64)
         grp_len = np.asarray(lens_l, dtype=np.int64)
     grp_parts = nparts_by_row[grp_row] if tot else np.zeros(0, np.int64)
-    keep = grp_parts > 0
+    keep = (grp_parts > 0) & ~tiled[grp_row] if tot else grp_parts > 0
     grp_row, grp_len, grp_parts = grp_row[keep], grp_len[keep], grp_parts[keep]
     W = int(grp_parts.sum())
     work = np.zeros((W, 4), dtype=np.int64)
@@ -208,6 +258,9 @@ def build_step_metadata(positions, seq_slices, block_tables, context_lens, *, bl
         work[:, 3] = row_ctx_by_row[rep_rows]
     if max(T, W, max_nb, total_parts) >= 2**24 - 1:
         raise ValueError("step too large for int32 metadata")
+    tiles.sort(key=lambda t: -t[4])                   # most positions first (stable)
+    tiles_np = np.asarray([t[:4] for t in tiles], dtype=np.int64).reshape(-1, 4)
+    split_rows = np.nonzero(nparts_by_row > 1)[0]
 
     return StepMetadata(
         num_tokens=T, num_seqs=B, block_size=block_size, partition_tokens=P,
@@ -215,9 +268,13 @@ def build_step_metadata(positions, seq_slices, block_tables, context_lens, *, bl
         max_parts_per_row=int(nparts_by_row.max()) if T else 0,
         decode_only=bool(B) and bool(np.all(qlens == 1)),
         rows_per_item=int(rows_per_item),
+        num_prefill_tiles=int(tiles_np.shape[0]),
+        num_split_rows=int(split_rows.size),
         slot_mapping_np=slots.astype(np.int32),
         block_tables_np=tables[:max(B, 1)].astype(np.int32),
         work_np=work.astype(np.int32),
         row_part_off_np=row_part_off.astype(np.int32),
         row_ctx_np=row_ctx_by_row.astype(np.int32),
+        prefill_tiles_np=tiles_np.astype(np.int32),
+        split_rows_np=split_rows.astype(np.int32),
     )

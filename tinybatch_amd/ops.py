@@ -155,6 +155,8 @@ def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, 
     os_ = _rows_view("out", out, num_heads, d)
     if meta.work is None:
         raise ValueError("metadata has not been uploaded (call meta.to(device))")
+    if meta.num_prefill_tiles and q.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("prefill tiles need fp16/bf16; build fp32 metadata with tile_prefill=False")
     if meta.rows_per_item > rows_per_item(q.dtype, num_heads, hkv):
         raise ValueError(f"metadata groups {meta.rows_per_item} rows per item; this geometry allows "
                          f"{rows_per_item(q.dtype, num_heads, hkv)}")
@@ -165,7 +167,7 @@ def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, 
     if k_new is not None or v_new is not None:
         if k_new is None or v_new is None:
             raise ValueError("k_new and v_new go together")
-        if not meta.decode_only:
+        if not meta.decode_only or meta.num_prefill_tiles:
             raise ValueError("fused append needs a decode-only step (one query row per sequence)")
         for name, t in (("k_new", k_new), ("v_new", v_new)):
             _lib.require_gpu_tensor(name, t)
@@ -182,7 +184,9 @@ def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, 
         q.data_ptr(), qs, pool.data_ptr(), nb, out.data_ptr(), os_,
         meta.block_tables.data_ptr(), meta.max_blocks_per_seq,
         meta.work.data_ptr(), meta.num_work_items,
+        meta.prefill_tiles.data_ptr(), meta.num_prefill_tiles,
         meta.row_part_off.data_ptr(), T,
+        meta.split_rows.data_ptr(), meta.num_split_rows,
         max(meta.max_parts_per_row, 1), meta.partition_tokens, meta.total_partitions,
         num_heads, hkv, d, bs, float(scale), _lib.DTYPE_CODE[q.dtype],
         ksp, ks, vsp, vs, _ptr(ws), ws_bytes, _lib.stream_handle(q.device))
