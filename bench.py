@@ -221,6 +221,73 @@ def bench_mixed(args, dev) -> int:
     return 0
 
 
+def bench_e2e(args, dev) -> int:
+    """Continuous batching of 32 random-token requests on a random-init Qwen2 at
+    0.5B dimensions (bf16), 75% sharing a 400-token prefix, greedy outputs of
+    U{16..256} tokens, everything submitted at t = 0. Reports output tokens per
+    second of wall time, decode-only-step token rate, and TTFT mean / p99."""
+    import statistics
+
+    import torch
+
+    from tinybatch_amd.config import EngineConfig
+    from tinybatch_amd.engine import LLMEngine
+    from tinybatch_amd.model import ModelConfig, Qwen2Paged
+    from tinybatch_amd.workloads import make_serving_workload
+
+    mc = ModelConfig.qwen2_0_5b()
+    ecfg = EngineConfig(num_blocks=4096, block_size=16, max_batch_tokens=2048, max_running=32, seed=0)
+    t0 = time.perf_counter()
+    model = Qwen2Paged(mc, dev, torch.bfloat16, seed=0)
+    torch.cuda.synchronize()
+    _log(f"model {mc.num_params()} params ({time.perf_counter() - t0:.1f}s)")
+    wl = make_serving_workload()
+
+    def run(prompts, outs):
+        eng = LLMEngine(ecfg, model=model)
+        torch.cuda.synchronize()
+        start = time.perf_counter()
+        reqs = [eng.add_request(p, max_new_tokens=m) for p, m in zip(prompts, outs)]
+        for r in reqs:
+            r.arrival_time = start
+        dec_time = dec_tokens = 0.0
+        while eng.scheduler.has_work():
+            ts = time.perf_counter()
+            outs_ = eng.step()
+            dt = time.perf_counter() - ts
+            if outs_ and eng.last_step_prefills == 0:   # decode-only step
+                dec_time += dt
+                dec_tokens += len(outs_)
+        wall = time.perf_counter() - start
+        return eng, reqs, wall, dec_tokens, dec_time
+
+    for _ in range(max(args.warmup, 1)):           # untimed: kernels, GEMM heuristics, allocator
+        run(wl.prompts[:4], [8] * 4)
+    eng, reqs, wall, dec_tokens, dec_time = run(wl.prompts, wl.max_new_tokens)
+    out_tokens = sum(len(r.output_token_ids) for r in reqs)
+    ttft = sorted(r.first_token_time - r.arrival_time for r in reqs)
+    line = {
+        "metric": "e2e decode tok/s (continuous batching, random-init Qwen2 0.5B dims)",
+        "value": round(out_tokens / wall, 1), "unit": "tok/s", "n_gpus": 1, "steps": eng.steps, "warmup": args.warmup,
+        "ms_per_step": round(wall / max(eng.steps, 1) * 1e3, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random token ids; seeded random-init weights; 24/32 requests share a 400-token prefix)",
+        "config": {"workload": f"{wl.name}: 32 requests, prompts U{{32..512}} (sharing ones U{{401..512}}), "
+                               f"outputs U{{16..256}}, greedy", "params": mc.num_params(), "layers": mc.n_layers,
+                   "num_blocks": ecfg.num_blocks, "max_batch_tokens": ecfg.max_batch_tokens,
+                   "max_running": ecfg.max_running, "rope_theta": mc.rope_theta, "rms_eps": mc.rms_eps},
+        "output_tokens": out_tokens, "wall_s": round(wall, 4),
+        "decode_only_tok_s": round(dec_tokens / dec_time, 1) if dec_time else None,
+        "ttft_mean_ms": round(statistics.mean(ttft) * 1e3, 2),
+        "ttft_p99_ms": round(ttft[int(0.99 * (len(ttft) - 1))] * 1e3, 2),
+        "prefix_hit_rate": round(eng.block_manager.hit_rate(), 3),
+        "preemptions": sum(r.preemptions for r in reqs),
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -271,6 +338,8 @@ def main() -> int:
 
     if args.workload == "qwen-bf16-mixed":
         return bench_mixed(args, dev)
+    if args.workload == "qwen2-0.5b-e2e":
+        return bench_e2e(args, dev)
 
     big = args.workload == "llama-bf16-b256"
     t0 = time.perf_counter()

@@ -1,0 +1,114 @@
+"""The engine on the GPU against the oracle: model forward logits, and whole
+continuous-batching runs (prefix hits, block-multiple prompts, mixed steps)
+token for token against the same schedule driven through the CPU restatement."""
+import pytest
+import torch
+
+from oracle import model_reference as mref
+from tinybatch_amd.block_manager import BlockManager
+from tinybatch_amd.config import EngineConfig
+from tinybatch_amd.engine import LLMEngine
+from tinybatch_amd.kv_cache import PagedKVCache
+from tinybatch_amd.model import ModelConfig, Qwen2Paged
+from tinybatch_amd.scheduler import Request, Scheduler
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+
+
+def small_cfg(layers=2, heads=2, kv_heads=1, vocab=300):
+    return ModelConfig(n_layers=layers, n_heads=heads, n_kv_heads=kv_heads, d_model=64 * heads, head_dim=64,
+                       d_ff=256, vocab_size=vocab, rms_eps=1e-6, rope_theta=1e6, tie_embeddings=True,
+                       max_position=2048)
+
+
+def cpu_weights(model):
+    return {k: v.detach().float().cpu() for k, v in model.reference_weights().items()}
+
+
+def test_forward_logits_match_oracle_fp32_mixed_step():
+    mc = small_cfg(layers=3, heads=4, kv_heads=2)
+    model = Qwen2Paged(mc, DEV, torch.float32, seed=1)
+    w = cpu_weights(model)
+    BS, NB = 16, 64
+    cache = PagedKVCache(mc.n_layers, NB, BS, mc.n_kv_heads, mc.head_dim, DEV, torch.float32)
+    pools = [torch.zeros(NB, 2, mc.n_kv_heads, BS, mc.head_dim) for _ in range(mc.n_layers)]
+    g = torch.Generator().manual_seed(2)
+    # step 1: two prefills (one of exactly two blocks); step 2: both decode + a new prefill
+    tables = [[5, 9, 2], [11, 3, 6], [7, 1, 0, 4]]   # the 32-token prompt has its decode block
+    p0 = torch.randint(0, mc.vocab_size, (40,), generator=g).tolist()
+    p1 = torch.randint(0, mc.vocab_size, (32,), generator=g).tolist()
+    p2 = torch.randint(0, mc.vocab_size, (50,), generator=g).tolist()
+    steps = [
+        (p0 + p1, list(range(40)) + list(range(32)), [(0, 40), (40, 72)], tables[:2], [40, 32]),
+        (p2 + [7, 8], list(range(50)) + [40, 32], [(0, 50), (50, 51), (51, 52)], [tables[2]] + tables[:2],
+         [50, 41, 33]),
+    ]
+    for ids, pos, slices, tbls, ctx in steps:
+        ids_t, pos_t = torch.tensor(ids), torch.tensor(pos)
+        got = model.forward(ids_t.to(DEV), pos_t.to(DEV), slices, tbls, ctx, cache)
+        want = mref.forward(w, mc, ids_t, pos_t, slices, tbls, ctx, pools, BS)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(got.cpu(), want, atol=2e-4, rtol=2e-4)
+    for layer in range(mc.n_layers):
+        torch.testing.assert_close(cache.pools[layer].cpu(), pools[layer], atol=1e-5, rtol=1e-5)
+
+
+def oracle_generate(model, ecfg, prompts, max_new):
+    """The engine loop with the CPU restatement as the forward pass."""
+    mc = model.cfg
+    w = cpu_weights(model)
+    bm = BlockManager(ecfg.num_blocks, ecfg.block_size, ecfg.enable_prefix_caching)
+    sch = Scheduler(ecfg, bm)
+    pools = [torch.zeros(ecfg.num_blocks, 2, mc.n_kv_heads, ecfg.block_size, mc.head_dim)
+             for _ in range(mc.n_layers)]
+    reqs = [Request(prompt_token_ids=list(p), max_new_tokens=m) for p, m in zip(prompts, max_new)]
+    for r in reqs:
+        sch.add(r)
+    while sch.has_work():
+        b = sch.schedule()
+        ordered = b.prefill + b.decode
+        ids, pos, slices, tables, ctx = LLMEngine.build_step(b.prefill, b.decode)
+        logits = mref.forward(w, mc, torch.tensor(ids), torch.tensor(pos), slices, tables, ctx, pools,
+                              ecfg.block_size)
+        for r, t in zip(ordered, logits.argmax(-1).tolist()):
+            r.output_token_ids.append(int(t))
+            if len(r.output_token_ids) >= r.max_new_tokens:
+                sch.finish(r)
+    return [r.output_token_ids for r in reqs], bm.hit_rate()
+
+
+def test_engine_generation_matches_oracle_token_for_token_fp32():
+    mc = small_cfg(layers=2, heads=4, kv_heads=2)
+    ecfg = EngineConfig(dtype="float32", num_blocks=96, block_size=16, max_batch_tokens=160, max_running=5)
+    model = Qwen2Paged(mc, DEV, torch.float32, seed=3)
+    g = torch.Generator().manual_seed(4)
+    shared = torch.randint(0, mc.vocab_size, (48,), generator=g).tolist()      # three full blocks
+    prompts = [shared + torch.randint(0, mc.vocab_size, (n,), generator=g).tolist() for n in (5, 17, 0)]
+    prompts += [torch.randint(0, mc.vocab_size, (n,), generator=g).tolist() for n in (32, 9, 70)]
+    max_new = [12, 7, 20, 15, 30, 9]
+    eng = LLMEngine(ecfg, model=model)
+    reqs = [eng.add_request(p, max_new_tokens=m) for p, m in zip(prompts, max_new)]
+    while eng.scheduler.has_work():
+        eng.step()
+    want, hit_rate = oracle_generate(model, ecfg, prompts, max_new)
+    assert [r.output_token_ids for r in reqs] == want
+    assert eng.block_manager.hit_rate() == hit_rate > 0
+    assert [len(r.output_token_ids) for r in reqs] == max_new
+
+
+def test_engine_qwen_dims_bf16_runs_with_prefix_hits():
+    """0.5B dimensions in bf16 (two layers to keep it short): the tiled prefill,
+    the row-group work items and decode all run inside one engine."""
+    mc = ModelConfig.qwen2_0_5b()
+    mc.n_layers = 2
+    ecfg = EngineConfig(num_blocks=256, max_batch_tokens=2048, max_running=8)
+    eng = LLMEngine(ecfg, model_config=mc)
+    g = torch.Generator().manual_seed(5)
+    prefix = torch.randint(0, mc.vocab_size, (400,), generator=g).tolist()
+    prompts = [prefix + torch.randint(0, mc.vocab_size, (n,), generator=g).tolist() for n in (1, 60, 111)]
+    prompts += [torch.randint(0, mc.vocab_size, (n,), generator=g).tolist() for n in (32, 512)]
+    outs = eng.generate(prompts, max_new_tokens=6)
+    assert [len(o) for o in outs] == [6] * 5
+    assert eng.block_manager.hit_rate() > 0
+    assert all(0 <= t < mc.vocab_size for o in outs for t in o)

@@ -1,0 +1,147 @@
+"""The engine: schedule -> one flat-batch forward -> sample (token ids in and out).
+
+Counterpart of LLMEngine (reference src/tinybatch/engine.py:32-171) without a
+tokenizer: requests carry token ids, outputs are token ids. One ``step`` runs
+one iteration of continuous batching: prefills of newly admitted requests
+(their uncached prompt tokens) followed by one decode token for every running
+sequence, in that order in the flat batch (engine.py:99-120), then greedy
+(or temperature / top-p) sampling of each sequence's next token
+(engine.py:145-159).
+
+MI355X-side choices: the step's metadata is built once and shared by all
+layers (the cache object memoises it on the positions tensor); greedy rows
+are sampled by one batched argmax and one device-to-host copy instead of one
+``int()`` synchronisation per sequence.
+"""
+from __future__ import annotations
+
+import time
+from dataclasses import dataclass, field
+
+import torch
+
+from .block_manager import BlockManager
+from .config import EngineConfig
+from .kv_cache import PagedKVCache
+from .model import ModelConfig, Qwen2Paged
+from .scheduler import Request, Scheduler
+
+
+@dataclass
+class StepOutput:
+    req_id: int
+    token_id: int
+    finished: bool
+    request: Request = field(repr=False)
+
+
+class LLMEngine:
+    def __init__(self, config: EngineConfig | None = None, model_config: ModelConfig | None = None,
+                 model: Qwen2Paged | None = None):
+        self.cfg = config or EngineConfig()
+        self.device = torch.device(self.cfg.device)
+        self.dtype = getattr(torch, self.cfg.dtype)
+        self.model = model or Qwen2Paged(model_config or ModelConfig.qwen2_0_5b(), self.device, self.dtype,
+                                         seed=self.cfg.seed)
+        mc = self.model.cfg
+        self.kv_cache = PagedKVCache(mc.n_layers, self.cfg.num_blocks, self.cfg.block_size, mc.n_kv_heads,
+                                     mc.head_dim, self.device, self.dtype)
+        self.block_manager = BlockManager(self.cfg.num_blocks, self.cfg.block_size, self.cfg.enable_prefix_caching)
+        self.scheduler = Scheduler(self.cfg, self.block_manager)
+        self.eos_ids = set(self.cfg.stop_token_ids)
+        self.steps = 0
+        self.last_step_prefills = 0
+
+    # ---- API -----------------------------------------------------------------
+    def add_request(self, prompt_token_ids: list[int], *, max_new_tokens: int | None = None,
+                    temperature: float | None = None, top_p: float | None = None) -> Request:
+        ids = list(prompt_token_ids)[: self.cfg.max_model_len - 1]
+        if not ids:
+            raise ValueError("empty prompt")
+        req = Request(prompt_token_ids=ids,
+                      max_new_tokens=self.cfg.max_new_tokens if max_new_tokens is None else max_new_tokens,
+                      temperature=self.cfg.temperature if temperature is None else temperature,
+                      top_p=self.cfg.top_p if top_p is None else top_p)
+        self.scheduler.add(req)
+        return req
+
+    def generate(self, prompts: list[list[int]], **kw) -> list[list[int]]:
+        reqs = [self.add_request(p, **kw) for p in prompts]
+        while self.scheduler.has_work():
+            self.step()
+        return [r.output_token_ids for r in reqs]
+
+    # ---- one iteration ---------------------------------------------------------
+    @staticmethod
+    def build_step(prefill: list[Request], decode: list[Request]):
+        """Flat-batch inputs of a step (engine.py:99-120)."""
+        token_ids: list[int] = []
+        positions: list[int] = []
+        seq_slices: list[tuple[int, int]] = []
+        block_tables: list[list[int]] = []
+        context_lens: list[int] = []
+        for req in prefill:
+            start = len(token_ids)
+            token_ids.extend(req.prompt_token_ids[req.num_cached_tokens:])
+            positions.extend(range(req.num_cached_tokens, len(req.prompt_token_ids)))
+            seq_slices.append((start, len(token_ids)))
+            block_tables.append(req.block_table)
+            context_lens.append(len(req.prompt_token_ids))
+        for req in decode:
+            start = len(token_ids)
+            token_ids.append(req.all_token_ids()[-1])
+            positions.append(req.context_len() - 1)
+            seq_slices.append((start, len(token_ids)))
+            block_tables.append(req.block_table)
+            context_lens.append(req.context_len())
+        return token_ids, positions, seq_slices, block_tables, context_lens
+
+    def step(self) -> list[StepOutput]:
+        batch = self.scheduler.schedule()
+        if batch.is_empty():
+            return []
+        ordered = batch.prefill + batch.decode
+        self.last_step_prefills = len(batch.prefill)
+        token_ids, positions, seq_slices, block_tables, context_lens = self.build_step(batch.prefill, batch.decode)
+        tok = torch.tensor(token_ids, dtype=torch.int64).pin_memory().to(self.device, non_blocking=True)
+        pos = torch.tensor(positions, dtype=torch.int64).pin_memory().to(self.device, non_blocking=True)
+        # the step's metadata, built from the host lists (no device round trip) and shared by every layer
+        self.kv_cache.step_metadata(pos, seq_slices, block_tables, context_lens,
+                                    self.kv_cache.rows_per_item(self.model.cfg.n_heads), host_positions=positions)
+        logits = self.model.forward(tok, pos, seq_slices, block_tables, context_lens, self.kv_cache)
+        next_ids = self._sample(logits, ordered)
+        now = time.perf_counter()
+        outputs = []
+        for req, t in zip(ordered, next_ids):
+            if req.first_token_time is None:
+                req.first_token_time = now
+            req.output_token_ids.append(t)
+            finished = (t in self.eos_ids or len(req.output_token_ids) >= req.max_new_tokens
+                        or req.context_len() >= self.cfg.max_model_len)
+            if finished:
+                self.scheduler.finish(req)
+            outputs.append(StepOutput(req.req_id, t, finished, req))
+        self.steps += 1
+        return outputs
+
+    def _sample(self, logits: torch.Tensor, reqs: list[Request]) -> list[int]:
+        greedy = logits.argmax(dim=-1).cpu().tolist()        # one copy for the whole batch
+        out = []
+        for i, req in enumerate(reqs):
+            if req.temperature <= 0.0:
+                out.append(int(greedy[i]))
+                continue
+            probs = torch.softmax(logits[i] / req.temperature, dim=-1)
+            if req.top_p < 1.0:
+                sorted_p, idx = probs.sort(descending=True)
+                keep = sorted_p.cumsum(0) - sorted_p < req.top_p
+                probs = torch.zeros_like(probs).scatter(0, idx[keep], sorted_p[keep])
+                probs = probs / probs.sum()
+            out.append(int(torch.multinomial(probs, 1)))
+        return out
+
+    def stats(self) -> dict:
+        bm = self.block_manager
+        return {"kv_pool_mb": round(self.kv_cache.memory_bytes() / 2**20, 1), "free_blocks": bm.num_free(),
+                "prefix_hit_rate": round(bm.hit_rate(), 3), "running": len(self.scheduler.running),
+                "waiting": len(self.scheduler.waiting), "steps": self.steps}

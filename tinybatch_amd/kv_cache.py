@@ -54,7 +54,7 @@ class PagedKVCache:
 
     # ---- per-step metadata -------------------------------------------------
     def step_metadata(self, positions, seq_slices, block_tables, context_lens=None,
-                      rows_per_item: int = 1) -> StepMetadata:
+                      rows_per_item: int = 1, host_positions=None) -> StepMetadata:
         """Build (or reuse) the step's device metadata.
 
         Every layer of a forward pass passes the same argument objects, so the
@@ -62,7 +62,9 @@ class PagedKVCache:
         object is the same one (held by the cache, so its identity cannot be
         recycled) with an unchanged in-place version, and the slices, tables
         and context lengths compare equal. write() (no context lengths) may
-        reuse an entry built for attention().
+        reuse an entry built for attention(). ``host_positions`` (the same
+        positions as a host list) spares the device-to-host copy of a device
+        ``positions`` tensor; the entry is still keyed on ``positions``.
         """
         pos_key = (positions, positions._version) if isinstance(positions, torch.Tensor) else list(positions)
         for e in self._meta_cache:
@@ -72,7 +74,8 @@ class PagedKVCache:
                 return e["meta"]
         # 16-bit pools serve long runs of new rows (prefills) with the tile kernel
         tile = self.pools[0].dtype in (torch.float16, torch.bfloat16)
-        meta = build_step_metadata(positions, seq_slices, block_tables, context_lens,
+        meta = build_step_metadata(positions if host_positions is None else host_positions,
+                                   seq_slices, block_tables, context_lens,
                                    block_size=self.block_size, num_blocks=self.num_blocks,
                                    partition_tokens=self.partition_tokens, rows_per_item=rows_per_item,
                                    tile_prefill=tile)
@@ -104,12 +107,16 @@ class PagedKVCache:
         return ops.kv_gather(self.pools[layer], t, context_len)
 
     # ---- fused data path ---------------------------------------------------
+    def rows_per_item(self, num_heads: int) -> int:
+        """Query rows per attention work item for this cache's dtype and geometry."""
+        return ops.rows_per_item(self.dtype, num_heads, self.n_kv_heads)
+
     def attention(self, layer: int, q: torch.Tensor, positions, seq_slices, block_tables, context_lens,
                   *, num_heads: int | None = None, scale: float | None = None,
                   out: torch.Tensor | None = None) -> torch.Tensor:
         """attn_out [T, Hq*D] for the whole flat batch (reference model.py:130-147)."""
         hq = num_heads if num_heads is not None else q.shape[1]
-        rows = ops.rows_per_item(q.dtype, hq, self.n_kv_heads)
+        rows = self.rows_per_item(hq)
         meta = self._lookup_or_build(positions, seq_slices, block_tables, context_lens, q.shape[0], rows)
         return ops.paged_attention(q, self.pools[layer], meta, num_heads=hq, scale=scale, out=out)
 

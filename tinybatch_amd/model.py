@@ -1,0 +1,149 @@
+"""Random-initialised Qwen2 forward pass over the paged KV cache (GPU).
+
+Counterpart of Qwen2Paged (reference src/tinybatch/model.py:111-158) with the
+attention region (model.py:127-147) replaced by the paged data path:
+kv_cache.write (K1, slot-mapped append) and kv_cache.attention (K2, fused
+paged attention over every sequence of the flat batch in one launch). The
+rest follows the reference layer by layer: RMSNorm computed in fp32
+(model.py:65-69), rotate-half RoPE in fp32 (model.py:72-80), q/k/v
+projections with biases, o_proj, SwiGLU MLP, residuals, final norm, tied LM
+head on the last token of each sequence (model.py:153-158).
+
+MI355X-side choices: q/k/v are one GEMM over a concatenated weight (and
+gate/up another), the RoPE tables are built once for every position up to
+max_position, and the final norm and LM head run on the last rows only (the
+norm is per row, so this equals norming every row and selecting).
+
+Weights are drawn from a seeded generator (no checkpoint exists offline):
+N(0, 0.02) for embeddings, projections and biases, ones for the norms.
+``reference_weights`` returns them under the reference's state-dict names.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from .kv_cache import PagedKVCache
+
+
+@dataclass
+class ModelConfig:
+    n_layers: int
+    n_heads: int
+    n_kv_heads: int
+    d_model: int
+    head_dim: int
+    d_ff: int
+    vocab_size: int
+    rms_eps: float
+    rope_theta: float
+    tie_embeddings: bool
+    max_position: int
+
+    @staticmethod
+    def qwen2_0_5b() -> "ModelConfig":
+        """Qwen2.5-0.5B dimensions (494,032,768 parameters with tied embeddings);
+        rope_theta / rms_eps are Qwen2.5's published 1e6 / 1e-6."""
+        return ModelConfig(n_layers=24, n_heads=14, n_kv_heads=2, d_model=896, head_dim=64, d_ff=4864,
+                           vocab_size=151936, rms_eps=1e-6, rope_theta=1e6, tie_embeddings=True,
+                           max_position=32768)
+
+    def num_params(self) -> int:
+        qkv = (self.n_heads + 2 * self.n_kv_heads) * self.head_dim
+        per_layer = (self.d_model * qkv + qkv + self.n_heads * self.head_dim * self.d_model
+                     + 3 * self.d_model * self.d_ff + 2 * self.d_model)
+        head = 0 if self.tie_embeddings else self.vocab_size * self.d_model
+        return self.vocab_size * self.d_model + self.n_layers * per_layer + self.d_model + head
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """model.py:65-69: normalise in fp32, scale, cast back."""
+    xf = x.float()
+    xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return (xf * weight.float()).to(x.dtype)
+
+
+def rope_tables(head_dim: int, theta: float, max_position: int, device) -> tuple[torch.Tensor, torch.Tensor]:
+    """cos / sin [max_position, head_dim/2] with the reference's fp32 arithmetic (model.py:74-76)."""
+    inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, device=device).float() / head_dim))
+    freqs = torch.arange(max_position, device=device).float()[:, None] * inv_freq[None, :]
+    return freqs.cos(), freqs.sin()
+
+
+def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Rotate-half RoPE (model.py:77-80); x [T, heads, D], cos/sin [T, D/2]."""
+    c, s = cos[:, None, :], sin[:, None, :]
+    x1, x2 = x.float().chunk(2, dim=-1)
+    return torch.cat((x1 * c - x2 * s, x2 * c + x1 * s), dim=-1).to(x.dtype)
+
+
+class Qwen2Paged:
+    """Weights + forward; inference only."""
+
+    def __init__(self, cfg: ModelConfig, device: torch.device, dtype: torch.dtype, seed: int = 0):
+        self.cfg, self.device, self.dtype = cfg, torch.device(device), dtype
+        g = torch.Generator(device=self.device).manual_seed(seed)
+
+        def rnd(*shape):
+            return (torch.randn(*shape, generator=g, device=self.device, dtype=torch.float32) * 0.02).to(dtype)
+
+        c = cfg
+        qkv = (c.n_heads + 2 * c.n_kv_heads) * c.head_dim
+        self.embed = rnd(c.vocab_size, c.d_model)
+        self.lm_head = self.embed if c.tie_embeddings else rnd(c.vocab_size, c.d_model)
+        self.layers = []
+        for _ in range(c.n_layers):
+            self.layers.append({
+                "ln1": torch.ones(c.d_model, device=self.device, dtype=dtype),
+                "w_qkv": rnd(qkv, c.d_model), "b_qkv": rnd(qkv),
+                "w_o": rnd(c.d_model, c.n_heads * c.head_dim),
+                "ln2": torch.ones(c.d_model, device=self.device, dtype=dtype),
+                "w_gu": rnd(2 * c.d_ff, c.d_model),
+                "w_down": rnd(c.d_model, c.d_ff),
+            })
+        self.norm = torch.ones(c.d_model, device=self.device, dtype=dtype)
+        self.cos, self.sin = rope_tables(c.head_dim, c.rope_theta, c.max_position, self.device)
+
+    def reference_weights(self) -> dict[str, torch.Tensor]:
+        """The weights under the reference's state-dict names (model.py:97-98,111-151)."""
+        c = self.cfg
+        hq, hk = c.n_heads * c.head_dim, c.n_kv_heads * c.head_dim
+        w = {"model.embed_tokens.weight": self.embed, "model.norm.weight": self.norm, "lm_head.weight": self.lm_head}
+        for i, L in enumerate(self.layers):
+            p = f"model.layers.{i}."
+            w[p + "input_layernorm.weight"] = L["ln1"]
+            w[p + "post_attention_layernorm.weight"] = L["ln2"]
+            for name, lo, hi in (("q", 0, hq), ("k", hq, hq + hk), ("v", hq + hk, hq + 2 * hk)):
+                w[p + f"self_attn.{name}_proj.weight"] = L["w_qkv"][lo:hi]
+                w[p + f"self_attn.{name}_proj.bias"] = L["b_qkv"][lo:hi]
+            w[p + "self_attn.o_proj.weight"] = L["w_o"]
+            w[p + "mlp.gate_proj.weight"] = L["w_gu"][:c.d_ff]
+            w[p + "mlp.up_proj.weight"] = L["w_gu"][c.d_ff:]
+            w[p + "mlp.down_proj.weight"] = L["w_down"]
+        return w
+
+    @torch.inference_mode()
+    def forward(self, token_ids: torch.Tensor, positions: torch.Tensor, seq_slices: list[tuple[int, int]],
+                block_tables: list[list[int]], context_lens: list[int], kv_cache: PagedKVCache) -> torch.Tensor:
+        """Logits [n_seqs, vocab] (fp32) for the last token of each sequence (model.py:101-158)."""
+        c = self.cfg
+        T = token_ids.shape[0]
+        hq, hk = c.n_heads * c.head_dim, c.n_kv_heads * c.head_dim
+        cos, sin = self.cos[positions], self.sin[positions]
+        h = F.embedding(token_ids, self.embed)
+        for i, L in enumerate(self.layers):
+            x = rms_norm(h, L["ln1"], c.rms_eps)
+            qkv = F.linear(x, L["w_qkv"], L["b_qkv"])
+            q = apply_rope(qkv[:, :hq].view(T, c.n_heads, c.head_dim), cos, sin)
+            k = apply_rope(qkv[:, hq:hq + hk].view(T, c.n_kv_heads, c.head_dim), cos, sin)
+            v = qkv[:, hq + hk:].view(T, c.n_kv_heads, c.head_dim)
+            kv_cache.write(i, k, v, positions, seq_slices, block_tables)
+            attn = kv_cache.attention(i, q, positions, seq_slices, block_tables, context_lens)
+            h = h + F.linear(attn, L["w_o"])
+            x = rms_norm(h, L["ln2"], c.rms_eps)
+            gate, up = F.linear(x, L["w_gu"]).split(c.d_ff, dim=-1)
+            h = h + F.linear(F.silu(gate) * up, L["w_down"])
+        last = torch.tensor([e - 1 for _, e in seq_slices], device=h.device)
+        return F.linear(rms_norm(h[last], self.norm, c.rms_eps), self.lm_head).float()

@@ -281,3 +281,44 @@ def make_mixed_workload(name: str = "qwen-bf16-mixed", *, seed: int = 4, num_blo
                          num_blocks=num_blocks, q_lens=q_lens, context_lens=ctx, block_tables=tables, q=q,
                          k_new=k_new, v_new=v_new, pool=pool, copy_src=src, copy_dst=dst,
                          shared_prefix=prefix, num_prefill=n_pre, seed=seed)
+
+
+@dataclass
+class ServingWorkload:
+    """Continuous-batching workload of requests (token ids), all arriving at t = 0."""
+    name: str
+    prompts: list[list[int]]
+    max_new_tokens: list[int]
+    shared_prefix_len: int
+    sharing: list[bool]
+    seed: int
+
+
+def make_serving_workload(name: str = "qwen2-0.5b-e2e", *, seed: int = 5, vocab_size: int = 151936,
+                          num_requests: int = 32, share_frac: float = 0.75, prefix_len: int = 400,
+                          max_prompt: int = 512, min_prompt: int = 32, out_lo: int = 16,
+                          out_hi: int = 256) -> ServingWorkload:
+    """Random-token requests: ``share_frac`` of them (chosen by a seeded
+    permutation) start with one common ``prefix_len``-token prefix and have
+    lengths U{prefix_len+1..max_prompt}; the rest U{min_prompt..max_prompt};
+    output lengths U{out_lo..out_hi} (greedy, no stop tokens)."""
+    if name != "qwen2-0.5b-e2e":
+        raise KeyError(name)
+    gen = torch.Generator().manual_seed(seed)
+    n_share = round(share_frac * num_requests)
+    order = torch.randperm(num_requests, generator=gen).tolist()
+    sharing = [False] * num_requests
+    for i in order[:n_share]:
+        sharing[i] = True
+    prefix = torch.randint(0, vocab_size, (prefix_len,), generator=gen).tolist()
+    prompts, outs = [], []
+    for i in range(num_requests):
+        if sharing[i]:
+            n = int(torch.randint(prefix_len + 1, max_prompt + 1, (1,), generator=gen))
+            prompts.append(prefix + torch.randint(0, vocab_size, (n - prefix_len,), generator=gen).tolist())
+        else:
+            n = int(torch.randint(min_prompt, max_prompt + 1, (1,), generator=gen))
+            prompts.append(torch.randint(0, vocab_size, (n,), generator=gen).tolist())
+        outs.append(int(torch.randint(out_lo, out_hi + 1, (1,), generator=gen)))
+    return ServingWorkload(name=name, prompts=prompts, max_new_tokens=outs, shared_prefix_len=prefix_len,
+                           sharing=sharing, seed=seed)
