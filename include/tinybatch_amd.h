@@ -113,6 +113,12 @@ int32_t tb_kv_gather(const void* pool, int64_t num_blocks,
  *     only used when a row has > 1 partition (max_parts_per_row > 1), which
  *     also launches a second (combine) kernel. Calls that may overlap in time
  *     need their own workspace.
+ * device_counts (may be NULL): device array {work items, split rows, prefill
+ *   tiles} read by the kernels when they run; num_work_items, num_split_rows
+ *   and num_prefill_tiles are then capacities that size the grids and the
+ *   workgroups past the counts exit at once. One launch recorded in a HIP
+ *   graph thus serves every step whose metadata fits the capacities (the
+ *   metadata arrays are refreshed in place before each replay).
  * Fused decode append (k_new != NULL): each row's own newest position
  * row_ctx-1 is read from k_new/v_new ([num_rows][num_kv_heads][head_dim]) and
  * written to its slot in the pool by the same kernel, replacing a separate
@@ -143,7 +149,7 @@ int32_t tb_paged_attention(const void* q, int64_t q_row_stride,
                            const void* k_new, int64_t k_row_stride,
                            const void* v_new, int64_t v_row_stride,
                            void* workspace, size_t workspace_bytes,
-                           hipStream_t stream);
+                           const int32_t* device_counts, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * K3 — block copy across every layer pool in one launch.
@@ -169,6 +175,36 @@ int32_t tb_block_gather(const void* pool, int64_t num_blocks, const int32_t* blo
 int32_t tb_block_scatter(const void* staging, void* pool, int64_t num_blocks,
                          const int32_t* blocks, int32_t num_blocks_to_move,
                          int64_t block_bytes, hipStream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Model-side fused elementwise ops of the engine's Qwen2 layer (one launch
+ * each instead of chains of tensor ops). Row strides are in elements.
+ *
+ * RMSNorm, src/tinybatch/model.py:65-69 (with the residual add of
+ * model.py:149/154 when residual != NULL):
+ *   if residual: residual[r] = x[r] + residual[r]  (rounded), h = residual[r]
+ *   else h = x[r];  out[r] = (h * rsqrt(mean(h^2) + eps)) * weight, in fp32.
+ *   dim <= 4096.
+ */
+int32_t tb_rms_norm(const void* x, int64_t x_row_stride, void* residual, int64_t residual_row_stride,
+                    const void* weight, void* out, int64_t out_row_stride, int32_t rows, int32_t dim,
+                    float eps, int32_t dtype, hipStream_t stream);
+
+/* Rotate-half RoPE of q and k, src/tinybatch/model.py:72-80,125: qkv rows hold
+ * num_heads q heads then num_kv_heads k heads of head_dim each; with
+ * c, s = cos_table / sin_table [max_position][head_dim/2] (fp32) at the row's
+ * position, x1 = x[i], x2 = x[i + D/2]:
+ *   out[i] = x1*c - x2*s,  out[i + D/2] = x2*c + x1*s,
+ * written to q_out [rows][num_heads][D] and k_out [rows][num_kv_heads][D]. */
+int32_t tb_rope_qk(const void* qkv, int64_t row_stride, const int64_t* positions, const float* cos_table,
+                   const float* sin_table, int32_t max_position, void* q_out, void* k_out, int32_t rows,
+                   int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t dtype,
+                   hipStream_t stream);
+
+/* SwiGLU gate, src/tinybatch/model.py:152-154: gate_up rows hold gate [d_ff]
+ * then up [d_ff]; out = silu(gate) (rounded) * up. */
+int32_t tb_silu_mul(const void* gate_up, int64_t row_stride, void* out, int64_t out_row_stride,
+                    int32_t rows, int32_t d_ff, int32_t dtype, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -68,7 +68,7 @@ def test_attention_rejects_bad_arguments_without_launching():
         return L.tb_paged_attention(a["q"], a["qs"], a["pool"], a["nb"], a["out"], a["os"], a["bt"], a["mnb"],
                                     a["work"], a["nw"], a["tiles"], a["nt"], a["rpo"], a["nr"], a["split"], a["ns"],
                                     a["mpr"], a["pt"], a["tp"], a["hq"], a["hkv"], a["d"], a["bs"], a["scale"],
-                                    a["dt"], a["kn"], a["ks"], a["vn"], a["vs"], a["ws"], a["wsb"], None)
+                                    a["dt"], a["kn"], a["ks"], a["vn"], a["vs"], a["ws"], a["wsb"], None, None)
 
     assert call(d=96) == _lib.TB_ERR_UNSUPPORTED               # no kernel for head_dim 96
     assert call(hq=13) == _lib.TB_ERR_INVALID_ARG              # heads not a multiple of kv heads

@@ -78,9 +78,13 @@ def oracle_generate(model, ecfg, prompts, max_new):
     return [r.output_token_ids for r in reqs], bm.hit_rate()
 
 
-def test_engine_generation_matches_oracle_token_for_token_fp32():
+@pytest.mark.parametrize("graphs", [True, False])
+def test_engine_generation_matches_oracle_token_for_token_fp32(graphs):
+    """Eager steps, and decode steps replayed from captured graphs (batch buckets
+    1, 2, 4, 5 with padded rows), against the oracle-driven schedule."""
     mc = small_cfg(layers=2, heads=4, kv_heads=2)
-    ecfg = EngineConfig(dtype="float32", num_blocks=96, block_size=16, max_batch_tokens=160, max_running=5)
+    ecfg = EngineConfig(dtype="float32", num_blocks=96, block_size=16, max_batch_tokens=160, max_running=5,
+                        decode_graphs=graphs)
     model = Qwen2Paged(mc, DEV, torch.float32, seed=3)
     g = torch.Generator().manual_seed(4)
     shared = torch.randint(0, mc.vocab_size, (48,), generator=g).tolist()      # three full blocks
@@ -95,6 +99,7 @@ def test_engine_generation_matches_oracle_token_for_token_fp32():
     assert [r.output_token_ids for r in reqs] == want
     assert eng.block_manager.hit_rate() == hit_rate > 0
     assert [len(r.output_token_ids) for r in reqs] == max_new
+    assert (eng.graph_steps > 0) == graphs
 
 
 def test_engine_qwen_dims_bf16_runs_with_prefix_hits():
@@ -112,3 +117,48 @@ def test_engine_qwen_dims_bf16_runs_with_prefix_hits():
     assert [len(o) for o in outs] == [6] * 5
     assert eng.block_manager.hit_rate() > 0
     assert all(0 <= t < mc.vocab_size for o in outs for t in o)
+
+
+def test_decode_graph_replays_match_eager_steps_bf16():
+    """The same decode steps through a captured graph and eagerly (fused vs
+    separate append, padded bucket rows): identical K/V written and next tokens
+    within bf16 noise of each other's logits."""
+    from tinybatch_amd.decode_graphs import DecodeGraphs
+    mc = small_cfg(layers=2, heads=14, kv_heads=2, vocab=500)
+    model = Qwen2Paged(mc, DEV, torch.bfloat16, seed=7)
+    BS, NB = 16, 128
+    caches = [PagedKVCache(mc.n_layers, NB, BS, mc.n_kv_heads, mc.head_dim, DEV, torch.bfloat16) for _ in range(2)]
+    g = torch.Generator().manual_seed(8)
+    lens = [37, 300, 16, 64, 129]
+    tables, at = [], 0
+    for n in lens:
+        k = n // BS + 1
+        tables.append(list(range(at, at + k))); at += k
+    prompts = [torch.randint(0, mc.vocab_size, (n,), generator=g).tolist() for n in lens]
+    ids = torch.tensor(sum(prompts, []), device=DEV)
+    pos = torch.tensor(sum([list(range(n)) for n in lens], []), device=DEV)
+    slices, at = [], 0
+    for n in lens:
+        slices.append((at, at + n)); at += n
+    for cache in caches:                                     # the same prefill into both caches
+        model.forward(ids, pos, slices, tables, lens, cache)
+    graphs = DecodeGraphs(model, caches[1], max_batch=8, max_model_len=1024)
+    toks = [p[-1] for p in prompts]
+    ctx = list(lens)
+    for _ in range(3):
+        positions = list(ctx)
+        ctx = [c + 1 for c in ctx]
+        eager = model.forward(torch.tensor(toks, device=DEV), torch.tensor(positions, device=DEV),
+                              [(i, i + 1) for i in range(len(toks))], tables, ctx, caches[0])
+        got = graphs.run(toks, positions, tables, ctx)
+        top2 = eager.topk(2, dim=-1)
+        for b, t in enumerate(got):
+            if t != int(top2.indices[b, 0]):                 # only a near tie may differ
+                assert float(top2.values[b, 0] - eager[b, t]) < 0.05
+        toks = got
+    torch.cuda.synchronize()
+    for layer in range(mc.n_layers):
+        a, b = caches[0].pools[layer], caches[1].pools[layer]
+        assert torch.equal(a[:sum(len(t) for t in tables)].view(torch.int16)[:, 1],
+                           b[:sum(len(t) for t in tables)].view(torch.int16)[:, 1]) or \
+            torch.allclose(a.float(), b.float(), atol=2e-2, rtol=2e-2)

@@ -1,0 +1,61 @@
+"""The fused layer kernels against the oracle's restatement of the reference
+ops (oracle/model_reference.py, CPU): RMSNorm with and without the residual
+add, RoPE of q and k from qkv rows, SiLU * up."""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import model_reference as mref
+from tinybatch_amd import layer_ops
+from tinybatch_amd.model import rope_tables
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+TOL = {torch.float32: dict(atol=1e-5, rtol=1e-5), torch.bfloat16: dict(atol=2e-2, rtol=2e-2),
+       torch.float16: dict(atol=2e-3, rtol=2e-3)}
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dim", [896, 4096, 100])
+def test_rms_norm_with_and_without_residual(dtype, dim):
+    g = torch.Generator().manual_seed(dim)
+    x = (torch.randn(37, dim, generator=g) * 3).to(dtype)
+    r = torch.randn(37, dim, generator=g).to(dtype)
+    w = (1 + 0.1 * torch.randn(dim, generator=g)).to(dtype)
+    got = layer_ops.rms_norm(x.to(DEV), w.to(DEV), 1e-6)
+    torch.testing.assert_close(got.cpu().float(), mref.rms_norm(x, w, 1e-6).float(), **TOL[dtype])
+    res = r.to(DEV)
+    got = layer_ops.rms_norm(x.to(DEV), w.to(DEV), 1e-6, residual=res)
+    h = r + x                                                    # the tensor add of the reference layer
+    assert torch.equal(res.cpu(), h)                             # same rounding as the tensor add
+    torch.testing.assert_close(got.cpu().float(), mref.rms_norm(h, w, 1e-6).float(), **TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("hq,hkv,d", [(14, 2, 64), (32, 8, 128)])
+def test_rope_qk_from_qkv_rows(dtype, hq, hkv, d):
+    """fp32 tolerance: the angle pos * inv_freq is rounded to fp32 (and cos/sin
+    evaluated) by each platform's own routines, so the GPU table and the CPU
+    oracle differ by about pos * 2^-24 rad; small positions pin the kernel's
+    arithmetic tightly, large ones within that angle error."""
+    g = torch.Generator().manual_seed(hq)
+    T = 29
+    qkv = torch.randn(T, (hq + 2 * hkv) * d, generator=g).to(dtype)
+    cos, sin = rope_tables(d, 1e6, 8192, DEV)
+    for hi, atol in ((64, 2e-5), (5000, 2e-3)):
+        pos = torch.randint(0, hi, (T,), generator=g)
+        q, k = layer_ops.rope_qk(qkv.to(DEV), pos.to(DEV), cos, sin, hq, hkv, d)
+        want_q = mref.rope(qkv[:, :hq * d].view(T, hq, d), pos, 1e6)
+        want_k = mref.rope(qkv[:, hq * d:(hq + hkv) * d].view(T, hkv, d), pos, 1e6)
+        tol = dict(atol=atol, rtol=0) if dtype == torch.float32 else TOL[dtype]
+        torch.testing.assert_close(q.cpu().float(), want_q.float(), **tol)
+        torch.testing.assert_close(k.cpu().float(), want_k.float(), **tol)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_silu_mul(dtype):
+    g = torch.Generator().manual_seed(9)
+    gu = (torch.randn(13, 2 * 4864, generator=g) * 4).to(dtype)
+    got = layer_ops.silu_mul(gu.to(DEV), 4864)
+    want = F.silu(gu[:, :4864]) * gu[:, 4864:]                   # the reference's two tensor ops
+    torch.testing.assert_close(got.cpu().float(), want.float(), **TOL[dtype])

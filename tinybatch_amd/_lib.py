@@ -44,11 +44,16 @@ SIGNATURES = {
         c_i32, c_i32, c_i32, c_i32,  # num_heads, num_kv_heads, head_dim, block_size
         c_f32, c_i32,           # scale, dtype
         c_vp, c_i64, c_vp, c_i64,  # k_new, k_row_stride, v_new, v_row_stride
-        c_vp, c_sz, c_vp,       # workspace, workspace_bytes, stream
+        c_vp, c_sz,             # workspace, workspace_bytes
+        c_vp, c_vp,             # device_counts, stream
     ]),
     "tb_block_copy": (c_i32, [c_vp, c_i32, c_i64, c_vp, c_vp, c_i32, c_i64, c_vp]),
     "tb_block_gather": (c_i32, [c_vp, c_i64, c_vp, c_i32, c_vp, c_i64, c_vp]),
     "tb_block_scatter": (c_i32, [c_vp, c_vp, c_i64, c_vp, c_i32, c_i64, c_vp]),
+    "tb_rms_norm": (c_i32, [c_vp, c_i64, c_vp, c_i64, c_vp, c_vp, c_i64, c_i32, c_i32, c_f32, c_i32, c_vp]),
+    "tb_rope_qk": (c_i32, [c_vp, c_i64, c_vp, c_vp, c_vp, c_i32, c_vp, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32,
+                           c_vp]),
+    "tb_silu_mul": (c_i32, [c_vp, c_i64, c_vp, c_i64, c_i32, c_i32, c_i32, c_vp]),
 }
 
 _LIB: ctypes.CDLL | None = None

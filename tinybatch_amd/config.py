@@ -26,6 +26,8 @@ class EngineConfig:
     temperature: float = 0.0
     top_p: float = 1.0
     stop_token_ids: tuple = field(default_factory=tuple)
+    # decode-only steps replay a captured HIP graph per batch-size bucket
+    decode_graphs: bool = True
     # random-init weights
     seed: int = 0
 

@@ -75,6 +75,7 @@ struct attn_args {
   const int32_t* row_part_off;
   const int4* tiles;      // prefill tiles (row0, seq, rows, pos0)
   const int32_t* split_rows;
+  const int32_t* counts;  // optional: work items, split rows, tiles present (grids are capacities)
   float* ws_acc;          // [parts][Hq][D]
   float* ws_ml;           // [parts][Hq][2]
   int32_t num_heads;
@@ -153,6 +154,7 @@ __global__ __launch_bounds__(64) void paged_attn_valu_kernel(const attn_args a) 
   const int j = lane % LPT;  // 16-byte column of the token row
   const int g = lane / LPT;  // token slot inside one wave load
 
+  if (a.counts && (int)blockIdx.x >= a.counts[0]) return;   // beyond this step's work items
   const int4 wi = a.work[blockIdx.x];   // one row per item on this path
   const int row = wi.x, seq = wi.y, part = wi.z & 0xFFFFFF, ctx = wi.w;
   const int kvh = blockIdx.y;
@@ -321,6 +323,7 @@ void paged_attn_mfma_kernel(const attn_args a) {
   // Work item: rows row0 .. row0+nrows-1 of one sequence (consecutive query
   // rows, row_ctx ctx0, ctx0+1, ...), one partition. The 16 MFMA columns are
   // (row, head) pairs: column c = qi*R + h. Decode rows come one per item.
+  if (a.counts && (int)blockIdx.x >= a.counts[0]) return;   // whole workgroup: beyond this step's items
   const int4 wi = a.work[blockIdx.x];
   const int row0 = wi.x, seq = wi.y, part = wi.z & 0xFFFFFF, nrows = (wi.z >> 24) + 1, ctx0 = wi.w;
   const int kvh = blockIdx.y;
@@ -584,6 +587,7 @@ void paged_prefill_mfma_kernel(const attn_args a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lc = lane & 15, lg = lane >> 4;
   const int item = blockIdx.x / a.num_heads;
   const int head = blockIdx.x - item * a.num_heads;
+  if (a.counts && item >= a.counts[2]) return;   // whole workgroup: beyond this step's tiles
   const int4 ti = a.tiles[item];
   const int row0 = ti.x, seq = ti.y, nrows = ti.z & 0xFF, part = ti.z >> 8, pos0 = ti.w;
   const int kvh = head / a.rep;
@@ -775,6 +779,7 @@ template <typename Tag, int D>
 __global__ __launch_bounds__(256) void combine_partials_kernel(const attn_args a) {
   constexpr int EB = elem<Tag>::bytes;
   constexpr int QPH = D / 4;                       // float4 columns per head
+  if (a.counts && (int)blockIdx.x >= a.counts[1]) return;   // beyond this step's split rows
   const int row = a.split_rows[blockIdx.x];
   const int pbeg = a.row_part_off[row];
   const int n = a.row_part_off[row + 1] - pbeg;
@@ -924,7 +929,8 @@ extern "C" int32_t tb_paged_attention(const void* q, int64_t q_row_stride, void*
                                       int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                                       float scale, int32_t dtype, const void* k_new,
                                       int64_t k_row_stride, const void* v_new, int64_t v_row_stride,
-                                      void* workspace, size_t workspace_bytes, hipStream_t stream) {
+                                      void* workspace, size_t workspace_bytes,
+                                      const int32_t* device_counts, hipStream_t stream) {
   using namespace tb;
   const int eb = elem_bytes(dtype);
   TB_CHECK_ARG(eb > 0);
@@ -977,6 +983,7 @@ extern "C" int32_t tb_paged_attention(const void* q, int64_t q_row_stride, void*
   a.row_part_off = row_part_offsets;
   a.tiles = reinterpret_cast<const int4*>(prefill_tiles);
   a.split_rows = split_rows;
+  a.counts = device_counts;
   // workspace: [acc partials: parts x Hq x D][max/sum partials: parts x Hq x 2]
   a.ws_acc = (float*)workspace;
   a.ws_ml = workspace ? a.ws_acc + (size_t)total_partitions * num_heads * head_dim : nullptr;

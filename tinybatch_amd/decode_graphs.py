@@ -1,0 +1,165 @@
+"""HIP-graph replays of decode-only engine steps.
+
+A decode step of B running sequences is the same chain of ~240 launches every
+time (24 layers of norm, projections, RoPE, fused append + paged attention,
+MLP); only the metadata changes. Each batch-size bucket (B padded up) gets one
+graph, captured once, whose launches read fixed device buffers:
+
+* tokens and positions [Bmax];
+* the step metadata at fixed capacities — slot mapping, block tables
+  [Bmax, ceil(max_model_len / BS)], work items for every partition a row can
+  have, partition offsets, split rows — plus the device counts the attention
+  kernels read at run time (tb_paged_attention's device_counts), so a launch
+  sized for the capacities only runs this step's work items;
+* the output token ids (argmax inside the graph).
+
+Per step the host packs the metadata (the same builder as the eager path)
+into one pinned staging buffer, copies it with one host-to-device copy, and
+replays. Padded rows get no work items and slot -1: they read nothing and
+write nothing, and their outputs are ignored.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from . import ops
+from .kv_cache import PagedKVCache
+from .metadata import StepMetadata, build_step_metadata
+from .model import Qwen2Paged
+
+DEFAULT_BUCKETS = (1, 2, 4, 8, 16, 24, 32, 48, 64, 96, 128, 192, 256)
+
+
+class DecodeGraphs:
+    def __init__(self, model: Qwen2Paged, kv_cache: PagedKVCache, max_batch: int, max_model_len: int,
+                 buckets=DEFAULT_BUCKETS):
+        self.model, self.cache = model, kv_cache
+        self.dev = kv_cache.device
+        c = model.cfg
+        self.BS = kv_cache.block_size
+        self.P = kv_cache.partition_tokens
+        self.max_nb = -(-max_model_len // self.BS)
+        self.max_parts = -(-max_model_len // self.P)
+        self.buckets = sorted({b for b in buckets if b < max_batch} | {max_batch})
+        B = self.buckets[-1]
+        self.wcap = B * self.max_parts
+        # int32 layout: slot [B] | tables [B*max_nb] | work [wcap*4] | row_part_off [B+1] | split [B] | counts [4]
+        sizes = [B, B * self.max_nb, self.wcap * 4, B + 1, B, 4]
+        self.offs = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
+        n = int(self.offs[-1])
+        self.dev_i32 = torch.zeros(n, dtype=torch.int32, device=self.dev)
+        self.host_i32 = torch.zeros(n, dtype=torch.int32).pin_memory()
+        self.host_np = self.host_i32.numpy()
+        self.tok = torch.zeros(B, dtype=torch.int64, device=self.dev)
+        self.pos = torch.zeros(B, dtype=torch.int64, device=self.dev)
+        self.host_tp = torch.zeros(2, B, dtype=torch.int64).pin_memory()
+        self.ids = torch.zeros(B, dtype=torch.int64, device=self.dev)
+        ws_bytes = ops._lib.lib().tb_paged_attention_workspace_bytes(self.wcap, c.n_heads, c.head_dim)
+        self.ws = torch.empty(max(int(ws_bytes), 16), dtype=torch.uint8, device=self.dev)
+        self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
+        self.pool = None    # graph memory pool shared by the buckets
+
+    # ---- metadata at capacity ---------------------------------------------------
+    def _view(self, i: int, n: int) -> torch.Tensor:
+        return self.dev_i32.narrow(0, int(self.offs[i]), n)
+
+    def _meta(self, Bp: int) -> StepMetadata:
+        e = np.zeros(0, np.int32)
+        m = StepMetadata(num_tokens=Bp, num_seqs=Bp, block_size=self.BS, partition_tokens=self.P,
+                         max_blocks_per_seq=self.max_nb, num_work_items=Bp * self.max_parts,
+                         total_partitions=Bp * self.max_parts, max_parts_per_row=self.max_parts,
+                         decode_only=True, rows_per_item=1, num_prefill_tiles=0, num_split_rows=Bp,
+                         slot_mapping_np=e, block_tables_np=e, work_np=e, row_part_off_np=e, row_ctx_np=e,
+                         prefill_tiles_np=e, split_rows_np=e)
+        m.slot_mapping = self._view(0, Bp)
+        m.block_tables = self._view(1, Bp * self.max_nb).view(Bp, self.max_nb)
+        m.work = self._view(2, Bp * self.max_parts * 4).view(-1, 4)
+        m.row_part_off = self._view(3, Bp + 1)
+        m.split_rows = self._view(4, Bp)
+        m.prefill_tiles = m.split_rows            # never read: no tiles in a decode step
+        m.device_counts = self._view(5, 4)
+        return m
+
+    def _pack(self, Bp: int, meta: StepMetadata) -> None:
+        """The step's metadata into the staging buffer, padded to bucket Bp."""
+        h, o = self.host_np, self.offs
+        B = meta.num_tokens
+        h[o[0]:o[0] + Bp] = -1
+        h[o[0]:o[0] + B] = meta.slot_mapping_np
+        tab = h[o[1]:o[1] + Bp * self.max_nb].reshape(Bp, self.max_nb)
+        nb = min(meta.block_tables_np.shape[1], self.max_nb)   # entries past the context are never read
+        tab[:B, :nb] = meta.block_tables_np[:B, :nb]
+        W = meta.num_work_items
+        h[o[2]:o[2] + W * 4] = meta.work_np.reshape(-1)
+        h[o[3]:o[3] + B + 1] = meta.row_part_off_np
+        h[o[3] + B + 1:o[3] + Bp + 1] = meta.row_part_off_np[-1]
+        S = meta.num_split_rows
+        h[o[4]:o[4] + S] = meta.split_rows_np
+        h[o[5]:o[5] + 4] = (W, S, 0, 0)
+
+    # ---- the captured step -------------------------------------------------------
+    @torch.inference_mode()
+    def _forward(self, Bp: int, meta: StepMetadata) -> None:
+        m, c = self.model, self.model.cfg
+
+        def attention(i, q, k, v):   # fused append + attention (a decode step)
+            return ops.paged_attention(q, self.cache.pools[i], meta, num_heads=c.n_heads, k_new=k, v_new=v,
+                                       workspace=self.ws)
+
+        x = m.run_layers(self.tok[:Bp], self.pos[:Bp], attention)
+        self.ids[:Bp].copy_(F.linear(x, m.lm_head).argmax(dim=-1))
+
+    def bucket(self, B: int) -> int | None:
+        for b in self.buckets:
+            if b >= B:
+                return b
+        return None
+
+    def _capture(self, Bp: int) -> torch.cuda.CUDAGraph:
+        meta = self._meta(Bp)
+        self.host_np[self.offs[5]:self.offs[5] + 4] = 0            # no work: warm-up launches exit at once
+        self.dev_i32.copy_(self.host_i32)
+        stream = torch.cuda.Stream(device=self.dev)
+        stream.wait_stream(torch.cuda.current_stream(self.dev))
+        with torch.cuda.stream(stream):
+            self._forward(Bp, meta)                                 # eager warm-up outside the graph
+        torch.cuda.synchronize(self.dev)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream, pool=self.pool):
+            self._forward(Bp, meta)
+        torch.cuda.synchronize(self.dev)
+        if self.pool is None:
+            self.pool = g.pool()
+        return g
+
+    def capture_all(self) -> None:
+        """Capture every bucket now (otherwise each is captured on first use)."""
+        for b in self.buckets:
+            if b not in self.graphs:
+                self.graphs[b] = self._capture(b)
+
+    def run(self, tokens: list[int], positions: list[int], block_tables: list[list[int]],
+            context_lens: list[int]) -> list[int]:
+        """Greedy next token of each decode row (one row per sequence)."""
+        B = len(tokens)
+        Bp = self.bucket(B)
+        if Bp is None:
+            raise ValueError(f"batch {B} exceeds the largest bucket {self.buckets[-1]}")
+        if max(context_lens) > self.max_nb * self.BS:
+            raise ValueError("context longer than max_model_len")
+        meta = build_step_metadata(positions, [(i, i + 1) for i in range(B)], block_tables, context_lens,
+                                   block_size=self.BS, num_blocks=self.cache.num_blocks, partition_tokens=self.P)
+        g = self.graphs.get(Bp)
+        if g is None:
+            g = self.graphs[Bp] = self._capture(Bp)
+        self._pack(Bp, meta)
+        self.host_tp[0, :B] = torch.tensor(tokens)
+        self.host_tp[1, :B] = torch.tensor(positions)
+        self.host_tp[:, B:Bp] = 0
+        self.dev_i32.copy_(self.host_i32, non_blocking=True)
+        self.tok[:Bp].copy_(self.host_tp[0, :Bp], non_blocking=True)
+        self.pos[:Bp].copy_(self.host_tp[1, :Bp], non_blocking=True)
+        g.replay()
+        return self.ids[:B].cpu().tolist()

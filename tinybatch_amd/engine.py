@@ -11,7 +11,9 @@ sequence, in that order in the flat batch (engine.py:99-120), then greedy
 MI355X-side choices: the step's metadata is built once and shared by all
 layers (the cache object memoises it on the positions tensor); greedy rows
 are sampled by one batched argmax and one device-to-host copy instead of one
-``int()`` synchronisation per sequence.
+``int()`` synchronisation per sequence; greedy decode-only steps replay a
+captured HIP graph of the whole forward (DecodeGraphs) instead of issuing
+its launches one by one.
 """
 from __future__ import annotations
 
@@ -22,6 +24,7 @@ import torch
 
 from .block_manager import BlockManager
 from .config import EngineConfig
+from .decode_graphs import DecodeGraphs
 from .kv_cache import PagedKVCache
 from .model import ModelConfig, Qwen2Paged
 from .scheduler import Request, Scheduler
@@ -51,6 +54,9 @@ class LLMEngine:
         self.eos_ids = set(self.cfg.stop_token_ids)
         self.steps = 0
         self.last_step_prefills = 0
+        self.graph_steps = 0
+        self.graphs = (DecodeGraphs(self.model, self.kv_cache, self.cfg.max_running, self.cfg.max_model_len)
+                       if self.cfg.decode_graphs else None)
 
     # ---- API -----------------------------------------------------------------
     def add_request(self, prompt_token_ids: list[int], *, max_new_tokens: int | None = None,
@@ -103,6 +109,11 @@ class LLMEngine:
         ordered = batch.prefill + batch.decode
         self.last_step_prefills = len(batch.prefill)
         token_ids, positions, seq_slices, block_tables, context_lens = self.build_step(batch.prefill, batch.decode)
+        if (self.graphs is not None and not batch.prefill and all(r.temperature <= 0.0 for r in ordered)
+                and self.graphs.bucket(len(ordered)) is not None):
+            next_ids = self.graphs.run(token_ids, positions, block_tables, context_lens)
+            self.graph_steps += 1
+            return self._finish_step(ordered, next_ids)
         tok = torch.tensor(token_ids, dtype=torch.int64).pin_memory().to(self.device, non_blocking=True)
         pos = torch.tensor(positions, dtype=torch.int64).pin_memory().to(self.device, non_blocking=True)
         # the step's metadata, built from the host lists (no device round trip) and shared by every layer
@@ -110,6 +121,9 @@ class LLMEngine:
                                     self.kv_cache.rows_per_item(self.model.cfg.n_heads), host_positions=positions)
         logits = self.model.forward(tok, pos, seq_slices, block_tables, context_lens, self.kv_cache)
         next_ids = self._sample(logits, ordered)
+        return self._finish_step(ordered, next_ids)
+
+    def _finish_step(self, ordered: list[Request], next_ids: list[int]) -> list[StepOutput]:
         now = time.perf_counter()
         outputs = []
         for req, t in zip(ordered, next_ids):
@@ -144,4 +158,4 @@ class LLMEngine:
         bm = self.block_manager
         return {"kv_pool_mb": round(self.kv_cache.memory_bytes() / 2**20, 1), "free_blocks": bm.num_free(),
                 "prefix_hit_rate": round(bm.hit_rate(), 3), "running": len(self.scheduler.running),
-                "waiting": len(self.scheduler.waiting), "steps": self.steps}
+                "waiting": len(self.scheduler.waiting), "steps": self.steps, "graph_steps": self.graph_steps}

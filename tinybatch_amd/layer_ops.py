@@ -1,0 +1,71 @@
+"""Host wrappers of the fused layer kernels (tb_rms_norm, tb_rope_qk, tb_silu_mul).
+
+They replace the PyTorch op chains of the reference's layer
+(src/tinybatch/model.py:65-80,115-154) with one launch each; see
+include/tinybatch_amd.h for the exact arithmetic.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+
+def _row_stride(name: str, t: torch.Tensor, width: int) -> int:
+    _lib.require_gpu_tensor(name, t)
+    if t.dim() != 2 or t.shape[1] < width or t.stride(1) != 1:
+        raise ValueError(f"{name} must be a 2-D tensor with contiguous rows of >= {width} elements")
+    return t.stride(0) if t.shape[0] > 1 else t.shape[1]
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, *, residual: torch.Tensor | None = None,
+             out: torch.Tensor | None = None) -> torch.Tensor:
+    """RMSNorm of x's rows (model.py:65-69). With ``residual``: residual += x
+    first (in place) and the sum is normalised (the residual add of model.py:149,154)."""
+    rows, dim = x.shape
+    xs = _row_stride("x", x, dim)
+    if weight.shape != (dim,) or weight.dtype != x.dtype or not weight.is_contiguous():
+        raise ValueError("weight must be a contiguous [dim] tensor of x's dtype")
+    rs = 0
+    if residual is not None:
+        rs = _row_stride("residual", residual, dim)
+        if residual.shape != x.shape or residual.dtype != x.dtype:
+            raise ValueError("residual must match x")
+    if out is None:
+        out = torch.empty(rows, dim, dtype=x.dtype, device=x.device)
+    os_ = _row_stride("out", out, dim)
+    st = _lib.lib().tb_rms_norm(x.data_ptr(), xs, None if residual is None else residual.data_ptr(), rs,
+                                weight.data_ptr(), out.data_ptr(), os_, rows, dim, float(eps),
+                                _lib.DTYPE_CODE[x.dtype], _lib.stream_handle(x.device))
+    _lib.check(st, "tb_rms_norm")
+    return out
+
+
+def rope_qk(qkv: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, num_heads: int,
+            num_kv_heads: int, head_dim: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Rotated q [T, Hq, D] and k [T, Hkv, D] from the q|k|v rows of the qkv GEMM (model.py:72-80)."""
+    T = qkv.shape[0]
+    rs = _row_stride("qkv", qkv, (num_heads + num_kv_heads) * head_dim)
+    if positions.dtype != torch.int64 or not positions.is_cuda or positions.numel() != T:
+        raise TypeError("positions must be an int64 GPU tensor with one entry per row")
+    for name, t in (("cos", cos), ("sin", sin)):
+        if t.dtype != torch.float32 or not t.is_cuda or not t.is_contiguous() or t.shape[1] != head_dim // 2:
+            raise TypeError(f"{name} must be a contiguous fp32 GPU table [max_position, head_dim/2]")
+    q = torch.empty(T, num_heads, head_dim, dtype=qkv.dtype, device=qkv.device)
+    k = torch.empty(T, num_kv_heads, head_dim, dtype=qkv.dtype, device=qkv.device)
+    st = _lib.lib().tb_rope_qk(qkv.data_ptr(), rs, positions.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+                               cos.shape[0], q.data_ptr(), k.data_ptr(), T, num_heads, num_kv_heads, head_dim,
+                               _lib.DTYPE_CODE[qkv.dtype], _lib.stream_handle(qkv.device))
+    _lib.check(st, "tb_rope_qk")
+    return q, k
+
+
+def silu_mul(gate_up: torch.Tensor, d_ff: int) -> torch.Tensor:
+    """silu(gate) * up for gate_up rows [gate | up] (model.py:152-154)."""
+    T = gate_up.shape[0]
+    rs = _row_stride("gate_up", gate_up, 2 * d_ff)
+    out = torch.empty(T, d_ff, dtype=gate_up.dtype, device=gate_up.device)
+    st = _lib.lib().tb_silu_mul(gate_up.data_ptr(), rs, out.data_ptr(), d_ff, T, d_ff,
+                                _lib.DTYPE_CODE[gate_up.dtype], _lib.stream_handle(gate_up.device))
+    _lib.check(st, "tb_silu_mul")
+    return out

@@ -72,6 +72,8 @@ class StepMetadata:
     row_part_off: torch.Tensor | None = None
     prefill_tiles: torch.Tensor | None = None
     split_rows: torch.Tensor | None = None
+    # set for capacity-sized (graph) metadata: {work items, split rows, tiles} on the device
+    device_counts: torch.Tensor | None = None
 
     def to(self, device: torch.device) -> "StepMetadata":
         """Upload every array with one host-to-device copy (views into one buffer)."""

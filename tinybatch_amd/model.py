@@ -10,9 +10,10 @@ projections with biases, o_proj, SwiGLU MLP, residuals, final norm, tied LM
 head on the last token of each sequence (model.py:153-158).
 
 MI355X-side choices: q/k/v are one GEMM over a concatenated weight (and
-gate/up another), the RoPE tables are built once for every position up to
-max_position, and the final norm and LM head run on the last rows only (the
-norm is per row, so this equals norming every row and selecting).
+gate/up another); the residual add + RMSNorm, the RoPE of q and k and the
+SwiGLU gate are one fused kernel each (layer_ops) instead of chains of tensor
+ops; the RoPE tables are built once for every position up to max_position;
+the LM head runs on the last rows only.
 
 Weights are drawn from a seeded generator (no checkpoint exists offline):
 N(0, 0.02) for embeddings, projections and biases, ones for the norms.
@@ -25,6 +26,7 @@ from dataclasses import dataclass
 import torch
 import torch.nn.functional as F
 
+from . import layer_ops
 from .kv_cache import PagedKVCache
 
 
@@ -58,25 +60,11 @@ class ModelConfig:
         return self.vocab_size * self.d_model + self.n_layers * per_layer + self.d_model + head
 
 
-def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
-    """model.py:65-69: normalise in fp32, scale, cast back."""
-    xf = x.float()
-    xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
-    return (xf * weight.float()).to(x.dtype)
-
-
 def rope_tables(head_dim: int, theta: float, max_position: int, device) -> tuple[torch.Tensor, torch.Tensor]:
     """cos / sin [max_position, head_dim/2] with the reference's fp32 arithmetic (model.py:74-76)."""
     inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, device=device).float() / head_dim))
     freqs = torch.arange(max_position, device=device).float()[:, None] * inv_freq[None, :]
     return freqs.cos(), freqs.sin()
-
-
-def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
-    """Rotate-half RoPE (model.py:77-80); x [T, heads, D], cos/sin [T, D/2]."""
-    c, s = cos[:, None, :], sin[:, None, :]
-    x1, x2 = x.float().chunk(2, dim=-1)
-    return torch.cat((x1 * c - x2 * s, x2 * c + x1 * s), dim=-1).to(x.dtype)
 
 
 class Qwen2Paged:
@@ -124,26 +112,33 @@ class Qwen2Paged:
             w[p + "mlp.down_proj.weight"] = L["w_down"]
         return w
 
+    def run_layers(self, token_ids: torch.Tensor, positions: torch.Tensor, attention) -> torch.Tensor:
+        """Hidden states after the final norm, [T, d_model]. ``attention(layer, q, k, v)``
+        appends the step's K/V and returns attn_out [T, Hq*D] (model.py:127-147)."""
+        c = self.cfg
+        T = token_ids.shape[0]
+        hq, hk = c.n_heads * c.head_dim, c.n_kv_heads * c.head_dim
+        h = F.embedding(token_ids, self.embed)                       # the residual stream
+        x = layer_ops.rms_norm(h, self.layers[0]["ln1"], c.rms_eps)
+        for i, L in enumerate(self.layers):
+            qkv = F.linear(x, L["w_qkv"], L["b_qkv"])
+            q, k = layer_ops.rope_qk(qkv, positions, self.cos, self.sin, c.n_heads, c.n_kv_heads, c.head_dim)
+            v = qkv[:, hq + hk:].view(T, c.n_kv_heads, c.head_dim)
+            attn = attention(i, q, k, v)
+            x = layer_ops.rms_norm(F.linear(attn, L["w_o"]), L["ln2"], c.rms_eps, residual=h)
+            act = layer_ops.silu_mul(F.linear(x, L["w_gu"]), c.d_ff)
+            nxt = self.layers[i + 1]["ln1"] if i + 1 < len(self.layers) else self.norm
+            x = layer_ops.rms_norm(F.linear(act, L["w_down"]), nxt, c.rms_eps, residual=h)
+        return x
+
     @torch.inference_mode()
     def forward(self, token_ids: torch.Tensor, positions: torch.Tensor, seq_slices: list[tuple[int, int]],
                 block_tables: list[list[int]], context_lens: list[int], kv_cache: PagedKVCache) -> torch.Tensor:
         """Logits [n_seqs, vocab] (fp32) for the last token of each sequence (model.py:101-158)."""
-        c = self.cfg
-        T = token_ids.shape[0]
-        hq, hk = c.n_heads * c.head_dim, c.n_kv_heads * c.head_dim
-        cos, sin = self.cos[positions], self.sin[positions]
-        h = F.embedding(token_ids, self.embed)
-        for i, L in enumerate(self.layers):
-            x = rms_norm(h, L["ln1"], c.rms_eps)
-            qkv = F.linear(x, L["w_qkv"], L["b_qkv"])
-            q = apply_rope(qkv[:, :hq].view(T, c.n_heads, c.head_dim), cos, sin)
-            k = apply_rope(qkv[:, hq:hq + hk].view(T, c.n_kv_heads, c.head_dim), cos, sin)
-            v = qkv[:, hq + hk:].view(T, c.n_kv_heads, c.head_dim)
+        def attention(i, q, k, v):
             kv_cache.write(i, k, v, positions, seq_slices, block_tables)
-            attn = kv_cache.attention(i, q, positions, seq_slices, block_tables, context_lens)
-            h = h + F.linear(attn, L["w_o"])
-            x = rms_norm(h, L["ln2"], c.rms_eps)
-            gate, up = F.linear(x, L["w_gu"]).split(c.d_ff, dim=-1)
-            h = h + F.linear(F.silu(gate) * up, L["w_down"])
-        last = torch.tensor([e - 1 for _, e in seq_slices], device=h.device)
-        return F.linear(rms_norm(h[last], self.norm, c.rms_eps), self.lm_head).float()
+            return kv_cache.attention(i, q, positions, seq_slices, block_tables, context_lens)
+
+        x = self.run_layers(token_ids, positions, attention)
+        last = torch.tensor([e - 1 for _, e in seq_slices], device=x.device)
+        return F.linear(x[last], self.lm_head).float()

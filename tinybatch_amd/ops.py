@@ -189,7 +189,7 @@ def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, 
         meta.split_rows.data_ptr(), meta.num_split_rows,
         max(meta.max_parts_per_row, 1), meta.partition_tokens, meta.total_partitions,
         num_heads, hkv, d, bs, float(scale), _lib.DTYPE_CODE[q.dtype],
-        ksp, ks, vsp, vs, _ptr(ws), ws_bytes, _lib.stream_handle(q.device))
+        ksp, ks, vsp, vs, _ptr(ws), ws_bytes, _ptr(meta.device_counts), _lib.stream_handle(q.device))
     _lib.check(st, "tb_paged_attention")
     return out
 
