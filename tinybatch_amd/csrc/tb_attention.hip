@@ -772,9 +772,10 @@ void paged_prefill_mfma_kernel(const attn_args a) {
 }
 
 // ---------------------------------------------------------------------------
-// Log-sum-exp merge of the partials of one split row, all heads: one
-// workgroup of 256 threads, thread t owns 4 consecutive output dims (head
-// (t + 256 k) / (D/4)); every partial of the row is read once, in parallel.
+// Log-sum-exp merge of the partials of one split row: workgroup (r, c) owns
+// 256 float4 columns (4 consecutive output dims each, head = column / (D/4))
+// of split row r, starting at column 256 c; every partial is read once, in
+// batches of 8 whose loads are all in flight.
 template <typename Tag, int D>
 __global__ __launch_bounds__(256) void combine_partials_kernel(const attn_args a) {
   constexpr int EB = elem<Tag>::bytes;
@@ -784,7 +785,8 @@ __global__ __launch_bounds__(256) void combine_partials_kernel(const attn_args a
   const int pbeg = a.row_part_off[row];
   const int n = a.row_part_off[row + 1] - pbeg;
   char* orow = a.out + row * a.out_row_bytes;
-  for (int col = threadIdx.x; col < a.num_heads * QPH; col += 256) {
+  const int col = threadIdx.x + 256 * blockIdx.y;
+  if (col < a.num_heads * QPH) {
     const int head = col / QPH, d4 = col - head * QPH;
     // batches of 8 partials, all loads of a batch in flight, merged online
     float M = -INFINITY, L = 0.f;
@@ -862,7 +864,8 @@ static void launch_mfma(const attn_args& a, int num_work, hipStream_t stream) {
 template <typename Tag, int D>
 static void launch_combine(const attn_args& a, int num_split_rows, hipStream_t stream) {
   if (num_split_rows > 0)
-    hipLaunchKernelGGL((combine_partials_kernel<Tag, D>), dim3(num_split_rows), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((combine_partials_kernel<Tag, D>), dim3(num_split_rows, (a.num_heads * (D / 4) + 255) / 256),
+                       dim3(256), 0, stream, a);
 }
 
 template <typename Tag, int D>
