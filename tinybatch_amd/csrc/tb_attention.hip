@@ -304,7 +304,12 @@ struct mfma_shape {
   static_assert(TILES % (2 * HALVES) == 0 && P % CT == 0 && VLD % HALVES == 0, "chunk shape");
 };
 
-template <typename Tag, int D>
+// Loads of one kv head's K/V rows. UT ("uniform tiles", block_size >= 16):
+// every 16-position K tile and every V row group of a wave lies inside one
+// block, so the block id and the tile base are wave-uniform (a scalar table
+// read and scalar address arithmetic per tile); otherwise each lane looks its
+// block up in a per-lane copy of the partition's table entries.
+template <typename Tag, int D, bool UT>
 __global__ __launch_bounds__(64 * mfma_shape<D>::NW) __attribute__((amdgpu_waves_per_eu(5)))
 void paged_attn_mfma_kernel(const attn_args a) {
   using S = mfma_shape<D>;
@@ -323,10 +328,14 @@ void paged_attn_mfma_kernel(const attn_args a) {
   // Work item: rows row0 .. row0+nrows-1 of one sequence (consecutive query
   // rows, row_ctx ctx0, ctx0+1, ...), one partition. The 16 MFMA columns are
   // (row, head) pairs: column c = qi*R + h. Decode rows come one per item.
-  if (a.counts && (int)blockIdx.x >= a.counts[0]) return;   // whole workgroup: beyond this step's items
-  const int4 wi = a.work[blockIdx.x];
+  // The kv head varies fastest across the grid: the workgroups reading the K
+  // and V tiles of the same blocks for the two (or more) kv heads run side by
+  // side, so each block's bytes are fetched close together in time.
+  const int item = blockIdx.x / a.num_kv_heads;
+  const int kvh = blockIdx.x - item * a.num_kv_heads;
+  if (a.counts && item >= a.counts[0]) return;   // whole workgroup: beyond this step's items
+  const int4 wi = a.work[item];
   const int row0 = wi.x, seq = wi.y, part = wi.z & 0xFFFFFF, nrows = (wi.z >> 24) + 1, ctx0 = wi.w;
-  const int kvh = blockIdx.y;
   const int R = a.group;                    // heads of this workgroup; nrows * R <= 16
   const int head0 = kvh * a.rep + blockIdx.z * R;
   const int p0 = part * P;
@@ -339,13 +348,6 @@ void paged_attn_mfma_kernel(const attn_args a) {
   const bool busy = wb < n;                // wave 0 always is
   const int bs = 1 << a.log2_bs;
 
-  // Block-table entries of this partition: lane l holds entry p0/BS + l.
-  const int blk_count = ((n - 1) >> a.log2_bs) + 1;   // <= 64: BS >= 4
-  int my_blk = 0;
-  if (lane < blk_count) {
-    my_blk = a.block_tables[(int64_t)seq * a.max_nb + (p0 >> a.log2_bs) + lane];
-    if (my_blk < 0 || my_blk >= a.num_blocks) my_blk = 0;  // host validates; stay inside the pool
-  }
   const int64_t tile_bytes = (int64_t)bs * RB;
   const int64_t blk_bytes = 2 * (int64_t)a.num_kv_heads * tile_bytes;
   const int64_t v_off = (int64_t)a.num_kv_heads * tile_bytes;
@@ -354,31 +356,59 @@ void paged_attn_mfma_kernel(const attn_args a) {
   const int new_tau = ctx - 1 - p0;         // partition-relative index of the newest position
   const char* k_new_row = fused ? a.k_new + row0 * a.k_new_row_bytes + (int64_t)kvh * RB : nullptr;
   const char* v_new_row = fused ? a.v_new + row0 * a.v_new_row_bytes + (int64_t)kvh * RB : nullptr;
-  // Pool offset of position p0+tau (this kv head). Shuffles: every lane runs it.
-  auto pos_off = [&](int tau) -> int64_t {
+
+  // Pool addresses: K tile t (A operand: lane holds position wb+16t+lc, bytes
+  // 64s+16lg) and V row group i (16-byte column lane%VCOLS of row VT*i + lane/VCOLS),
+  // recomputed where used so that no per-lane 64-bit pointer stays live.
+  char* tile_base[TILES];   // UT: wave-uniform start of tile t in the pool
+  int my_blk = 0;           // otherwise: lane l holds the partition's table entry p0/BS + l
+  if constexpr (UT) {
+    const int32_t* tbl = a.block_tables + (int64_t)seq * a.max_nb;
+    const int wbu = __builtin_amdgcn_readfirstlane(wb);
+#pragma unroll
+    for (int t = 0; t < TILES; ++t) {
+      const int pt = p0 + wbu + 16 * t;     // the tile's first position (wave-uniform)
+      int blk = 0;
+      if (wbu + 16 * t < n) {               // entries past the context are never read
+        blk = tbl[pt >> a.log2_bs];
+        if (blk < 0 || blk >= a.num_blocks) blk = 0;   // host validates; stay inside the pool
+      }
+      tile_base[t] = pool_kvh + (int64_t)blk * blk_bytes + (int64_t)(pt & (bs - 1)) * RB;
+    }
+  } else {
+    const int blk_count = ((n - 1) >> a.log2_bs) + 1;   // <= 64: BS >= 4
+    if (lane < blk_count) {
+      my_blk = a.block_tables[(int64_t)seq * a.max_nb + (p0 >> a.log2_bs) + lane];
+      if (my_blk < 0 || my_blk >= a.num_blocks) my_blk = 0;
+    }
+  }
+  auto pos_off = [&](int tau) -> int64_t {   // generic path; shuffles: every lane runs it
     const int blk = __shfl(my_blk, (tau >> a.log2_bs) & 63);
     return (int64_t)blk * blk_bytes + (int64_t)(tau & (bs - 1)) * RB;
   };
+  auto k_at = [&](int t) -> char* {
+    if constexpr (UT) return tile_base[t] + (lc * RB + 16 * lg);
+    else return pool_kvh + pos_off(wb + 16 * t + lc) + 16 * lg;
+  };
+  auto v_at = [&](int i) -> char* {
+    if constexpr (UT) return tile_base[(VT * i) / 16] + (v_off + ((VT * i) % 16 + lane / VCOLS) * RB + 16 * (lane % VCOLS));
+    else return pool_kvh + v_off + pos_off(wb + VT * i + lane / VCOLS) + 16 * (lane % VCOLS);
+  };
 
-  // K tiles (A operand: lane holds position wb+16t+lc, bytes 64s+16lg) and V rows
-  // (16-byte column lane%VCOLS of row VT*i + lane/VCOLS), all issued now.
+  // all of the wave's K and V loads are issued now
   vec16 kd[TILES][KS], vd[VLD];
   if (busy) {
 #pragma unroll
     for (int t = 0; t < TILES; ++t) {
       const int tau = wb + 16 * t + lc;
-      const int64_t off = pos_off(tau);
-      const char* src = pool_kvh + off + 16 * lg;
-      if (fused && tau == new_tau) src = k_new_row + 16 * lg;
+      const char* src = (fused && tau == new_tau) ? k_new_row + 16 * lg : k_at(t);
 #pragma unroll
       for (int s = 0; s < KS; ++s) kd[t][s] = (tau < n) ? ld16_stream(src + 64 * s) : zero16();
     }
 #pragma unroll
     for (int i = 0; i < VLD; ++i) {
       const int tau = wb + VT * i + lane / VCOLS;
-      const int64_t off = pos_off(tau);
-      const char* src = pool_kvh + v_off + off + 16 * (lane % VCOLS);
-      if (fused && tau == new_tau) src = v_new_row + 16 * (lane % VCOLS);
+      const char* src = (fused && tau == new_tau) ? v_new_row + 16 * (lane % VCOLS) : v_at(i);
       vd[i] = (tau < n) ? ld16_stream(src) : zero16();
     }
   }
@@ -404,19 +434,14 @@ void paged_attn_mfma_kernel(const attn_args a) {
     if (fused) {   // the newest position's K/V rows go to their pool slot
 #pragma unroll
       for (int t = 0; t < TILES; ++t) {
-        const int tau = wb + 16 * t + lc;
-        const int64_t off = pos_off(tau);
-        if (tau == new_tau) {
+        if (wb + 16 * t + lc == new_tau) {
 #pragma unroll
-          for (int s = 0; s < KS; ++s) st16(pool_kvh + off + 16 * lg + 64 * s, kd[t][s]);
+          for (int s = 0; s < KS; ++s) st16(k_at(t) + 64 * s, kd[t][s]);
         }
       }
 #pragma unroll
-      for (int i = 0; i < VLD; ++i) {
-        const int tau = wb + VT * i + lane / VCOLS;
-        const int64_t off = pos_off(tau);
-        if (tau == new_tau) st16(pool_kvh + v_off + off + 16 * (lane % VCOLS), vd[i]);
-      }
+      for (int i = 0; i < VLD; ++i)
+        if (wb + VT * i + lane / VCOLS == new_tau) st16(v_at(i), vd[i]);
     }
 #pragma unroll
     for (int t = 0; t < TILES; ++t) {
@@ -434,8 +459,7 @@ void paged_attn_mfma_kernel(const attn_args a) {
         sc[t][j] = v;
         cm = fmaxf(cm, v);
       }
-    cm = fmaxf(cm, __shfl_xor(cm, 16));
-    m_w = fmaxf(cm, __shfl_xor(cm, 32));
+    m_w = max_xor32(max_xor16(cm));
     // a column whose visible positions all lie before this wave's range gets p = 0
     const float m_safe = m_w == -INFINITY ? 0.f : m_w;
 #pragma unroll
@@ -469,16 +493,15 @@ void paged_attn_mfma_kernel(const attn_args a) {
         pa[j] = (scalar_t)sc[2 * u][j];
         pa[4 + j] = (scalar_t)sc[2 * u + 1][j];
       }
-      const char* vbase = vl + (32 * u - hf * S::HALF + 4 * lg) * RS + 2 * lc;
+      // B operand lane (lg, lc): V[position of k = 8lg + j][16nn + lc], two transpose reads
+      const char* vsrc = vl + (32 * u - hf * S::HALF + 4 * lg + (lc >> 2)) * RS + 8 * (lc & 3);
 #pragma unroll
       for (int nn = 0; nn < NSL; ++nn) {
-        vec8_t vb;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          vb[j] = *reinterpret_cast<const scalar_t*>(vbase + j * RS + 32 * nn);
-          vb[4 + j] = *reinterpret_cast<const scalar_t*>(vbase + (16 + j) * RS + 32 * nn);
-        }
-        acc[nn] = M::mfma(pa, vb, acc[nn]);
+        const uint2 lo = lds_read_tr16(vsrc + 32 * nn);            // positions 32u + 4lg + 0..3
+        const uint2 hi = lds_read_tr16(vsrc + 16 * RS + 32 * nn);  // positions 32u + 16 + 4lg + 0..3
+        vec16 vb;
+        vb.w[0] = lo.x; vb.w[1] = lo.y; vb.w[2] = hi.x; vb.w[3] = hi.y;
+        acc[nn] = M::mfma(pa, __builtin_bit_cast(vec8_t, vb), acc[nn]);
       }
     }
     }
@@ -857,8 +880,11 @@ static int dispatch_valu_rep(const attn_args& a, int num_work, hipStream_t s) {
 
 template <typename Tag, int D>
 static void launch_mfma(const attn_args& a, int num_work, hipStream_t stream) {
-  hipLaunchKernelGGL((paged_attn_mfma_kernel<Tag, D>), dim3(num_work, a.num_kv_heads, a.rep / a.group),
-                     dim3(64 * mfma_shape<D>::NW), 0, stream, a);
+  const dim3 grid(num_work * a.num_kv_heads, 1, a.rep / a.group), block(64 * mfma_shape<D>::NW);
+  if (a.log2_bs >= 4)   // 16-position tiles never cross a block
+    hipLaunchKernelGGL((paged_attn_mfma_kernel<Tag, D, true>), grid, block, 0, stream, a);
+  else
+    hipLaunchKernelGGL((paged_attn_mfma_kernel<Tag, D, false>), grid, block, 0, stream, a);
 }
 
 template <typename Tag, int D>
@@ -972,6 +998,7 @@ extern "C" int32_t tb_paged_attention(const void* q, int64_t q_row_stride, void*
   // heads per wave: the MFMA operand holds 16; the fp32 kernel keeps 8 in registers
   const int group = largest_divisor_upto(rep, eb == 2 ? 16 : 8);
   TB_CHECK_ARG(num_kv_heads <= 65535 && rep / group <= 65535);
+  TB_CHECK_ARG((int64_t)num_work_items * num_kv_heads < ((int64_t)1 << 31));
 
   attn_args a;
   a.q = (const char*)q;

@@ -134,6 +134,19 @@ __device__ __forceinline__ float cross_group_sum(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// gfx950 LDS transpose read (ds_read_b64_tr_b16). Within each group of 16
+// lanes, lane i receives element (i & 3) of the 8-byte LDS rows addressed by
+// lanes (i >> 2) + 4j, j = 0..3, in that order. With lane s of a group
+// pointing at row r0 + (s >> 2), elements 4 (s & 3) .. 4 (s & 3) + 3 of a
+// row-major 16-bit matrix, lane i gets column i of rows r0 .. r0 + 3: the
+// k-contiguous operand layout of a 16x16x32 MFMA, read from row-major data.
+typedef short short4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint2 lds_read_tr16(const void* p) {
+  const short4_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) short4_t*)(const_cast<void*>(p)));
+  return __builtin_bit_cast(uint2, r);
+}
+
 // Reductions across the 16-lane rows of a wave on the VALU (gfx950 permlane
 // swaps, no LDS round trip): combine lane l with lane l ^ 16 / l ^ 32.
 __device__ __forceinline__ float max_xor16(float x) {
