@@ -106,8 +106,9 @@ int32_t tb_kv_gather(const void* pool, int64_t num_blocks,
  *     A tile row counts ceil(row_ctx/T) partitions in row_part_offsets; one
  *     item per partition its tile's last row reaches. Rows in tiles must not
  *     also appear in work items.
- *   split_rows: [num_split_rows] int32, the rows with more than one partition;
- *     their partials are merged by a combine kernel.
+ *   split_rows: [num_split_rows][4] int32 (16-byte aligned) = (row,
+ *     row_part_offsets[row], partition count, 0) of every row with more than
+ *     one partition; their partials are merged by a combine kernel.
  *   workspace: >= tb_paged_attention_workspace_bytes(total_partitions, ...)
  *     bytes of device memory (16-byte aligned) for the split-row partials;
  *     only used when a row has > 1 partition (max_parts_per_row > 1), which

@@ -272,6 +272,38 @@ def test_block_sizes_16bit(BS, dtype):
     _attention_vs_oracle(c, 16, 4, dtype)
 
 
+@pytest.mark.parametrize("BS", [4, 8, 16, 64])
+@pytest.mark.parametrize("dtype,Hq,Hkv,D", [(torch.float16, 14, 2, 64), (torch.bfloat16, 16, 4, 128)])
+def test_fused_decode_append_block_sizes(BS, dtype, Hq, Hkv, D):
+    """Fused append + attention on both address paths (block tables read per lane for
+    BS < 16, per 16-position tile otherwise); the newest position may sit in any
+    wave, partition and block offset."""
+    cached = [0, 1, 15, 63, 64, 255, 256, 700, 1023, 2047]
+    c = _mixed_case(30 + BS, Hq, Hkv, D, BS, dtype, qlens=[1] * len(cached), cached=cached)
+    pool_ref = c["pool"].clone()
+    want = ref.decode_step(pool_ref, c["q"], c["k"], c["v"], cached, c["tables"], Hq, Hkv, BS)
+    pool = c["pool"].to(DEV)
+    meta = _meta(c["pos"], c["slices"], c["tables"], c["ctx"], BS, c["NB"])
+    out = ops.paged_attention(c["q"].to(DEV), pool, meta, num_heads=Hq, k_new=c["k"].to(DEV), v_new=c["v"].to(DEV))
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out.cpu().float(), want.float(), **TOL[dtype])
+    assert torch.equal(_bits(pool.cpu()), _bits(pool_ref))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_split_rows_merge_the_same_bits_every_call(dtype):
+    """Rows over up to 20 partitions (two batches of the combine) and short rows
+    in one step; repeated calls give the same bits (the merge order is fixed)."""
+    Hq, Hkv, D = 16, 4, 128
+    c = _mixed_case(12, Hq, Hkv, D, 16, dtype, qlens=[1, 1, 1, 3], cached=[5000, 300, 2600, 1500])
+    meta = _meta(c["pos"], c["slices"], c["tables"], c["ctx"], 16, c["NB"])
+    assert meta.max_parts_per_row == 20 and meta.num_split_rows == 6
+    q, pool = c["q"].to(DEV), c["pool"].to(DEV)
+    outs = [ops.paged_attention(q, pool, meta, num_heads=Hq).cpu() for _ in range(3)]
+    assert all(torch.equal(_bits(outs[0]), _bits(o)) for o in outs[1:])
+    _attention_vs_oracle(c, Hq, Hkv, dtype)
+
+
 def test_golden_fixture_decode_fp32():
     """GPU decode step of the committed fixture (inputs regenerated from its seed)."""
     import os

@@ -136,7 +136,9 @@ def test_prefill_tiles_cover_tiled_rows_most_positions_first():
     for r in range(t):   # tile rows count tile partitions, work-item rows count P-position ones
         assert counts[r] == -(-int(m.row_ctx_np[r]) // (TP if r in tiled else P))
     assert m.total_partitions == int(counts.sum())
-    assert m.split_rows_np.tolist() == [r for r in range(t) if counts[r] > 1]
+    assert m.split_rows_np[:, 0].tolist() == [r for r in range(t) if counts[r] > 1]
+    for r, pbeg, n, z in m.split_rows_np.tolist():   # combine records: first slot and count
+        assert (pbeg, n, z) == (m.row_part_off_np[r], counts[r], 0)
     # fp32 metadata (no tiles) keeps every row in work items
     m32 = build_step_metadata(positions, slices, tables, ctx, block_size=16, num_blocks=at,
                               partition_tokens=P)
@@ -161,4 +163,4 @@ def test_long_prefill_tiles_span_tile_partitions():
     want = sum(-(-min(n, 64 * (t + 1)) // TILE_PARTITION) for t in range(ntiles))
     assert len(items) == want
     assert m.max_parts_per_row == 3
-    assert m.split_rows_np.tolist() == [r for r in range(n) if r + 1 > TILE_PARTITION]
+    assert m.split_rows_np[:, 0].tolist() == [r for r in range(n) if r + 1 > TILE_PARTITION]

@@ -6,32 +6,33 @@
 // offset-causal mask j <= ctx - q_len + i (model.py:139-145) and
 // scaled_dot_product_attention with scale 1/sqrt(D) (model.py:140,146).
 //
-// Work decomposition: one wave64 = one work item = (query row, kv head, head
-// group, partition of P positions). The wave reads each visible K/V row of its
-// partition once, in place through the block table, and serves every query
-// head of its GQA group from that one read (no repeat_interleave, no gathered
-// copy). A row longer than P is split over several waves that write
-// (max, sum, unnormalised acc) partials; combine_partials_kernel merges them
-// with a log-sum-exp (kernel boundaries make the partials visible across XCDs).
+// Work decomposition: one workgroup = one work item = (query rows of one
+// sequence, kv head, head group, partition of P positions). Each K/V row of the
+// partition is read once, in place through the block table, and serves every
+// query head of the GQA group (no repeat_interleave, no gathered copy). A row
+// longer than P is split over several workgroups that store (max, sum,
+// unnormalised acc) partials; combine_partials_kernel merges them with a
+// log-sum-exp (the kernel boundary makes the partials visible across XCDs).
 //
-// fp16 / bf16 (the hot path): paged_attn_mfma_kernel. The GQA group (up to 16
-// heads, padded) is one MFMA operand, so q.K^T and p.V are
+// fp16 / bf16 (the hot path): paged_attn_mfma_kernel, P/CT waves of CT
+// positions each, every wave issuing all of its loads at once. The GQA group
+// (up to 16 heads, padded) is one MFMA operand, so q.K^T and p.V are
 // v_mfma_f32_16x16x32_{f16,bf16} over 16-position tiles:
 //   S^T[pos][head] = K[pos][:] . Q[head][:]   A = K rows straight from the pool
 //                                              B = q (registers, loaded once)
 //   O[head][dv]   += P[head][pos] . V[pos][dv] A = p (the S^T tile registers,
-//                                              repacked in place), B = V read
-//                                              column-wise from an LDS copy
-// The online softmax runs per 64-position chunk on the S^T tiles (max / sum
-// across the four 16-lane groups by shuffles); loads of chunk c+1 are in
-// flight while chunk c is computed.
+//                                              repacked in place), B = V rows
+//                                              loaded into LDS directly, read
+//                                              transposed
+// and the waves' softmax states merge in LDS.
 // Prefill tiles (fp16 / bf16): paged_prefill_mfma_kernel, a flash-style
 // workgroup per (64 query rows of one sequence, query head) that walks the
 // causal range in 64-position chunks staged in LDS (see the kernel).
 // fp32: paged_attn_valu_kernel, fp32 FMAs on the VALU (no fp32 MFMA of the
 // needed precision on CDNA4), same decomposition.
-// Positions >= the row's context are never loaded (stale slots may hold any
-// bits, NaN included): their scores are -inf and their V rows zero.
+// Positions >= the row's context are never loaded from the pool (stale slots
+// may hold any bits, NaN included): their scores are -inf, so p = 0, and what
+// stands in for their V rows is finite.
 #include "tb_common.h"
 
 namespace tb {
@@ -74,7 +75,7 @@ struct attn_args {
   const int4* work;       // (row, seq, part, row_ctx)
   const int32_t* row_part_off;
   const int4* tiles;      // prefill tiles (row0, seq, rows, pos0)
-  const int32_t* split_rows;
+  const int4* split_rows;  // (row, first partial slot, partial count, 0)
   const int32_t* counts;  // optional: work items, split rows, tiles present (grids are capacities)
   float* ws_acc;          // [parts][Hq][D]
   float* ws_ml;           // [parts][Hq][2]
@@ -90,6 +91,7 @@ struct attn_args {
   const char* v_new;
   int64_t v_new_row_bytes;
 };
+
 
 // ---------------------------------------------------------------------------
 // fp32 path: single pass, online softmax per chunk, fp32 FMAs.
@@ -154,8 +156,8 @@ __global__ __launch_bounds__(64) void paged_attn_valu_kernel(const attn_args a) 
   const int j = lane % LPT;  // 16-byte column of the token row
   const int g = lane / LPT;  // token slot inside one wave load
 
+  const int4 wi = a.work[blockIdx.x];   // one row per item on this path; the array holds the grid's capacity
   if (a.counts && (int)blockIdx.x >= a.counts[0]) return;   // beyond this step's work items
-  const int4 wi = a.work[blockIdx.x];   // one row per item on this path
   const int row = wi.x, seq = wi.y, part = wi.z & 0xFFFFFF, ctx = wi.w;
   const int kvh = blockIdx.y;
   const int head0 = kvh * a.rep + blockIdx.z * REP;
@@ -295,13 +297,14 @@ struct mfma_shape {
   static constexpr int VCOLS = RB / 16;      // 16-byte columns of a row
   static constexpr int VT = 64 / VCOLS;      // rows per V load instruction
   static constexpr int VLD = CT / VT;        // V loads per lane
-  static constexpr int RS = RB + 8;          // LDS row stride: column reads hit 32 distinct banks
-  static constexpr int HALVES = (TILES % 4 == 0) ? 2 : 1;   // V staged in LDS in HALVES parts
-  static constexpr int HALF = CT / HALVES;   // V positions staged at a time
-  static constexpr int STAGE = HALF * RS;    // V staging bytes per wave
+  static constexpr int VST = CT * RB;        // V rows of one wave in LDS (loaded there directly)
   static constexpr int MERGE = 16 * D * 4;   // per-wave acc bytes in the merge
-  static constexpr int LDS = NW * (STAGE > MERGE ? STAGE : MERGE);
-  static_assert(TILES % (2 * HALVES) == 0 && P % CT == 0 && VLD % HALVES == 0, "chunk shape");
+  static constexpr int ML = NW * 16 * 8;     // per-column (max, sum) of every wave, after the acc area
+  static constexpr int LDS = (NW * VST > NW * MERGE + ML) ? NW * VST : NW * MERGE + ML;
+  static_assert(TILES % 2 == 0 && P % CT == 0 && VT * RB == 1024, "chunk shape");
+  // V row r of a wave keeps its 16-byte chunk c in slot c ^ swz(r): the transpose
+  // reads of P.V (4 rows x 32 bytes per 16 lanes) then hit distinct banks.
+  static __device__ __forceinline__ int swz(int r) { return 2 * (r & 3); }
 };
 
 // Loads of one kv head's K/V rows. UT ("uniform tiles", block_size >= 16):
@@ -317,10 +320,10 @@ void paged_attn_mfma_kernel(const attn_args a) {
   typedef typename M::vec8_t vec8_t;
   typedef typename M::scalar_t scalar_t;
   constexpr int RB = S::RB, KS = S::KS, NSL = S::NSL, P = S::P, CT = S::CT, NW = S::NW;
-  constexpr int TILES = S::TILES, VCOLS = S::VCOLS, VT = S::VT, VLD = S::VLD, RS = S::RS;
+  constexpr int TILES = S::TILES, VCOLS = S::VCOLS, VT = S::VT, VLD = S::VLD;
 
   __shared__ __align__(16) char lds[S::LDS];
-  __shared__ float2 ml_lds[NW][16];
+  float2 (*const ml_lds)[16] = reinterpret_cast<float2 (*)[16]>(lds + NW * S::MERGE);
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -333,8 +336,8 @@ void paged_attn_mfma_kernel(const attn_args a) {
   // side, so each block's bytes are fetched close together in time.
   const int item = blockIdx.x / a.num_kv_heads;
   const int kvh = blockIdx.x - item * a.num_kv_heads;
+  const int4 wi = a.work[item];                  // the array holds the grid's capacity
   if (a.counts && item >= a.counts[0]) return;   // whole workgroup: beyond this step's items
-  const int4 wi = a.work[item];
   const int row0 = wi.x, seq = wi.y, part = wi.z & 0xFFFFFF, nrows = (wi.z >> 24) + 1, ctx0 = wi.w;
   const int R = a.group;                    // heads of this workgroup; nrows * R <= 16
   const int head0 = kvh * a.rep + blockIdx.z * R;
@@ -390,29 +393,13 @@ void paged_attn_mfma_kernel(const attn_args a) {
     if constexpr (UT) return tile_base[t] + (lc * RB + 16 * lg);
     else return pool_kvh + pos_off(wb + 16 * t + lc) + 16 * lg;
   };
-  auto v_at = [&](int i) -> char* {
-    if constexpr (UT) return tile_base[(VT * i) / 16] + (v_off + ((VT * i) % 16 + lane / VCOLS) * RB + 16 * (lane % VCOLS));
-    else return pool_kvh + v_off + pos_off(wb + VT * i + lane / VCOLS) + 16 * (lane % VCOLS);
+  auto v_row = [&](int i) -> char* {   // pool address of V row VT*i + lane/VCOLS of the wave
+    if constexpr (UT) return tile_base[(VT * i) / 16] + (v_off + ((VT * i) % 16 + lane / VCOLS) * RB);
+    else return pool_kvh + v_off + pos_off(wb + VT * i + lane / VCOLS);
   };
 
-  // all of the wave's K and V loads are issued now
-  vec16 kd[TILES][KS], vd[VLD];
-  if (busy) {
-#pragma unroll
-    for (int t = 0; t < TILES; ++t) {
-      const int tau = wb + 16 * t + lc;
-      const char* src = (fused && tau == new_tau) ? k_new_row + 16 * lg : k_at(t);
-#pragma unroll
-      for (int s = 0; s < KS; ++s) kd[t][s] = (tau < n) ? ld16_stream(src + 64 * s) : zero16();
-    }
-#pragma unroll
-    for (int i = 0; i < VLD; ++i) {
-      const int tau = wb + VT * i + lane / VCOLS;
-      const char* src = (fused && tau == new_tau) ? v_new_row + 16 * (lane % VCOLS) : v_at(i);
-      vd[i] = (tau < n) ? ld16_stream(src) : zero16();
-    }
-  }
-  // q as the B operand of S^T = K.Q^T: lane holds q[row0+qi][head0+h][32s + 8lg .. +8].
+  // q first (vector loads retire in order: S^T = K.Q^T can start while V is
+  // still in flight); the B operand of S^T: lane holds q[row0+qi][head0+h][32s + 8lg .. +8].
   vec16 qb[KS];
 #pragma unroll
   for (int s = 0; s < KS; ++s) qb[s] = zero16();
@@ -421,8 +408,41 @@ void paged_attn_mfma_kernel(const attn_args a) {
 #pragma unroll
     for (int s = 0; s < KS; ++s) qb[s] = ld16(qrow + 64 * s);
   }
+  // All of the wave's K and V loads are issued now, unconditionally: a lane
+  // whose position lies past the context reads 16 bytes of q instead (a cache
+  // hit, finite values that meet p = 0). A predicated load would put a branch
+  // and a copy of the loaded value in between, and that copy waits for the
+  // load. K goes to registers (the A operand of S^T = K.Q^T); V goes straight
+  // to this wave's LDS rows (global_load_lds: lane l of load i fills bytes
+  // 16 l .. 16 l + 15 of the i-th KiB), swizzled per row. The fused append's
+  // newest position is read from k_new/v_new.
+  char* const vl = lds + wave * S::VST;
+  vec16 kd[TILES][KS];
+  if (busy) {
+    const char* const dummy = a.q;
+#pragma unroll
+    for (int t = 0; t < TILES; ++t) {
+      const int tau = wb + 16 * t + lc;
+      const char* const kp = k_at(t);   // on every lane: the generic lookup is a shuffle
+      const char* src = tau >= n ? dummy : (fused && tau == new_tau) ? k_new_row + 16 * lg : kp;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) kd[t][s] = ld16_stream(src + 64 * s);
+    }
+#pragma unroll
+    for (int i = 0; i < VLD; ++i) {
+      const int r = VT * i + lane / VCOLS;                  // wave-relative row
+      const int c = (lane % VCOLS) ^ S::swz(r);             // the row's chunk this lane's slot holds
+      const int tau = wb + r;
+      const char* const vp = v_row(i);
+      const char* src = tau >= n ? dummy + 16 * c : (fused && tau == new_tau) ? v_new_row + 16 * c : vp + 16 * c;
+      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                       (__attribute__((address_space(3))) void*)(vl + 1024 * i), 16, 0, 2);
+    }
+  }
+  // every load is issued before the first use of K (the scheduler would
+  // otherwise sink direct loads below the wait for K, serialising V behind it)
+  __builtin_amdgcn_sched_barrier(0);
 
-  char* const vl = lds + wave * S::STAGE;
   float m_w = -INFINITY;     // max of head lc over this wave's positions (base-2 domain)
   float l_part = 0.f;        // this lane's share of head lc's sum
   float4_t acc[NSL];         // O[head 4lg+j][16n + lc]
@@ -431,18 +451,6 @@ void paged_attn_mfma_kernel(const attn_args a) {
   float4_t sc[TILES];        // S^T, then P: lane holds positions 16t + 4lg + j of head lc
 
   if (busy) {
-    if (fused) {   // the newest position's K/V rows go to their pool slot
-#pragma unroll
-      for (int t = 0; t < TILES; ++t) {
-        if (wb + 16 * t + lc == new_tau) {
-#pragma unroll
-          for (int s = 0; s < KS; ++s) st16(k_at(t) + 64 * s, kd[t][s]);
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < VLD; ++i)
-        if (wb + VT * i + lane / VCOLS == new_tau) st16(v_at(i), vd[i]);
-    }
 #pragma unroll
     for (int t = 0; t < TILES; ++t) {
       sc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -471,42 +479,47 @@ void paged_attn_mfma_kernel(const attn_args a) {
       }
   }
   // O += P.V over 32-position blocks: k index 8lg+j <-> position 32u + 4lg + j (j<4)
-  // or 32u + 16 + 4lg + (j-4): exactly the S^T values this lane holds. V goes
-  // through LDS in two halves of HALF positions (barriers are workgroup-uniform).
+  // or 32u + 16 + 4lg + (j-4): exactly the S^T values this lane holds. The B
+  // operand comes from the wave's V rows by transpose reads once its direct
+  // loads have landed (the wait is explicit: the compiler does not see that
+  // these LDS reads depend on them).
+  if (busy) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
-  for (int hf = 0; hf < S::HALVES; ++hf) {
-    if (busy) {   // V rows of this part into the wave's stage (8-byte stores: 8-byte aligned stride)
-#pragma unroll
-      for (int i = hf * (VLD / S::HALVES); i < (hf + 1) * (VLD / S::HALVES); ++i) {
-        char* dst = vl + (VT * i - hf * S::HALF + lane / VCOLS) * RS + 16 * (lane % VCOLS);
-        *reinterpret_cast<uint2*>(dst) = make_uint2(vd[i].w[0], vd[i].w[1]);
-        *reinterpret_cast<uint2*>(dst + 8) = make_uint2(vd[i].w[2], vd[i].w[3]);
-      }
-    }
-    __syncthreads();   // stage visible
-    if (busy) {
-#pragma unroll
-    for (int u = hf * (TILES / 2 / S::HALVES); u < (hf + 1) * (TILES / 2 / S::HALVES); ++u) {
+    for (int u = 0; u < TILES / 2; ++u) {
       vec8_t pa;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         pa[j] = (scalar_t)sc[2 * u][j];
         pa[4 + j] = (scalar_t)sc[2 * u + 1][j];
       }
-      // B operand lane (lg, lc): V[position of k = 8lg + j][16nn + lc], two transpose reads
-      const char* vsrc = vl + (32 * u - hf * S::HALF + 4 * lg + (lc >> 2)) * RS + 8 * (lc & 3);
+      // lane (lg, lc) points at elements 4 (lc & 3) .. +3 of dims 16nn.. of row
+      // 32u + 4lg + (lc >> 2) (and the row 16 further): chunk (lc & 3) / 2 + 2nn
+      const int rlo = 32 * u + 4 * lg + (lc >> 2), rhi = rlo + 16;
+      const int half8 = 8 * (lc & 1);
 #pragma unroll
       for (int nn = 0; nn < NSL; ++nn) {
-        const uint2 lo = lds_read_tr16(vsrc + 32 * nn);            // positions 32u + 4lg + 0..3
-        const uint2 hi = lds_read_tr16(vsrc + 16 * RS + 32 * nn);  // positions 32u + 16 + 4lg + 0..3
+        const int c = ((lc & 3) >> 1) + 2 * nn;
+        const uint2 lo = lds_read_tr16(vl + rlo * RB + 16 * (c ^ S::swz(rlo)) + half8);
+        const uint2 hi = lds_read_tr16(vl + rhi * RB + 16 * (c ^ S::swz(rhi)) + half8);
         vec16 vb;
         vb.w[0] = lo.x; vb.w[1] = lo.y; vb.w[2] = hi.x; vb.w[3] = hi.y;
         acc[nn] = M::mfma(pa, __builtin_bit_cast(vec8_t, vb), acc[nn]);
       }
     }
+    // Fused append: the wave holding the newest position (wave-uniform test)
+    // writes its K and V rows to their pool slot, lanes 0..VCOLS-1 the K row
+    // and the next VCOLS lanes the V row; one head group does it for the kv head.
+    if (fused && blockIdx.z == 0 && new_tau >= wb && new_tau < wb + CT && lane < 2 * VCOLS) {
+      int blk = a.block_tables[(int64_t)seq * a.max_nb + ((ctx - 1) >> a.log2_bs)];
+      if (blk < 0 || blk >= a.num_blocks) blk = 0;   // host validates; stay inside the pool
+      const int c = lane % VCOLS;
+      const bool is_v = lane >= VCOLS;
+      char* const dst = pool_kvh + (int64_t)blk * blk_bytes + (int64_t)((ctx - 1) & (bs - 1)) * RB;
+      st16(dst + (is_v ? v_off : 0) + 16 * c, ld16((is_v ? v_new_row : k_new_row) + 16 * c));
     }
-    __syncthreads();   // stage consumed
   }
+  __syncthreads();   // every wave is done with its V rows: the area takes the merge
   float l_w = l_part + __shfl_xor(l_part, 16);
   l_w += __shfl_xor(l_w, 32);
   if (lg == 0) ml_lds[wave][lc] = make_float2(m_w, l_w);
@@ -610,8 +623,8 @@ void paged_prefill_mfma_kernel(const attn_args a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lc = lane & 15, lg = lane >> 4;
   const int item = blockIdx.x / a.num_heads;
   const int head = blockIdx.x - item * a.num_heads;
+  const int4 ti = a.tiles[item];                 // the array holds the grid's capacity
   if (a.counts && item >= a.counts[2]) return;   // whole workgroup: beyond this step's tiles
-  const int4 ti = a.tiles[item];
   const int row0 = ti.x, seq = ti.y, nrows = ti.z & 0xFF, part = ti.z >> 8, pos0 = ti.w;
   const int kvh = head / a.rep;
   const int limit = pos0 + nrows;                  // positions the tile's last row sees
@@ -797,62 +810,63 @@ void paged_prefill_mfma_kernel(const attn_args a) {
 // ---------------------------------------------------------------------------
 // Log-sum-exp merge of the partials of one split row: workgroup (r, c) owns
 // 256 float4 columns (4 consecutive output dims each, head = column / (D/4))
-// of split row r, starting at column 256 c; every partial is read once, in
-// batches of 8 whose loads are all in flight.
+// of split row r, starting at column 256 c:
+//   out = sum_p 2^(m_p - M) acc_p / sum_p 2^(m_p - M) l_p.
+// The row's record (row, first partial, count) is one 16-byte load, issued
+// together with the device count; the partials follow in batches of 16 whose
+// loads are all in flight (one batch for a row of up to 16 partitions).
 template <typename Tag, int D>
 __global__ __launch_bounds__(256) void combine_partials_kernel(const attn_args a) {
   constexpr int EB = elem<Tag>::bytes;
   constexpr int QPH = D / 4;                       // float4 columns per head
-  if (a.counts && (int)blockIdx.x >= a.counts[1]) return;   // beyond this step's split rows
-  const int row = a.split_rows[blockIdx.x];
-  const int pbeg = a.row_part_off[row];
-  const int n = a.row_part_off[row + 1] - pbeg;
-  char* orow = a.out + row * a.out_row_bytes;
+  constexpr int BATCH = 16;
   const int col = threadIdx.x + 256 * blockIdx.y;
-  if (col < a.num_heads * QPH) {
-    const int head = col / QPH, d4 = col - head * QPH;
-    // batches of 8 partials, all loads of a batch in flight, merged online
-    float M = -INFINITY, L = 0.f;
-    float4_t o = float4_t{0.f, 0.f, 0.f, 0.f};
-    for (int p0 = 0; p0 < n; p0 += 8) {
-      float2 ml[8];
-      float4_t av[8];
+  if (col >= a.num_heads * QPH) return;
+  const int4 rec = a.split_rows[blockIdx.x];       // the array holds the grid's capacity
+  if (a.counts && (int)blockIdx.x >= a.counts[1]) return;   // beyond this step's split rows
+  const int row = rec.x, pbeg = rec.y, n = rec.z;
+  const int head = col / QPH, d4 = col - head * QPH;
+  float M = -INFINITY, L = 0.f;
+  float4_t o = float4_t{0.f, 0.f, 0.f, 0.f};
+  for (int p0 = 0; p0 < n; p0 += BATCH) {
+    float2 ml[BATCH];
+    float4_t av[BATCH];
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        if (p0 + k < n) {
-          const int64_t slot = (int64_t)(pbeg + p0 + k) * a.num_heads + head;
-          ml[k] = *reinterpret_cast<const float2*>(a.ws_ml + slot * 2);
-          av[k] = *reinterpret_cast<const float4_t*>(a.ws_acc + slot * D + 4 * d4);
-        } else {
-          ml[k] = make_float2(-INFINITY, 0.f);
-          av[k] = float4_t{0.f, 0.f, 0.f, 0.f};
-        }
+    for (int k = 0; k < BATCH; ++k) {
+      if (p0 + k < n) {
+        const int64_t slot = (int64_t)(pbeg + p0 + k) * a.num_heads + head;
+        ml[k] = *reinterpret_cast<const float2*>(a.ws_ml + slot * 2);
+        av[k] = *reinterpret_cast<const float4_t*>(a.ws_acc + slot * D + 4 * d4);
+      } else {
+        ml[k] = make_float2(-INFINITY, 0.f);
+        av[k] = float4_t{0.f, 0.f, 0.f, 0.f};
       }
-      float mb = M;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) mb = fmaxf(mb, ml[k].x);   // finite: every partial saw a position
-      const float keep = fast_exp2(M - mb);                    // 0 while M = -inf
-      L *= keep;
-      o *= keep;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const float w = ml[k].y > 0.f ? fast_exp2(ml[k].x - mb) : 0.f;
-        L = fmaf(ml[k].y, w, L);
-        o += av[k] * w;
-      }
-      M = mb;
     }
-    const float inv = 1.f / L;
-    if constexpr (EB == 4) {
-      *reinterpret_cast<float4_t*>(orow + ((int64_t)head * D + 4 * d4) * 4) = o * inv;
-    } else {
-      typedef typename elem<Tag>::type s_t;
-      typedef s_t s4_t __attribute__((ext_vector_type(4)));
-      s4_t r;
+    float mb = M;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) r[j] = (s_t)(o[j] * inv);
-      *reinterpret_cast<s4_t*>(orow + ((int64_t)head * D + 4 * d4) * EB) = r;
+    for (int k = 0; k < BATCH; ++k) mb = fmaxf(mb, ml[k].x);   // finite: every partial saw a position
+    const float keep = fast_exp2(M - mb);                        // 0 while M = -inf
+    L *= keep;
+    o *= keep;
+#pragma unroll
+    for (int k = 0; k < BATCH; ++k) {
+      const float w = ml[k].y > 0.f ? fast_exp2(ml[k].x - mb) : 0.f;
+      L = fmaf(ml[k].y, w, L);
+      o += av[k] * w;
     }
+    M = mb;
+  }
+  const float inv = 1.f / L;
+  char* const dst = a.out + row * a.out_row_bytes + ((int64_t)head * D + 4 * d4) * EB;
+  if constexpr (EB == 4) {
+    *reinterpret_cast<float4_t*>(dst) = o * inv;
+  } else {
+    typedef typename elem<Tag>::type s_t;
+    typedef s_t s4_t __attribute__((ext_vector_type(4)));
+    s4_t r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r[j] = (s_t)(o[j] * inv);
+    *reinterpret_cast<s4_t*>(dst) = r;
   }
 }
 
@@ -982,6 +996,7 @@ extern "C" int32_t tb_paged_attention(const void* q, int64_t q_row_stride, void*
   TB_CHECK_ARG((q_row_stride * eb) % 16 == 0 && (out_row_stride * eb) % 16 == 0);
   TB_CHECK_ARG(max_parts_per_row >= (num_work_items > 0 ? 1 : 0) && total_partitions >= num_work_items);
   TB_CHECK_ARG(num_split_rows <= num_rows && (num_split_rows == 0 || (split_rows && max_parts_per_row > 1)));
+  TB_CHECK_ARG(((uintptr_t)split_rows & 15u) == 0);
   if (max_parts_per_row > 1) {
     TB_CHECK_ARG(workspace != nullptr);
     TB_CHECK_ARG(workspace_bytes >= tb_paged_attention_workspace_bytes(total_partitions, num_heads, head_dim));
@@ -1012,7 +1027,7 @@ extern "C" int32_t tb_paged_attention(const void* q, int64_t q_row_stride, void*
   a.work = reinterpret_cast<const int4*>(work_items);
   a.row_part_off = row_part_offsets;
   a.tiles = reinterpret_cast<const int4*>(prefill_tiles);
-  a.split_rows = split_rows;
+  a.split_rows = reinterpret_cast<const int4*>(split_rows);
   a.counts = device_counts;
   // workspace: [acc partials: parts x Hq x D][max/sum partials: parts x Hq x 2]
   a.ws_acc = (float*)workspace;

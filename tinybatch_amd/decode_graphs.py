@@ -26,7 +26,7 @@ import torch.nn.functional as F
 
 from . import ops
 from .kv_cache import PagedKVCache
-from .metadata import StepMetadata, build_step_metadata
+from .metadata import StepMetadata, pad4, build_step_metadata
 from .model import Qwen2Paged
 
 DEFAULT_BUCKETS = (1, 2, 4, 8, 16, 24, 32, 48, 64, 96, 128, 192, 256)
@@ -45,8 +45,9 @@ class DecodeGraphs:
         self.buckets = sorted({b for b in buckets if b < max_batch} | {max_batch})
         B = self.buckets[-1]
         self.wcap = B * self.max_parts
-        # int32 layout: slot [B] | tables [B*max_nb] | work [wcap*4] | row_part_off [B+1] | split [B] | counts [4]
-        sizes = [B, B * self.max_nb, self.wcap * 4, B + 1, B, 4]
+        # int32 layout (each part 16-byte aligned): slot [B] | tables [B*max_nb] | work [wcap*4] |
+        # row_part_off [B+1] | split-row records [B*4] | counts [4]
+        sizes = [pad4(n) for n in (B, B * self.max_nb, self.wcap * 4, B + 1, B * 4, 4)]
         self.offs = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
         n = int(self.offs[-1])
         self.dev_i32 = torch.zeros(n, dtype=torch.int32, device=self.dev)
@@ -77,7 +78,7 @@ class DecodeGraphs:
         m.block_tables = self._view(1, Bp * self.max_nb).view(Bp, self.max_nb)
         m.work = self._view(2, Bp * self.max_parts * 4).view(-1, 4)
         m.row_part_off = self._view(3, Bp + 1)
-        m.split_rows = self._view(4, Bp)
+        m.split_rows = self._view(4, Bp * 4).view(Bp, 4)
         m.prefill_tiles = m.split_rows            # never read: no tiles in a decode step
         m.device_counts = self._view(5, 4)
         return m
@@ -96,7 +97,7 @@ class DecodeGraphs:
         h[o[3]:o[3] + B + 1] = meta.row_part_off_np
         h[o[3] + B + 1:o[3] + Bp + 1] = meta.row_part_off_np[-1]
         S = meta.num_split_rows
-        h[o[4]:o[4] + S] = meta.split_rows_np
+        h[o[4]:o[4] + 4 * S] = meta.split_rows_np.reshape(-1)
         h[o[5]:o[5] + 4] = (W, S, 0, 0)
 
     # ---- the captured step -------------------------------------------------------

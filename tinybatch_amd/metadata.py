@@ -19,8 +19,9 @@ step and uploaded in a single host-to-device copy:
   positions query row i may see (the mask rule j <= ctx - q_len + i of
   model.py:139-145) and the group's later rows see one more position each.
 * ``row_part_off[T + 1]`` - running count of partitions per row.
-* ``split_rows[S]`` - rows whose work spans more than one partition (their
-  partials are merged by the combine pass).
+* ``split_rows[S, 4]`` - (row, first partial slot, partial count, 0) of every
+  row whose work spans more than one partition (their partials are merged by
+  the combine pass; the record saves it the lookups in row_part_off).
 * ``prefill_tiles[N, 4]`` - (row0, seq, rows | partition << 8, pos0) when
   ``tile_prefill``: sequences with many new rows (full prefills and long
   prefill tails) are cut into tiles of up to TILE_ROWS consecutive rows (row0
@@ -63,7 +64,7 @@ class StepMetadata:
     row_part_off_np: np.ndarray
     row_ctx_np: np.ndarray       # [T] visible positions per row (0 for rows outside slices)
     prefill_tiles_np: np.ndarray  # [N, 4]
-    split_rows_np: np.ndarray     # [S]
+    split_rows_np: np.ndarray     # [S, 4]
     # device views (int32, one backing buffer)
     device_buffer: torch.Tensor | None = None
     slot_mapping: torch.Tensor | None = None
@@ -78,8 +79,8 @@ class StepMetadata:
     def to(self, device: torch.device) -> "StepMetadata":
         """Upload every array with one host-to-device copy (views into one buffer)."""
         parts = [self.slot_mapping_np, self.block_tables_np.reshape(-1), self.work_np.reshape(-1),
-                 self.row_part_off_np, self.prefill_tiles_np.reshape(-1), self.split_rows_np]
-        sizes = [_pad4(p.size) for p in parts]
+                 self.row_part_off_np, self.prefill_tiles_np.reshape(-1), self.split_rows_np.reshape(-1)]
+        sizes = [pad4(p.size) for p in parts]
         host = np.zeros(sum(sizes), dtype=np.int32)
         offs = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
         for p, o in zip(parts, offs):
@@ -94,7 +95,7 @@ class StepMetadata:
         self.work = buf.narrow(0, int(offs[2]), parts[2].size).view(-1, 4)
         self.row_part_off = buf.narrow(0, int(offs[3]), parts[3].size)
         self.prefill_tiles = buf.narrow(0, int(offs[4]), parts[4].size).view(-1, 4)
-        self.split_rows = buf.narrow(0, int(offs[5]), parts[5].size)
+        self.split_rows = buf.narrow(0, int(offs[5]), parts[5].size).view(-1, 4)
         return self
 
 
@@ -112,7 +113,7 @@ def tiles_sequence(q_len: int, ctx: int, min_rows: int = 16, max_ctx: int = 4096
     return q_len >= min_rows and (ctx <= max_ctx or ctx <= 16 * q_len)
 
 
-def _pad4(n: int) -> int:
+def pad4(n: int) -> int:
     return (n + 3) // 4 * 4
 
 
@@ -262,7 +263,11 @@ def build_step_metadata(positions, seq_slices, block_tables, context_lens, *, bl
         raise ValueError("step too large for int32 metadata")
     tiles.sort(key=lambda t: -t[4])                   # most positions first (stable)
     tiles_np = np.asarray([t[:4] for t in tiles], dtype=np.int64).reshape(-1, 4)
-    split_rows = np.nonzero(nparts_by_row > 1)[0]
+    split_ids = np.nonzero(nparts_by_row > 1)[0]
+    split_rows = np.zeros((split_ids.size, 4), dtype=np.int64)
+    split_rows[:, 0] = split_ids
+    split_rows[:, 1] = row_part_off[split_ids]
+    split_rows[:, 2] = nparts_by_row[split_ids]
 
     return StepMetadata(
         num_tokens=T, num_seqs=B, block_size=block_size, partition_tokens=P,
@@ -271,7 +276,7 @@ def build_step_metadata(positions, seq_slices, block_tables, context_lens, *, bl
         decode_only=bool(B) and bool(np.all(qlens == 1)),
         rows_per_item=int(rows_per_item),
         num_prefill_tiles=int(tiles_np.shape[0]),
-        num_split_rows=int(split_rows.size),
+        num_split_rows=int(split_ids.size),
         slot_mapping_np=slots.astype(np.int32),
         block_tables_np=tables[:max(B, 1)].astype(np.int32),
         work_np=work.astype(np.int32),
