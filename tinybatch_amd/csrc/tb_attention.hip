@@ -297,11 +297,18 @@ struct mfma_shape {
   static constexpr int VCOLS = RB / 16;      // 16-byte columns of a row
   static constexpr int VT = 64 / VCOLS;      // rows per V load instruction
   static constexpr int VLD = CT / VT;        // V loads per lane
-  static constexpr int VST = CT * RB;        // V rows of one wave in LDS (loaded there directly)
+  // V rows of a wave pass through LDS in VPH phases of CT / VPH rows. With
+  // two phases (D = 64) the first half is loaded straight into LDS and the
+  // second half into registers, written over the first once that is consumed:
+  // 16 KB of LDS per workgroup instead of 32, so five workgroups fit on a CU
+  // instead of four.
+  static constexpr int VPH = (TILES % 4 == 0) ? 2 : 1;
+  static constexpr int VDMA = VLD / VPH;     // V loads per lane that go straight to LDS
+  static constexpr int VST = CT * RB / VPH;  // LDS bytes of V per wave
   static constexpr int MERGE = 16 * D * 4;   // per-wave acc bytes in the merge
   static constexpr int ML = NW * 16 * 8;     // per-column (max, sum) of every wave, after the acc area
   static constexpr int LDS = (NW * VST > NW * MERGE + ML) ? NW * VST : NW * MERGE + ML;
-  static_assert(TILES % 2 == 0 && P % CT == 0 && VT * RB == 1024, "chunk shape");
+  static_assert(TILES % 2 == 0 && P % CT == 0 && VT * RB == 1024 && VLD % VPH == 0, "chunk shape");
   // V row r of a wave keeps its 16-byte chunk c in slot c ^ swz(r): the transpose
   // reads of P.V (4 rows x 32 bytes per 16 lanes) then hit distinct banks.
   static __device__ __forceinline__ int swz(int r) { return 2 * (r & 3); }
@@ -418,6 +425,7 @@ void paged_attn_mfma_kernel(const attn_args a) {
   // newest position is read from k_new/v_new.
   char* const vl = lds + wave * S::VST;
   vec16 kd[TILES][KS];
+  vec16 vr[VLD > S::VDMA ? VLD - S::VDMA : 1];   // second-phase V rows (registers)
   if (busy) {
     const char* const dummy = a.q;
 #pragma unroll
@@ -435,9 +443,25 @@ void paged_attn_mfma_kernel(const attn_args a) {
       const int tau = wb + r;
       const char* const vp = v_row(i);
       const char* src = tau >= n ? dummy + 16 * c : (fused && tau == new_tau) ? v_new_row + 16 * c : vp + 16 * c;
-      __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
-                                       (__attribute__((address_space(3))) void*)(vl + 1024 * i), 16, 0, 2);
+      if (i < S::VDMA)
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                         (__attribute__((address_space(3))) void*)(vl + 1024 * i), 16, 0, 2);
+      else
+        vr[i - S::VDMA] = ld16_stream(src);
     }
+  }
+  // Read now what the tail needs, so that no workgroup ends on a memory round
+  // trip: the item's first partial slot and partition count (the item's rows
+  // are consecutive with equal counts, so row row0 + i starts at pbeg0 + i *
+  // nparts) and, for the wave holding the fused append's newest position, its
+  // block id.
+  const int pbeg0 = a.row_part_off[row0];
+  const int nparts = a.row_part_off[row0 + 1] - pbeg0;
+  const bool stores_new = fused && blockIdx.z == 0 && new_tau >= wb && new_tau < wb + CT;   // wave-uniform
+  int new_blk = 0;
+  if (stores_new) {
+    new_blk = a.block_tables[(int64_t)seq * a.max_nb + ((ctx - 1) >> a.log2_bs)];
+    if (new_blk < 0 || new_blk >= a.num_blocks) new_blk = 0;   // host validates; stay inside the pool
   }
   // every load is issued before the first use of K (the scheduler would
   // otherwise sink direct loads below the wait for K, serialising V behind it)
@@ -487,6 +511,12 @@ void paged_attn_mfma_kernel(const attn_args a) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
     for (int u = 0; u < TILES / 2; ++u) {
+      if (S::VPH == 2 && u == TILES / 4) {
+        // the first half's rows are consumed (LDS accesses of a wave run in
+        // order): the second half takes their place, in the same slot layout
+#pragma unroll
+        for (int j = 0; j < VLD - S::VDMA; ++j) st16(vl + 1024 * j + 16 * lane, vr[j]);
+      }
       vec8_t pa;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -495,7 +525,8 @@ void paged_attn_mfma_kernel(const attn_args a) {
       }
       // lane (lg, lc) points at elements 4 (lc & 3) .. +3 of dims 16nn.. of row
       // 32u + 4lg + (lc >> 2) (and the row 16 further): chunk (lc & 3) / 2 + 2nn
-      const int rlo = 32 * u + 4 * lg + (lc >> 2), rhi = rlo + 16;
+      // (rows of the second phase sit CT/2 rows lower; swz has period 4, so their slots match)
+      const int rlo = 32 * u - (S::VPH == 2 && u >= TILES / 4 ? CT / 2 : 0) + 4 * lg + (lc >> 2), rhi = rlo + 16;
       const int half8 = 8 * (lc & 1);
 #pragma unroll
       for (int nn = 0; nn < NSL; ++nn) {
@@ -510,12 +541,10 @@ void paged_attn_mfma_kernel(const attn_args a) {
     // Fused append: the wave holding the newest position (wave-uniform test)
     // writes its K and V rows to their pool slot, lanes 0..VCOLS-1 the K row
     // and the next VCOLS lanes the V row; one head group does it for the kv head.
-    if (fused && blockIdx.z == 0 && new_tau >= wb && new_tau < wb + CT && lane < 2 * VCOLS) {
-      int blk = a.block_tables[(int64_t)seq * a.max_nb + ((ctx - 1) >> a.log2_bs)];
-      if (blk < 0 || blk >= a.num_blocks) blk = 0;   // host validates; stay inside the pool
+    if (stores_new && lane < 2 * VCOLS) {
       const int c = lane % VCOLS;
       const bool is_v = lane >= VCOLS;
-      char* const dst = pool_kvh + (int64_t)blk * blk_bytes + (int64_t)((ctx - 1) & (bs - 1)) * RB;
+      char* const dst = pool_kvh + (int64_t)new_blk * blk_bytes + (int64_t)((ctx - 1) & (bs - 1)) * RB;
       st16(dst + (is_v ? v_off : 0) + 16 * c, ld16((is_v ? v_new_row : k_new_row) + 16 * c));
     }
   }
@@ -544,9 +573,7 @@ void paged_attn_mfma_kernel(const attn_args a) {
   for (int idx = threadIdx.x; idx < ncols * D; idx += 64 * NW) {
     const int h = idx / D, d = idx - h * D;          // h: column
     const int row = row0 + h / R, head = head0 + h - (h / R) * R;
-    const int pbeg = a.row_part_off[row];
-    const int nparts = a.row_part_off[row + 1] - pbeg;   // the same for every row of the item
-    const int64_t pidx = pbeg + part;
+    const int64_t pidx = pbeg0 + (h / R) * nparts + part;
     float Mh = ml_lds[0][h].x;
 #pragma unroll
     for (int w = 1; w < NW; ++w) Mh = fmaxf(Mh, ml_lds[w][h].x);
