@@ -59,6 +59,25 @@ int32_t tb_kv_append(const void* k, int64_t k_row_stride,
                      int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                      int32_t dtype, hipStream_t stream);
 
+/* K1 with the K rotation folded in: the engine's rotate-half RoPE of k
+ * (src/tinybatch/model.py:72-80, applied at :125) followed by write
+ * (kv_cache.py:25-38). K rows are rotated at positions[t] (int64) on their way
+ * to the pool, V rows are copied:
+ *   k1' = k1 cos - k2 sin,  k2' = k2 cos + k1 sin   (k1 / k2 the two halves of a head row)
+ * with rope_cos / rope_sin fp32 [rope_max_position][head_dim / 2] (16-byte
+ * aligned; positions are clamped into the table), each product rounded on its
+ * own and the result rounded to the element type: the bits of rotating with
+ * the separate tensor ops, then tb_kv_append. head_dim * element size must be
+ * a multiple of 32 bytes.
+ */
+int32_t tb_kv_append_rope(const void* k, int64_t k_row_stride,
+                          const void* v, int64_t v_row_stride,
+                          void* pool, int64_t num_blocks,
+                          const int32_t* slot_mapping, const int64_t* positions,
+                          const float* rope_cos, const float* rope_sin, int32_t rope_max_position,
+                          int32_t num_tokens, int32_t num_kv_heads, int32_t head_dim,
+                          int32_t block_size, int32_t dtype, hipStream_t stream);
+
 /* ---------------------------------------------------------------------------
  * Paged gather of one sequence into contiguous K and V.
  * Replaces PagedKVCache.gather (src/tinybatch/kv_cache.py:40-45):
@@ -125,6 +144,11 @@ int32_t tb_kv_gather(const void* pool, int64_t num_blocks,
  * written to its slot in the pool by the same kernel, replacing a separate
  * tb_kv_append. Valid only when no row reads another row's newest slot, which
  * holds for a batch of decode rows (one new token per sequence).
+ * RoPE in the prologue (rope_cos != NULL, the tables of tb_kv_append_rope):
+ * q holds the projections before rotation; every query row is rotated at its
+ * position row_ctx - 1 as it is loaded (the engine's _rope of q,
+ * src/tinybatch/model.py:72-80,125), and with the fused append so is the K row
+ * of k_new. NULL: q (and k_new) are already rotated.
  */
 int32_t tb_attention_partition_tokens(int32_t dtype, int32_t head_dim);
 
@@ -150,7 +174,9 @@ int32_t tb_paged_attention(const void* q, int64_t q_row_stride,
                            const void* k_new, int64_t k_row_stride,
                            const void* v_new, int64_t v_row_stride,
                            void* workspace, size_t workspace_bytes,
-                           const int32_t* device_counts, hipStream_t stream);
+                           const int32_t* device_counts,
+                           const float* rope_cos, const float* rope_sin, int32_t rope_max_position,
+                           hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * K3 — block copy across every layer pool in one launch.

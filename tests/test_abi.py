@@ -54,6 +54,12 @@ def test_append_rejects_bad_arguments_without_launching():
     assert L.tb_kv_append(fake, 120, fake, 120, fake, 16, fake, 4, 2, 60, 16, 1, None) == _lib.TB_ERR_UNSUPPORTED
     # zero tokens is a no-op
     assert L.tb_kv_append(None, 128, None, 128, fake, 16, None, 0, 2, 64, 16, 1, None) == _lib.TB_OK
+    # the RoPE append: tables required, each half a whole number of 16-byte chunks
+    ap = L.tb_kv_append_rope
+    assert ap(fake, 128, fake, 128, fake, 16, fake, fake, None, fake, 64, 4, 2, 64, 16, 1, None) == _lib.TB_ERR_INVALID_ARG
+    assert ap(fake, 128, fake, 128, fake, 16, fake, fake, fake, fake, 0, 4, 2, 64, 16, 1, None) == _lib.TB_ERR_INVALID_ARG
+    assert ap(fake, 128, fake, 128, fake, 16, fake, fake, fake, fake, 64, 4, 2, 8, 16, 1, None) == _lib.TB_ERR_UNSUPPORTED
+    assert ap(None, 128, None, 128, fake, 16, None, None, None, None, 0, 0, 2, 64, 16, 1, None) == _lib.TB_OK
 
 
 def test_attention_rejects_bad_arguments_without_launching():
@@ -63,12 +69,13 @@ def test_attention_rejects_bad_arguments_without_launching():
     def call(**kw):
         a = dict(q=f, qs=896, pool=f, nb=64, out=f, os=896, bt=f, mnb=4, work=f, nw=2, tiles=None, nt=0,
                  rpo=f, nr=2, split=None, ns=0, mpr=1, pt=256, tp=2, hq=14, hkv=2, d=64, bs=16, scale=0.125,
-                 dt=1, kn=None, ks=0, vn=None, vs=0, ws=None, wsb=0)
+                 dt=1, kn=None, ks=0, vn=None, vs=0, ws=None, wsb=0, rc=None, rs=None, rmax=0)
         a.update(kw)
         return L.tb_paged_attention(a["q"], a["qs"], a["pool"], a["nb"], a["out"], a["os"], a["bt"], a["mnb"],
                                     a["work"], a["nw"], a["tiles"], a["nt"], a["rpo"], a["nr"], a["split"], a["ns"],
                                     a["mpr"], a["pt"], a["tp"], a["hq"], a["hkv"], a["d"], a["bs"], a["scale"],
-                                    a["dt"], a["kn"], a["ks"], a["vn"], a["vs"], a["ws"], a["wsb"], None, None)
+                                    a["dt"], a["kn"], a["ks"], a["vn"], a["vs"], a["ws"], a["wsb"], None,
+                                    a["rc"], a["rs"], a["rmax"], None)
 
     assert call(d=96) == _lib.TB_ERR_UNSUPPORTED               # no kernel for head_dim 96
     assert call(hq=13) == _lib.TB_ERR_INVALID_ARG              # heads not a multiple of kv heads
@@ -83,6 +90,8 @@ def test_attention_rejects_bad_arguments_without_launching():
     assert call(tiles=None, nt=1) == _lib.TB_ERR_INVALID_ARG   # tiles announced, none given
     assert call(tiles=f, nt=1, kn=f, vn=f, ks=128, vs=128) == _lib.TB_ERR_INVALID_ARG   # fused append: decode only
     assert call(split=f, ns=1, mpr=1) == _lib.TB_ERR_INVALID_ARG   # split rows imply > 1 partition
+    assert call(rc=f, rs=None, rmax=64) == _lib.TB_ERR_INVALID_ARG   # RoPE needs both tables
+    assert call(rc=f, rs=f, rmax=0) == _lib.TB_ERR_INVALID_ARG       # ... and their length
     assert call(split=f, ns=3, nr=2, mpr=2, ws=f, wsb=1 << 20) == _lib.TB_ERR_INVALID_ARG   # more split rows than rows
 
 

@@ -28,6 +28,8 @@ c_i32, c_i64, c_f32, c_sz, c_vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float
 SIGNATURES = {
     "tb_status_string": (ctypes.c_char_p, [c_i32]),
     "tb_kv_append": (c_i32, [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp]),
+    "tb_kv_append_rope": (c_i32, [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_vp, c_vp, c_vp, c_i32,
+                                  c_i32, c_i32, c_i32, c_i32, c_i32, c_vp]),
     "tb_kv_gather": (c_i32, [c_vp, c_i64, c_vp, c_i32, c_vp, c_vp, c_i32, c_i32, c_i32, c_i32, c_vp]),
     "tb_attention_partition_tokens": (c_i32, [c_i32, c_i32]),
     "tb_paged_attention_workspace_bytes": (c_sz, [c_i32, c_i32, c_i32]),
@@ -45,7 +47,9 @@ SIGNATURES = {
         c_f32, c_i32,           # scale, dtype
         c_vp, c_i64, c_vp, c_i64,  # k_new, k_row_stride, v_new, v_row_stride
         c_vp, c_sz,             # workspace, workspace_bytes
-        c_vp, c_vp,             # device_counts, stream
+        c_vp,                   # device_counts
+        c_vp, c_vp, c_i32,      # rope_cos, rope_sin, rope_max_position
+        c_vp,                   # stream
     ]),
     "tb_block_copy": (c_i32, [c_vp, c_i32, c_i64, c_vp, c_vp, c_i32, c_i64, c_vp]),
     "tb_block_gather": (c_i32, [c_vp, c_i64, c_vp, c_i32, c_vp, c_i64, c_vp]),

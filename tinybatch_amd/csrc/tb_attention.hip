@@ -90,6 +90,7 @@ struct attn_args {
   int64_t k_new_row_bytes;
   const char* v_new;
   int64_t v_new_row_bytes;
+  rope_tables rope;       // rope.cos != null: q (and a fused append's K) rotated at position row_ctx - 1
 };
 
 
@@ -190,6 +191,26 @@ __global__ __launch_bounds__(64) void paged_attn_valu_kernel(const attn_args a) 
 #pragma unroll
     for (int h = 0; h < REP; ++h) qv[h] = ld16(qrow + (int64_t)(head0 + h) * D * EB);
   }
+  // RoPE: chunk j of the first half pairs with chunk j + LPT/2 of the second,
+  // held by lane ^ LPT/2 of the same token slot (every lane holds its chunk)
+  vec16 k_new_rot = zero16();
+  if (a.rope.cos) {
+    const bool first = j < LPT / 2;
+    const int64_t r = a.rope.row(ctx - 1, D / 2) + (first ? j : j - LPT / 2) * 4;
+    auto rotate = [&](vec16& x) {
+      vec16 y;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y.w[e] = (uint32_t)__shfl_xor((int)x.w[e], LPT / 2);
+      if (first) rope_pair<float>(x, y, a.rope.cos + r, a.rope.sin + r);
+      else rope_pair<float>(y, x, a.rope.cos + r, a.rope.sin + r);
+    };
+#pragma unroll
+    for (int h = 0; h < REP; ++h) rotate(qv[h]);
+    if (fused) {
+      k_new_rot = ld16(k_new_row);
+      rotate(k_new_rot);
+    }
+  }
 
   float m_run[REP], l_run[REP], acc[REP][EPL];
 #pragma unroll
@@ -218,6 +239,7 @@ __global__ __launch_bounds__(64) void paged_attn_valu_kernel(const attn_args a) 
       if (fused && tau == new_pos) { kp = k_new_row; vp = v_new_row; }
       if (tau < p1) { kbuf[i] = ld16(kp); vbuf[i] = ld16(vp); }
       else { kbuf[i] = zero16(); vbuf[i] = zero16(); }
+      if (fused && a.rope.cos && tau == new_pos) kbuf[i] = k_new_rot;
     }
     if (fused) {
 #pragma unroll
@@ -467,6 +489,28 @@ void paged_attn_mfma_kernel(const attn_args a) {
   // otherwise sink direct loads below the wait for K, serialising V behind it)
   __builtin_amdgcn_sched_barrier(0);
 
+  // RoPE: slice s (dims 32s + 8lg ..) of the first half pairs with slice
+  // s + KS/2 of the second in the same lane, for q and for the K row of the
+  // fused append's newest position
+  if (a.rope.cos) {
+    if (lc < ncols) {
+      const int64_t r = a.rope.row(ctx0 + qi - 1, D / 2) + 8 * lg;
+#pragma unroll
+      for (int s = 0; s < KS / 2; ++s)
+        rope_pair<scalar_t>(qb[s], qb[s + KS / 2], a.rope.cos + r + 32 * s, a.rope.sin + r + 32 * s);
+    }
+    if (fused && busy) {
+      const int64_t r = a.rope.row(ctx - 1, D / 2) + 8 * lg;
+#pragma unroll
+      for (int t = 0; t < TILES; ++t)
+        if (wb + 16 * t + lc == new_tau) {
+#pragma unroll
+          for (int s = 0; s < KS / 2; ++s)
+            rope_pair<scalar_t>(kd[t][s], kd[t][s + KS / 2], a.rope.cos + r + 32 * s, a.rope.sin + r + 32 * s);
+        }
+    }
+  }
+
   float m_w = -INFINITY;     // max of head lc over this wave's positions (base-2 domain)
   float l_part = 0.f;        // this lane's share of head lc's sum
   float4_t acc[NSL];         // O[head 4lg+j][16n + lc]
@@ -545,7 +589,16 @@ void paged_attn_mfma_kernel(const attn_args a) {
       const int c = lane % VCOLS;
       const bool is_v = lane >= VCOLS;
       char* const dst = pool_kvh + (int64_t)new_blk * blk_bytes + (int64_t)((ctx - 1) & (bs - 1)) * RB;
-      st16(dst + (is_v ? v_off : 0) + 16 * c, ld16((is_v ? v_new_row : k_new_row) + 16 * c));
+      vec16 x = ld16((is_v ? v_new_row : k_new_row) + 16 * c);
+      if (!is_v && a.rope.cos) {   // K chunk c pairs with chunk c +- VCOLS/2
+        const bool first = c < VCOLS / 2;
+        const int c1 = first ? c : c - VCOLS / 2;
+        vec16 y = ld16(k_new_row + 16 * (first ? c + VCOLS / 2 : c1));
+        const int64_t r = a.rope.row(ctx - 1, D / 2) + 8 * c1;
+        if (first) rope_pair<scalar_t>(x, y, a.rope.cos + r, a.rope.sin + r);
+        else rope_pair<scalar_t>(y, x, a.rope.cos + r, a.rope.sin + r);
+      }
+      st16(dst + (is_v ? v_off : 0) + 16 * c, x);
     }
   }
   __syncthreads();   // every wave is done with its V rows: the area takes the merge
@@ -801,6 +854,12 @@ void paged_prefill_mfma_kernel(const attn_args a) {
   load_ids(c0, ids);
   load_kv(c0, ids, kr, vr);
   load_ids(c0 + 1, ids);
+  if (a.rope.cos && my_row < nrows) {   // RoPE of q at the row's position (slices s and s + KS/2 pair)
+    const int64_t r = a.rope.row(pos0 + my_row, D / 2) + 8 * lg;
+#pragma unroll
+    for (int s = 0; s < KS / 2; ++s)
+      rope_pair<scalar_t>(qb[s], qb[s + KS / 2], a.rope.cos + r + 32 * s, a.rope.sin + r + 32 * s);
+  }
   for (int c = c0; c < c_end; ++c) {   // workgroup-uniform trip count
     stage(kr, vr);
     if (c + 1 < c_end) {   // the next chunk's loads are in flight during the compute
@@ -1000,7 +1059,9 @@ extern "C" int32_t tb_paged_attention(const void* q, int64_t q_row_stride, void*
                                       float scale, int32_t dtype, const void* k_new,
                                       int64_t k_row_stride, const void* v_new, int64_t v_row_stride,
                                       void* workspace, size_t workspace_bytes,
-                                      const int32_t* device_counts, hipStream_t stream) {
+                                      const int32_t* device_counts, const float* rope_cos,
+                                      const float* rope_sin, int32_t rope_max_position,
+                                      hipStream_t stream) {
   using namespace tb;
   const int eb = elem_bytes(dtype);
   TB_CHECK_ARG(eb > 0);
@@ -1029,6 +1090,10 @@ extern "C" int32_t tb_paged_attention(const void* q, int64_t q_row_stride, void*
     TB_CHECK_ARG(workspace_bytes >= tb_paged_attention_workspace_bytes(total_partitions, num_heads, head_dim));
     TB_CHECK_ARG(((uintptr_t)workspace & 15u) == 0);
   }
+  if (rope_cos || rope_sin) {
+    TB_CHECK_ARG(rope_cos && rope_sin && rope_max_position > 0);
+    TB_CHECK_ARG((((uintptr_t)rope_cos | (uintptr_t)rope_sin) & 15u) == 0);
+  }
   if (k_new || v_new) {
     TB_CHECK_ARG(k_new && v_new && num_prefill_tiles == 0);
     TB_CHECK_ARG(k_row_stride >= (int64_t)num_kv_heads * head_dim && v_row_stride >= (int64_t)num_kv_heads * head_dim);
@@ -1055,6 +1120,7 @@ extern "C" int32_t tb_paged_attention(const void* q, int64_t q_row_stride, void*
   a.row_part_off = row_part_offsets;
   a.tiles = reinterpret_cast<const int4*>(prefill_tiles);
   a.split_rows = reinterpret_cast<const int4*>(split_rows);
+  a.rope = rope_tables{rope_cos, rope_sin, rope_max_position};
   a.counts = device_counts;
   // workspace: [acc partials: parts x Hq x D][max/sum partials: parts x Hq x 2]
   a.ws_acc = (float*)workspace;

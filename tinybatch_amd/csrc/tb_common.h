@@ -166,6 +166,58 @@ __device__ __forceinline__ float sum_xor32(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// A product rounded on its own: one v_mul_f32 that the compiler cannot fuse
+// into a following add (HIP's __fmul_rn is a plain multiply, and whether it is
+// contracted into an FMA depends on where it is inlined).
+__device__ __forceinline__ float mul_rn(float a, float b) {
+  float p;
+  asm("v_mul_f32 %0, %1, %2" : "=v"(p) : "v"(a), "v"(b));
+  return p;
+}
+
+// Rotate-half RoPE (reference src/tinybatch/model.py:72-80) of one 16-byte
+// chunk pair of a head row: x1 holds dims i .. i+n-1 of the first half, x2 the
+// same dims of the second half, c / s point at the fp32 cos / sin table entries
+// of dims i .. of the position (n = 16 / sizeof(T)):
+//   x1' = x1 c - x2 s,  x2' = x2 c + x1 s,
+// each product rounded on its own as the separate tensor ops round it, the
+// result rounded to the element type (the arithmetic of tb_rope_qk).
+template <typename T>
+__device__ __forceinline__ void rope_pair(vec16& x1, vec16& x2, const float* c, const float* s) {
+  constexpr int N = 16 / sizeof(T);
+  T a[N], b[N];
+  __builtin_memcpy(a, &x1, 16);
+  __builtin_memcpy(b, &x2, 16);
+  float cv[N], sv[N];
+#pragma unroll
+  for (int q = 0; q < N; q += 4) {
+    const float4 c4 = *reinterpret_cast<const float4*>(c + q);
+    const float4 s4 = *reinterpret_cast<const float4*>(s + q);
+    cv[q] = c4.x; cv[q + 1] = c4.y; cv[q + 2] = c4.z; cv[q + 3] = c4.w;
+    sv[q] = s4.x; sv[q + 1] = s4.y; sv[q + 2] = s4.z; sv[q + 3] = s4.w;
+  }
+#pragma unroll
+  for (int e = 0; e < N; ++e) {
+    const float u = (float)a[e], w = (float)b[e];
+    a[e] = (T)(mul_rn(u, cv[e]) - mul_rn(w, sv[e]));
+    b[e] = (T)(mul_rn(w, cv[e]) + mul_rn(u, sv[e]));
+  }
+  __builtin_memcpy(&x1, a, 16);
+  __builtin_memcpy(&x2, b, 16);
+}
+
+// RoPE tables of a call: fp32 cos / sin [max_position][head_dim / 2]; the
+// position is clamped into the table (the host validates positions).
+struct rope_tables {
+  const float* cos;
+  const float* sin;
+  int32_t max_position;
+  __device__ __forceinline__ int64_t row(int64_t p, int half) const {
+    p = p < 0 ? 0 : (p >= max_position ? max_position - 1 : p);
+    return p * half;
+  }
+};
+
 }  // namespace tb
 
 // Status helpers shared by the C entry points.

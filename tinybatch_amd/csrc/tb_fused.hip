@@ -89,8 +89,8 @@ __global__ __launch_bounds__(256) void rope_qk_kernel(const T* qkv, int64_t row_
   const float c = cos_t[p * half + i], s = sin_t[p * half + i];
   const T* src = qkv + row * row_stride + (int64_t)head * d;     // q heads, then k heads
   const float x1 = to_f(src[i]), x2 = to_f(src[i + half]);
-  const float o1 = __fsub_rn(__fmul_rn(x1, c), __fmul_rn(x2, s));
-  const float o2 = __fadd_rn(__fmul_rn(x2, c), __fmul_rn(x1, s));
+  const float o1 = mul_rn(x1, c) - mul_rn(x2, s);   // each product rounded on its own
+  const float o2 = mul_rn(x2, c) + mul_rn(x1, s);
   T* dst = head < hq ? q_out + ((int64_t)row * hq + head) * d : k_out + ((int64_t)row * hkv + head - hq) * d;
   dst[i] = from_f<T>(o1);
   dst[i + half] = from_f<T>(o2);

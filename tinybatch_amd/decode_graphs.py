@@ -105,11 +105,13 @@ class DecodeGraphs:
     def _forward(self, Bp: int, meta: StepMetadata) -> None:
         m, c = self.model, self.model.cfg
 
-        def attention(i, q, k, v):   # fused append + attention (a decode step)
-            return ops.paged_attention(q, self.cache.pools[i], meta, num_heads=c.n_heads, k_new=k, v_new=v,
-                                       workspace=self.ws)
+        rope = m.rope if m.fused_rope else None
 
-        x = m.run_layers(self.tok[:Bp], self.pos[:Bp], attention)
+        def attention(i, q, k, v):   # fused append + attention (a decode step), RoPE in the kernel
+            return ops.paged_attention(q, self.cache.pools[i], meta, num_heads=c.n_heads, k_new=k, v_new=v,
+                                       workspace=self.ws, rope=rope)
+
+        x = m.run_layers(self.tok[:Bp], self.pos[:Bp], attention, fused_rope=m.fused_rope)
         self.ids[:Bp].copy_(F.linear(x, m.lm_head).argmax(dim=-1))
 
     def bucket(self, B: int) -> int | None:

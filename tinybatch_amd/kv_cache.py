@@ -89,10 +89,13 @@ class PagedKVCache:
 
     # ---- reference API -----------------------------------------------------
     def write(self, layer: int, k: torch.Tensor, v: torch.Tensor, positions: torch.Tensor,
-              seq_slices: list[tuple[int, int]], block_tables: list[list[int]]) -> None:
-        """Scatter each new token's K/V into its sequence's blocks (reference kv_cache.py:25-38)."""
+              seq_slices: list[tuple[int, int]], block_tables: list[list[int]],
+              rope: ops.Rope | None = None) -> None:
+        """Scatter each new token's K/V into its sequence's blocks (reference kv_cache.py:25-38).
+        With ``rope``, k is the projection before rotation and is rotated at ``positions``
+        (a device int64 tensor) on its way to the pool."""
         meta = self._lookup_or_build(positions, seq_slices, block_tables, None, k.shape[0])
-        ops.kv_append(self.pools[layer], k, v, meta.slot_mapping)
+        ops.kv_append(self.pools[layer], k, v, meta.slot_mapping, rope=rope, positions=positions)
 
     def gather(self, layer: int, table: list[int], context_len: int) -> tuple[torch.Tensor, torch.Tensor]:
         """Contiguous K, V [context_len, n_kv_heads, head_dim] (reference kv_cache.py:40-45)."""
@@ -113,12 +116,13 @@ class PagedKVCache:
 
     def attention(self, layer: int, q: torch.Tensor, positions, seq_slices, block_tables, context_lens,
                   *, num_heads: int | None = None, scale: float | None = None,
-                  out: torch.Tensor | None = None) -> torch.Tensor:
-        """attn_out [T, Hq*D] for the whole flat batch (reference model.py:130-147)."""
+                  out: torch.Tensor | None = None, rope: ops.Rope | None = None) -> torch.Tensor:
+        """attn_out [T, Hq*D] for the whole flat batch (reference model.py:130-147). With
+        ``rope``, q is the projection before rotation (rotated inside the kernels)."""
         hq = num_heads if num_heads is not None else q.shape[1]
         rows = self.rows_per_item(hq)
         meta = self._lookup_or_build(positions, seq_slices, block_tables, context_lens, q.shape[0], rows)
-        return ops.paged_attention(q, self.pools[layer], meta, num_heads=hq, scale=scale, out=out)
+        return ops.paged_attention(q, self.pools[layer], meta, num_heads=hq, scale=scale, out=out, rope=rope)
 
     def decode_step(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, meta: StepMetadata,
                     *, num_heads: int | None = None, scale: float | None = None,

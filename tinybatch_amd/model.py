@@ -13,7 +13,9 @@ MI355X-side choices: q/k/v are one GEMM over a concatenated weight (and
 gate/up another); the residual add + RMSNorm, the RoPE of q and k and the
 SwiGLU gate are one fused kernel each (layer_ops) instead of chains of tensor
 ops; the RoPE tables are built once for every position up to max_position;
-the LM head runs on the last rows only.
+the LM head runs on the last rows only. With ``fused_rope`` (the default) the
+RoPE of q and k is folded into the paged kernels (K1 rotates k on its way to
+the pool, K2 rotates q as it loads it) instead of a launch of its own.
 
 Weights are drawn from a seeded generator (no checkpoint exists offline):
 N(0, 0.02) for embeddings, projections and biases, ones for the norms.
@@ -26,7 +28,7 @@ from dataclasses import dataclass
 import torch
 import torch.nn.functional as F
 
-from . import layer_ops
+from . import layer_ops, ops
 from .kv_cache import PagedKVCache
 
 
@@ -93,6 +95,8 @@ class Qwen2Paged:
             })
         self.norm = torch.ones(c.d_model, device=self.device, dtype=dtype)
         self.cos, self.sin = rope_tables(c.head_dim, c.rope_theta, c.max_position, self.device)
+        self.rope = ops.Rope(self.cos, self.sin)
+        self.fused_rope = True
 
     def reference_weights(self) -> dict[str, torch.Tensor]:
         """The weights under the reference's state-dict names (model.py:97-98,111-151)."""
@@ -112,9 +116,12 @@ class Qwen2Paged:
             w[p + "mlp.down_proj.weight"] = L["w_down"]
         return w
 
-    def run_layers(self, token_ids: torch.Tensor, positions: torch.Tensor, attention) -> torch.Tensor:
+    def run_layers(self, token_ids: torch.Tensor, positions: torch.Tensor, attention,
+                   fused_rope: bool = False) -> torch.Tensor:
         """Hidden states after the final norm, [T, d_model]. ``attention(layer, q, k, v)``
-        appends the step's K/V and returns attn_out [T, Hq*D] (model.py:127-147)."""
+        appends the step's K/V and returns attn_out [T, Hq*D] (model.py:127-147); with
+        ``fused_rope`` q and k are the projections before RoPE (views of the qkv rows)
+        and ``attention`` must rotate them."""
         c = self.cfg
         T = token_ids.shape[0]
         hq, hk = c.n_heads * c.head_dim, c.n_kv_heads * c.head_dim
@@ -122,7 +129,11 @@ class Qwen2Paged:
         x = layer_ops.rms_norm(h, self.layers[0]["ln1"], c.rms_eps)
         for i, L in enumerate(self.layers):
             qkv = F.linear(x, L["w_qkv"], L["b_qkv"])
-            q, k = layer_ops.rope_qk(qkv, positions, self.cos, self.sin, c.n_heads, c.n_kv_heads, c.head_dim)
+            if fused_rope:
+                q = qkv[:, :hq].view(T, c.n_heads, c.head_dim)
+                k = qkv[:, hq:hq + hk].view(T, c.n_kv_heads, c.head_dim)
+            else:
+                q, k = layer_ops.rope_qk(qkv, positions, self.cos, self.sin, c.n_heads, c.n_kv_heads, c.head_dim)
             v = qkv[:, hq + hk:].view(T, c.n_kv_heads, c.head_dim)
             attn = attention(i, q, k, v)
             x = layer_ops.rms_norm(F.linear(attn, L["w_o"]), L["ln2"], c.rms_eps, residual=h)
@@ -135,10 +146,12 @@ class Qwen2Paged:
     def forward(self, token_ids: torch.Tensor, positions: torch.Tensor, seq_slices: list[tuple[int, int]],
                 block_tables: list[list[int]], context_lens: list[int], kv_cache: PagedKVCache) -> torch.Tensor:
         """Logits [n_seqs, vocab] (fp32) for the last token of each sequence (model.py:101-158)."""
-        def attention(i, q, k, v):
-            kv_cache.write(i, k, v, positions, seq_slices, block_tables)
-            return kv_cache.attention(i, q, positions, seq_slices, block_tables, context_lens)
+        rope = self.rope if self.fused_rope else None
 
-        x = self.run_layers(token_ids, positions, attention)
+        def attention(i, q, k, v):
+            kv_cache.write(i, k, v, positions, seq_slices, block_tables, rope=rope)
+            return kv_cache.attention(i, q, positions, seq_slices, block_tables, context_lens, rope=rope)
+
+        x = self.run_layers(token_ids, positions, attention, fused_rope=self.fused_rope)
         last = torch.tensor([e - 1 for _, e in seq_slices], device=x.device)
         return F.linear(x[last], self.lm_head).float()

@@ -37,6 +37,27 @@ def _check_pool(pool: torch.Tensor) -> tuple[int, int, int, int]:
     return nb, hkv, bs, d
 
 
+class Rope:
+    """RoPE tables for the fused rotations: fp32 cos / sin [max_position, head_dim / 2]
+    on the GPU (the angles of the reference's _rope, model.py:74-76)."""
+
+    def __init__(self, cos: torch.Tensor, sin: torch.Tensor):
+        for name, t in (("cos", cos), ("sin", sin)):
+            _lib.require_gpu_tensor(name, t)
+            if t.dtype != torch.float32 or t.dim() != 2 or not t.is_contiguous():
+                raise TypeError(f"rope {name} must be a contiguous fp32 [max_position, head_dim/2] tensor")
+        if cos.shape != sin.shape:
+            raise ValueError("rope cos and sin differ in shape")
+        self.cos, self.sin = cos, sin
+        self.max_position, self.half = cos.shape
+
+    def check(self, head_dim: int, device: torch.device) -> None:
+        if 2 * self.half != head_dim:
+            raise ValueError(f"rope tables are for head_dim {2 * self.half}, not {head_dim}")
+        if self.cos.device != device:
+            raise ValueError("rope tables are on another device")
+
+
 def _rows_view(name: str, t: torch.Tensor, n_heads: int, d: int) -> int:
     """Validate a [T, n_heads, D] (or [T, n_heads*D]) tensor with contiguous rows; return its row stride."""
     if t.dim() == 3:
@@ -54,8 +75,11 @@ def _rows_view(name: str, t: torch.Tensor, n_heads: int, d: int) -> int:
     return t.stride(0) if t.shape[0] > 1 else n_heads * d
 
 
-def kv_append(pool: torch.Tensor, k: torch.Tensor, v: torch.Tensor, slot_mapping: torch.Tensor) -> None:
-    """K1: pool[slot] <- (k, v) for every token with slot >= 0 (reference kv_cache.py:25-38)."""
+def kv_append(pool: torch.Tensor, k: torch.Tensor, v: torch.Tensor, slot_mapping: torch.Tensor,
+              rope: Rope | None = None, positions: torch.Tensor | None = None) -> None:
+    """K1: pool[slot] <- (k, v) for every token with slot >= 0 (reference kv_cache.py:25-38).
+    With ``rope`` (and int64 device ``positions``) k is rotated at its position on the way
+    (tb_kv_append_rope: the reference's _rope of k, model.py:72-80, folded into the write)."""
     nb, hkv, bs, d = _check_pool(pool)
     for name, t in (("k", k), ("v", v)):
         _lib.require_gpu_tensor(name, t)
@@ -68,10 +92,21 @@ def kv_append(pool: torch.Tensor, k: torch.Tensor, v: torch.Tensor, slot_mapping
         raise ValueError("k, v and slot_mapping disagree on the number of tokens")
     if slot_mapping.dtype != torch.int32 or not slot_mapping.is_cuda or not slot_mapping.is_contiguous():
         raise TypeError("slot_mapping must be a contiguous int32 GPU tensor")
-    st = _lib.lib().tb_kv_append(k.data_ptr(), ks, v.data_ptr(), vs, pool.data_ptr(), nb,
-                                 slot_mapping.data_ptr(), T, hkv, d, bs,
-                                 _lib.DTYPE_CODE[pool.dtype], _lib.stream_handle(pool.device))
-    _lib.check(st, "tb_kv_append")
+    if rope is None:
+        st = _lib.lib().tb_kv_append(k.data_ptr(), ks, v.data_ptr(), vs, pool.data_ptr(), nb,
+                                     slot_mapping.data_ptr(), T, hkv, d, bs,
+                                     _lib.DTYPE_CODE[pool.dtype], _lib.stream_handle(pool.device))
+        _lib.check(st, "tb_kv_append")
+        return
+    rope.check(d, pool.device)
+    if (positions is None or positions.dtype != torch.int64 or not positions.is_cuda
+            or not positions.is_contiguous() or positions.numel() != T):
+        raise TypeError("rope needs positions: a contiguous int64 GPU tensor with one entry per token")
+    st = _lib.lib().tb_kv_append_rope(k.data_ptr(), ks, v.data_ptr(), vs, pool.data_ptr(), nb,
+                                      slot_mapping.data_ptr(), positions.data_ptr(), rope.cos.data_ptr(),
+                                      rope.sin.data_ptr(), rope.max_position, T, hkv, d, bs,
+                                      _lib.DTYPE_CODE[pool.dtype], _lib.stream_handle(pool.device))
+    _lib.check(st, "tb_kv_append_rope")
 
 
 def kv_gather(pool: torch.Tensor, table: torch.Tensor, context_len: int) -> tuple[torch.Tensor, torch.Tensor]:
@@ -126,13 +161,15 @@ def workspace_for(meta: StepMetadata, num_heads: int, head_dim: int,
 def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, num_heads: int,
                     scale: float | None = None, out: torch.Tensor | None = None,
                     k_new: torch.Tensor | None = None, v_new: torch.Tensor | None = None,
-                    workspace: torch.Tensor | None = None) -> torch.Tensor:
+                    workspace: torch.Tensor | None = None, rope: Rope | None = None) -> torch.Tensor:
     """K2: paged attention of every query row of the step (reference model.py:130-147).
 
     q: [T, num_heads, head_dim]; returns out [T, num_heads * head_dim] in q's dtype
     (rows outside every sequence slice are left untouched). With k_new/v_new
     ([T, kv_heads, head_dim]) the kernel also appends each decode row's new
-    K/V (fused append); this requires a decode-only step.
+    K/V (fused append); this requires a decode-only step. With ``rope`` q (and
+    k_new) hold the projections before rotation: each row is rotated at its
+    position row_ctx - 1 inside the kernels (model.py:72-80,125 folded in).
     """
     nb, hkv, bs, d = _check_pool(pool)
     _lib.require_gpu_tensor("q", q)
@@ -162,6 +199,8 @@ def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, 
                          f"{rows_per_item(q.dtype, num_heads, hkv)}")
     if scale is None:
         scale = 1.0 / math.sqrt(d)   # scaled_dot_product_attention's default (model.py:140,146)
+    if rope is not None:
+        rope.check(d, q.device)
     ksp = vsp = None
     ks = vs = 0
     if k_new is not None or v_new is not None:
@@ -189,7 +228,9 @@ def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, 
         meta.split_rows.data_ptr(), meta.num_split_rows,
         max(meta.max_parts_per_row, 1), meta.partition_tokens, meta.total_partitions,
         num_heads, hkv, d, bs, float(scale), _lib.DTYPE_CODE[q.dtype],
-        ksp, ks, vsp, vs, _ptr(ws), ws_bytes, _ptr(meta.device_counts), _lib.stream_handle(q.device))
+        ksp, ks, vsp, vs, _ptr(ws), ws_bytes, _ptr(meta.device_counts),
+        None if rope is None else rope.cos.data_ptr(), None if rope is None else rope.sin.data_ptr(),
+        0 if rope is None else rope.max_position, _lib.stream_handle(q.device))
     _lib.check(st, "tb_paged_attention")
     return out
 
