@@ -162,3 +162,34 @@ def test_decode_graph_replays_match_eager_steps_bf16():
         assert torch.equal(a[:sum(len(t) for t in tables)].view(torch.int16)[:, 1],
                            b[:sum(len(t) for t in tables)].view(torch.int16)[:, 1]) or \
             torch.allclose(a.float(), b.float(), atol=2e-2, rtol=2e-2)
+
+
+@pytest.mark.parametrize("graphs", [True, False])
+def test_swap_preemption_gives_the_tokens_of_an_unpressured_run(graphs):
+    """preemption="swap" under block pressure: victims' blocks go to pinned host
+    memory (K3 gather) and come back into other block ids (K3 scatter); greedy
+    outputs are those of a run with room for everything (block ids never change
+    what attention computes). Recompute preemption regenerates the same tokens."""
+    mc = small_cfg(layers=2, heads=4, kv_heads=2)
+    model = Qwen2Paged(mc, DEV, torch.float32, seed=11)
+    g = torch.Generator().manual_seed(12)
+    prompts = [torch.randint(0, mc.vocab_size, (n,), generator=g).tolist() for n in (40, 33, 50, 20, 47)]
+    max_new = [40, 45, 30, 50, 38]
+
+    def run(num_blocks, preemption):
+        ecfg = EngineConfig(dtype="float32", num_blocks=num_blocks, block_size=16, max_batch_tokens=256,
+                            max_running=5, decode_graphs=graphs, preemption=preemption)
+        eng = LLMEngine(ecfg, model=model)
+        reqs = [eng.add_request(p, max_new_tokens=m) for p, m in zip(prompts, max_new)]
+        while eng.scheduler.has_work():
+            eng.step()
+        return [r.output_token_ids for r in reqs], eng, reqs
+
+    want, eng, _ = run(96, "swap")
+    assert eng.swap_outs == 0
+    got, eng, reqs = run(16, "swap")
+    assert got == want
+    assert eng.swap_outs > 0 and eng.swap_ins == eng.swap_outs and not eng.scheduler.swapped
+    assert sum(r.preemptions for r in reqs) == eng.swap_outs
+    got_rc, eng_rc, reqs_rc = run(16, "recompute")
+    assert got_rc == want and sum(r.preemptions for r in reqs_rc) > 0

@@ -5,9 +5,9 @@ from tinybatch_amd.config import EngineConfig
 from tinybatch_amd.scheduler import Request, Scheduler, Status
 
 
-def sched(max_batch_tokens=64, num_blocks=16, block_size=4, max_running=8, prefix=False):
+def sched(max_batch_tokens=64, num_blocks=16, block_size=4, max_running=8, prefix=False, preemption="recompute"):
     cfg = EngineConfig(max_batch_tokens=max_batch_tokens, num_blocks=num_blocks, block_size=block_size,
-                       max_running=max_running, enable_prefix_caching=prefix)
+                       max_running=max_running, enable_prefix_caching=prefix, preemption=preemption)
     return Scheduler(cfg, BlockManager(num_blocks, block_size, prefix))
 
 
@@ -67,6 +67,42 @@ def test_youngest_is_preempted_under_memory_pressure():
     assert b.status is Status.WAITING and b.preemptions >= 1 and b.output_token_ids == []
     assert a.status is Status.RUNNING
     assert s.waiting[0] is b                                 # back at the head of the queue
+
+
+def test_swap_preemption_keeps_tokens_and_resumes_first():
+    """preemption="swap": the victim keeps its tokens, its written blocks are listed
+    for a swap-out in the step that preempts it, nothing new is admitted while it
+    waits, and it resumes in fresh blocks listed for a swap-in."""
+    s = sched(num_blocks=4, block_size=4, preemption="swap")
+    a, b = req(8, max_new=64), req(7, max_new=64, base=100)
+    s.add(a)
+    s.add(b)
+    run_step(s)
+    swap_out = None
+    for _ in range(12):
+        batch = run_step(s)
+        if b.status is Status.SWAPPED:
+            swap_out = batch.swap_out
+            break
+    assert b.status is Status.SWAPPED and b.preemptions == 1 and b.block_table == []
+    kept = list(b.output_token_ids)
+    assert len(kept) >= 1                                    # the sampled tokens survive the preemption
+    written = b.context_len() - 1                            # positions 0 .. context_len - 2 hold K/V
+    assert [r for r, _ in swap_out] == [b] and len(swap_out[0][1]) == -(-written // 4) == b.swap_blocks
+    assert a in batch.decode and b not in batch.decode
+    s.add(req(3, base=200))
+    batch = run_step(s)                                      # still short of blocks: b waits, so does the new one
+    assert not batch.prefill and b.status is Status.SWAPPED
+    s.finish(a)
+    batch = run_step(s)
+    assert [r for r, _ in batch.swap_in] == [b] and b in batch.decode   # b first; the new one may follow
+    blocks = batch.swap_in[0][1]
+    assert len(blocks) == b.swap_blocks and b.block_table[:len(blocks)] == blocks
+    assert b.output_token_ids[:len(kept)] == kept and b.status is Status.RUNNING
+    # room for the position the step writes (run_step has appended its sampled token since)
+    assert len(b.block_table) * 4 >= b.context_len() - 1
+    used = set(b.block_table) | {x for r in batch.prefill for x in r.block_table}
+    assert len(s.bm.free_ids) + len(s.bm.evictable) + len(used) == 4
 
 
 def test_decode_slot_covers_the_written_position():

@@ -115,6 +115,20 @@ class BlockManager:
             table.append(blk.block_id)
         return table, cached
 
+    def allocate_private(self, num_blocks: int, token_ids: list[int]) -> list[int]:
+        """A table of fresh, uncached blocks for ``token_ids`` (a sequence coming back
+        from host memory: its contents are copied in, not looked up in the prefix cache)."""
+        if num_blocks > self.num_free():
+            raise OutOfBlocks(f"{num_blocks} blocks requested, {self.num_free()} free")
+        bs = self.block_size
+        table = []
+        for b in range(num_blocks):
+            blk = self._fresh()
+            blk.ref_count = 1
+            blk.token_ids = list(token_ids[b * bs:(b + 1) * bs])
+            table.append(blk.block_id)
+        return table
+
     def append_slot(self, table: list[int], seq_token_ids: list[int]) -> bool:
         """Make room for the token at index len(seq_token_ids) (call it before
         that token joins the sequence). Returns True when a block was added."""

@@ -21,6 +21,10 @@ class EngineConfig:
     max_batch_tokens: int = 2048
     max_running: int = 32
     max_model_len: int = 4096
+    # "recompute": a preempted sequence restarts from its prompt (the reference,
+    # scheduler.py:141-149); "swap": its KV blocks go to pinned host memory
+    # (K3 gather) and come back (K3 scatter) when blocks are free again
+    preemption: str = "recompute"
     # sampling defaults
     max_new_tokens: int = 256
     temperature: float = 0.0

@@ -57,6 +57,9 @@ class LLMEngine:
         self.graph_steps = 0
         self.graphs = (DecodeGraphs(self.model, self.kv_cache, self.cfg.max_running, self.cfg.max_model_len)
                        if self.cfg.decode_graphs else None)
+        self.swap_outs = 0
+        self.swap_ins = 0
+        self._swap_reads: list[torch.Tensor] = []   # host copies read by the last step's swap-ins
 
     # ---- API -----------------------------------------------------------------
     def add_request(self, prompt_token_ids: list[int], *, max_new_tokens: int | None = None,
@@ -102,8 +105,27 @@ class LLMEngine:
             context_lens.append(req.context_len())
         return token_ids, positions, seq_slices, block_tables, context_lens
 
+    def _swap(self, batch) -> None:
+        """Run the step's swaps on the compute stream, ahead of its forward: swap-outs
+        read blocks that this step may hand to others, swap-ins fill the blocks the
+        resumed sequences decode from (K3 gather / scatter to pinned host memory)."""
+        self._swap_reads = []          # the previous step ended with a synchronising copy
+        L = self.model.cfg.n_layers
+        for req, blocks in batch.swap_out:
+            staging = torch.empty((L, len(blocks)) + tuple(self.kv_cache.pools[0].shape[1:]),
+                                  dtype=self.dtype, pin_memory=True)
+            self.kv_cache.swap_out(blocks, list(staging))
+            req.swap_staging = staging
+            self.swap_outs += 1
+        for req, blocks in batch.swap_in:
+            self.kv_cache.swap_in(list(req.swap_staging), blocks)
+            self._swap_reads.append(req.swap_staging)
+            req.swap_staging = None
+            self.swap_ins += 1
+
     def step(self) -> list[StepOutput]:
         batch = self.scheduler.schedule()
+        self._swap(batch)
         if batch.is_empty():
             return []
         ordered = batch.prefill + batch.decode
@@ -158,4 +180,5 @@ class LLMEngine:
         bm = self.block_manager
         return {"kv_pool_mb": round(self.kv_cache.memory_bytes() / 2**20, 1), "free_blocks": bm.num_free(),
                 "prefix_hit_rate": round(bm.hit_rate(), 3), "running": len(self.scheduler.running),
-                "waiting": len(self.scheduler.waiting), "steps": self.steps, "graph_steps": self.graph_steps}
+                "waiting": len(self.scheduler.waiting), "swapped": len(self.scheduler.swapped), "steps": self.steps,
+                "graph_steps": self.graph_steps, "swap_outs": self.swap_outs, "swap_ins": self.swap_ins}

@@ -5,7 +5,12 @@ every running sequence decodes one token per step; waiting requests are
 admitted first come first served while the step's token budget, the running
 cap and the pool allow (scheduler.py:112-130); a decode that cannot get a
 slot preempts the youngest running sequence, whose blocks are freed and which
-restarts from its prompt (scheduler.py:92-110,141-154).
+restarts from its prompt (scheduler.py:92-110,141-154). With
+``preemption="swap"`` the preempted sequence keeps its tokens instead: the
+blocks holding its written positions are listed for a swap-out to host
+memory (the engine runs it before the step's forward, so blocks reused in the
+same step are read first), and it resumes, before any new admission, in fresh
+blocks filled by a swap-in.
 
 One deliberate difference: the decode slot is reserved for the position the
 step writes. The engine writes the last sampled token at position
@@ -32,6 +37,7 @@ _ids = itertools.count()
 class Status(Enum):
     WAITING = "waiting"
     RUNNING = "running"
+    SWAPPED = "swapped"
     FINISHED = "finished"
 
 
@@ -50,6 +56,8 @@ class Request:
     first_token_time: float | None = None
     finish_time: float | None = None
     preemptions: int = 0
+    swap_blocks: int = 0                    # blocks held in host memory while swapped
+    swap_staging: object = field(default=None, repr=False)   # the host copy (set by the engine)
 
     def all_token_ids(self) -> list[int]:
         return self.prompt_token_ids + self.output_token_ids
@@ -62,6 +70,8 @@ class Request:
 class ScheduledBatch:
     prefill: list[Request]
     decode: list[Request]
+    swap_out: list[tuple[Request, list[int]]] = field(default_factory=list)   # (request, pool blocks to save)
+    swap_in: list[tuple[Request, list[int]]] = field(default_factory=list)    # (request, pool blocks to fill)
 
     def is_empty(self) -> bool:
         return not self.prefill and not self.decode
@@ -73,12 +83,16 @@ class Scheduler:
         self.bm = block_manager
         self.waiting: list[Request] = []
         self.running: list[Request] = []
+        self.swapped: list[Request] = []
+        if config.preemption not in ("recompute", "swap"):
+            raise ValueError(f"unknown preemption mode {config.preemption!r}")
+        self._swap_out: list[tuple[Request, list[int]]] = []
 
     def add(self, req: Request) -> None:
         self.waiting.append(req)
 
     def has_work(self) -> bool:
-        return bool(self.waiting or self.running)
+        return bool(self.waiting or self.running or self.swapped)
 
     def _reserve_decode_slot(self, req: Request) -> None:
         # room for the position this step writes: context_len - 1
@@ -86,6 +100,7 @@ class Scheduler:
 
     def schedule(self) -> ScheduledBatch:
         budget = self.cfg.max_batch_tokens
+        self._swap_out = []
         decode: list[Request] = []
         for req in list(self.running):
             if req.status is not Status.RUNNING:
@@ -104,6 +119,24 @@ class Scheduler:
             budget -= 1
         decode = [r for r in decode if r.status is Status.RUNNING]
 
+        swap_in: list[tuple[Request, list[int]]] = []
+        while self.swapped and not self._swap_out and budget > 0 and len(self.running) < self.cfg.max_running:
+            req = self.swapped[0]
+            need = req.swap_blocks + (1 if (req.context_len() - 1) % self.bm.block_size == 0 else 0)
+            if need > self.bm.num_free():
+                break
+            self.swapped.pop(0)
+            req.block_table = self.bm.allocate_private(req.swap_blocks, req.all_token_ids()[:-1])
+            self._reserve_decode_slot(req)
+            req.status = Status.RUNNING
+            self.running.append(req)
+            swap_in.append((req, req.block_table[:req.swap_blocks]))
+            decode.append(req)
+            budget -= 1
+        if self.swapped:
+            # swapped sequences resume first: no new admission while any waits
+            return ScheduledBatch(prefill=[], decode=decode, swap_out=self._swap_out, swap_in=swap_in)
+
         prefill: list[Request] = []
         while self.waiting and len(self.running) < self.cfg.max_running:
             req = self.waiting[0]
@@ -118,7 +151,7 @@ class Scheduler:
             self.running.append(req)
             prefill.append(req)
             budget -= n - req.num_cached_tokens
-        return ScheduledBatch(prefill=prefill, decode=decode)
+        return ScheduledBatch(prefill=prefill, decode=decode, swap_out=self._swap_out, swap_in=swap_in)
 
     def finish(self, req: Request) -> None:
         req.status = Status.FINISHED
@@ -129,8 +162,19 @@ class Scheduler:
 
     def _preempt(self, req: Request) -> None:
         req.preemptions += 1
-        req.status = Status.WAITING
         self.running.remove(req)
+        if self.cfg.preemption == "swap" and req.output_token_ids:
+            # keep the tokens: positions 0 .. context_len - 2 are written, the last
+            # sampled token is written by the step that resumes it
+            written = req.context_len() - 1
+            req.swap_blocks = self.bm.blocks_needed(written)
+            self._swap_out.append((req, list(req.block_table[:req.swap_blocks])))
+            self.bm.free_table(req.block_table)
+            req.block_table = []
+            req.status = Status.SWAPPED
+            self.swapped.insert(0, req)
+            return
+        req.status = Status.WAITING
         self.bm.free_table(req.block_table)
         req.block_table = []
         req.output_token_ids = []                         # recompute from the prompt
