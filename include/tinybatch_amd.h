@@ -233,6 +233,18 @@ int32_t tb_rope_qk(const void* qkv, int64_t row_stride, const int64_t* positions
 int32_t tb_silu_mul(const void* gate_up, int64_t row_stride, void* out, int64_t out_row_stride,
                     int32_t rows, int32_t d_ff, int32_t dtype, hipStream_t stream);
 
+/* Skinny linear layer (engine layer, not the KV path): the projections of the
+ * reference's layer (src/tinybatch/model.py:121-124,149-154, F.linear with a
+ * [out_features][in_features] weight) at decode batch sizes:
+ *   y[r][n] = sum_k x[r][k] * w[n][k] (+ bias[n])   for rows <= 64,
+ * fp16 / bf16, fp32 accumulation, rounded once to the element type.
+ * out_features % 16 == 0 and in_features % 32 == 0 (TB_ERR_UNSUPPORTED
+ * otherwise, and for more than 64 rows); x, w 16-byte aligned, rows strided.
+ */
+int32_t tb_linear(const void* x, int64_t x_row_stride, const void* w, const void* bias,
+                  void* y, int64_t y_row_stride, int32_t rows, int32_t out_features,
+                  int32_t in_features, int32_t dtype, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

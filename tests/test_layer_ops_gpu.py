@@ -59,3 +59,22 @@ def test_silu_mul(dtype):
     got = layer_ops.silu_mul(gu.to(DEV), 4864)
     want = F.silu(gu[:, :4864]) * gu[:, 4864:]                   # the reference's two tensor ops
     torch.testing.assert_close(got.cpu().float(), want.float(), **TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n,k", [(1152, 896), (896, 896), (9728, 896), (896, 4864), (48, 64)])
+def test_linear_against_fp32_matmul(dtype, n, k):
+    """tb_linear against a float32 matmul of the same 16-bit inputs: one rounding
+    of an fp32 accumulation (bias included), rows 1 .. 64, strided rows."""
+    g = torch.Generator().manual_seed(n + k)
+    w = (torch.randn(n, k, generator=g) * 0.05).to(dtype)
+    b = (torch.randn(n, generator=g) * 0.05).to(dtype)
+    for rows in (1, 7, 16, 33, 64):
+        xs = torch.randn(rows, k + 32, generator=g).to(dtype)[:, 16:16 + k]   # strided rows
+        want = xs.float() @ w.float().t() + b.float()
+        got = layer_ops.linear(xs.to(DEV), w.to(DEV), b.to(DEV))
+        torch.testing.assert_close(got.cpu().float(), want, atol=1e-2, rtol=1e-2)
+        got = layer_ops.linear(xs.to(DEV), w.to(DEV))
+        torch.testing.assert_close(got.cpu().float(), want - b.float(), atol=1e-2, rtol=1e-2)
+    with pytest.raises(RuntimeError):   # more than 64 rows: not this kernel's shape
+        layer_ops.linear(torch.zeros(65, k, dtype=dtype, device=DEV), w.to(DEV))

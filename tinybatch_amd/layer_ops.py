@@ -69,3 +69,28 @@ def silu_mul(gate_up: torch.Tensor, d_ff: int) -> torch.Tensor:
                                 _lib.DTYPE_CODE[gate_up.dtype], _lib.stream_handle(gate_up.device))
     _lib.check(st, "tb_silu_mul")
     return out
+
+
+def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None,
+           out: torch.Tensor | None = None) -> torch.Tensor:
+    """F.linear for decode-sized batches (rows <= 64, fp16/bf16; tb_linear): the
+    weight is streamed once, fp32 accumulation, one rounding (model.py:121-154)."""
+    if x.dim() != 2 or weight.dim() != 2 or x.shape[1] != weight.shape[1]:
+        raise ValueError("x must be [rows, in_features] and weight [out_features, in_features]")
+    for name, t in (("x", x), ("weight", weight)):
+        _lib.require_gpu_tensor(name, t)
+        if t.dtype != x.dtype or t.stride(-1) != 1:
+            raise ValueError(f"{name} must share x's dtype and have contiguous rows")
+    if not weight.is_contiguous():
+        raise ValueError("weight must be contiguous")
+    rows, (n, k) = x.shape[0], weight.shape
+    if bias is not None and (bias.dtype != x.dtype or bias.shape != (n,) or not bias.is_contiguous()):
+        raise ValueError("bias must be a contiguous [out_features] tensor in x's dtype")
+    if out is None:
+        out = torch.empty(rows, n, device=x.device, dtype=x.dtype)
+    st = _lib.lib().tb_linear(x.data_ptr(), x.stride(0) if rows > 1 else k, weight.data_ptr(),
+                              None if bias is None else bias.data_ptr(), out.data_ptr(),
+                              out.stride(0) if rows > 1 else n, rows, n, k, _lib.DTYPE_CODE[x.dtype],
+                              _lib.stream_handle(x.device))
+    _lib.check(st, "tb_linear")
+    return out

@@ -116,6 +116,14 @@ class Qwen2Paged:
             w[p + "mlp.down_proj.weight"] = L["w_down"]
         return w
 
+    def _proj(self, x: torch.Tensor, w: torch.Tensor, b: torch.Tensor | None = None) -> torch.Tensor:
+        """q/k/v and o projections: the weight-streaming tb_linear for decode-sized
+        batches of 16-bit rows (measured faster than the library GEMM at these shapes
+        for up to 32 rows), F.linear otherwise."""
+        if x.shape[0] <= 32 and x.dtype in (torch.float16, torch.bfloat16):
+            return layer_ops.linear(x, w, b)
+        return F.linear(x, w, b)
+
     def run_layers(self, token_ids: torch.Tensor, positions: torch.Tensor, attention,
                    fused_rope: bool = False) -> torch.Tensor:
         """Hidden states after the final norm, [T, d_model]. ``attention(layer, q, k, v)``
@@ -128,7 +136,7 @@ class Qwen2Paged:
         h = F.embedding(token_ids, self.embed)                       # the residual stream
         x = layer_ops.rms_norm(h, self.layers[0]["ln1"], c.rms_eps)
         for i, L in enumerate(self.layers):
-            qkv = F.linear(x, L["w_qkv"], L["b_qkv"])
+            qkv = self._proj(x, L["w_qkv"], L["b_qkv"])
             if fused_rope:
                 q = qkv[:, :hq].view(T, c.n_heads, c.head_dim)
                 k = qkv[:, hq:hq + hk].view(T, c.n_kv_heads, c.head_dim)
@@ -136,7 +144,7 @@ class Qwen2Paged:
                 q, k = layer_ops.rope_qk(qkv, positions, self.cos, self.sin, c.n_heads, c.n_kv_heads, c.head_dim)
             v = qkv[:, hq + hk:].view(T, c.n_kv_heads, c.head_dim)
             attn = attention(i, q, k, v)
-            x = layer_ops.rms_norm(F.linear(attn, L["w_o"]), L["ln2"], c.rms_eps, residual=h)
+            x = layer_ops.rms_norm(self._proj(attn, L["w_o"]), L["ln2"], c.rms_eps, residual=h)
             act = layer_ops.silu_mul(F.linear(x, L["w_gu"]), c.d_ff)
             nxt = self.layers[i + 1]["ln1"] if i + 1 < len(self.layers) else self.norm
             x = layer_ops.rms_norm(F.linear(act, L["w_down"]), nxt, c.rms_eps, residual=h)
