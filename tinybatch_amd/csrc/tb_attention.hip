@@ -677,13 +677,14 @@ struct prefill_shape {
   static constexpr int RB = 2 * D;             // bytes per K or V row
   static constexpr int KS = D / 32;            // q.k k-slices
   static constexpr int NSL = D / 16;           // O^T slices of 16 dims
-  static constexpr int RS = RB + 16;           // LDS row stride: 16-byte aligned, K-row and V-column reads conflict-free
+  static constexpr int RS = RB + 16;           // K row stride in LDS: the 16-byte row reads of 16 lanes hit distinct banks
+  static constexpr int RSV = RB + 32;          // V row stride: the 4 rows of a transpose read start 8 banks apart
   static constexpr int CK = 64;                // positions per chunk
   static constexpr int NCH = PART_TILE / CK;   // chunks per partition
   static constexpr int VCOLS = RB / 16;        // 16-byte pieces of a row
   static constexpr int LPT = CK * VCOLS / 256; // 16-byte loads per thread per chunk, of K and of V each
-  static constexpr int VTS = 2 * CK + 8;       // V^T row stride (bytes): 8-byte aligned rows
-  static constexpr int LDS = CK * RS + D * VTS;
+  static constexpr int LDS = CK * RS + CK * RSV;
+  static constexpr int PF = LPT <= 2 ? 2 : 1;  // chunks loaded ahead (register sets; D = 128 has room for one)
   static_assert(LPT >= 1 && (CK * VCOLS) % 256 == 0 && PART_TILE % CK == 0, "chunk split");
 };
 
@@ -695,10 +696,10 @@ void paged_prefill_mfma_kernel(const attn_args a) {
   typedef typename M::vec8_t vec8_t;
   typedef typename M::scalar_t scalar_t;
   constexpr int RB = S::RB, KS = S::KS, NSL = S::NSL, RS = S::RS, CK = S::CK, NCH = S::NCH;
-  constexpr int VCOLS = S::VCOLS, LPT = S::LPT, VTS = S::VTS, EB = 2;
+  constexpr int VCOLS = S::VCOLS, LPT = S::LPT, RSV = S::RSV, EB = 2;
   __shared__ __align__(16) char lds[S::LDS];
   char* const k_lds = lds;
-  char* const vt_lds = lds + CK * RS;
+  char* const v_lds = lds + CK * RS;
 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lc = lane & 15, lg = lane >> 4;
   const int item = blockIdx.x / a.num_heads;
@@ -782,9 +783,7 @@ void paged_prefill_mfma_kernel(const attn_args a) {
       const int f = threadIdx.x + 256 * i;
       const int r = f / VCOLS, d0 = 8 * (f % VCOLS);
       st16(k_lds + r * RS + 2 * d0, kr[i]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e)   // V^T[d0 + e][r]
-        *reinterpret_cast<uint16_t*>(vt_lds + (d0 + e) * VTS + 2 * r) = (uint16_t)(vr[i].w[e >> 1] >> (16 * (e & 1)));
+      st16(v_lds + r * RSV + 2 * d0, vr[i]);
     }
     __syncthreads();   // chunk staged
   };
@@ -837,11 +836,13 @@ void paged_prefill_mfma_kernel(const attn_args a) {
         pb[j] = (scalar_t)sc[2 * u][j];
         pb[4 + j] = (scalar_t)sc[2 * u + 1][j];
       }
-      const char* vrow = vt_lds + lc * VTS + 2 * (32 * u + 4 * lg);
+      // A operand lane (lg, lc): V[position of k = 8lg + j][16nn + lc], by transpose
+      // reads of rows 32u + 4lg + 0..3 (and 16 further), elements 4 (lc & 3) ..
+      const char* vrow = v_lds + (32 * u + 4 * lg + (lc >> 2)) * RSV + 8 * (lc & 3);
 #pragma unroll
       for (int nn = 0; nn < NSL; ++nn) {
-        const uint2 lo = *reinterpret_cast<const uint2*>(vrow + 16 * nn * VTS);
-        const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16 * nn * VTS + 32);
+        const uint2 lo = lds_read_tr16(vrow + 32 * nn);
+        const uint2 hi = lds_read_tr16(vrow + 16 * RSV + 32 * nn);
         vec16 va;
         va.w[0] = lo.x; va.w[1] = lo.y; va.w[2] = hi.x; va.w[3] = hi.y;
         acc[nn] = M::mfma(__builtin_bit_cast(vec8_t, va), pb, acc[nn]);
@@ -849,24 +850,38 @@ void paged_prefill_mfma_kernel(const attn_args a) {
     }
   };
 
+  // K/V of chunk c + PF are loaded into registers while chunk c is computed
+  // (PF register sets; LDS holds the chunk being computed)
   int ids[LPT];
-  vec16 kr[LPT], vr[LPT];
+  vec16 kr0[LPT], vr0[LPT], kr1[LPT], vr1[LPT];
   load_ids(c0, ids);
-  load_kv(c0, ids, kr, vr);
+  load_kv(c0, ids, kr0, vr0);
   load_ids(c0 + 1, ids);
+  if constexpr (S::PF == 2) {
+    load_kv(c0 + 1, ids, kr1, vr1);
+    load_ids(c0 + 2, ids);
+  }
   if (a.rope.cos && my_row < nrows) {   // RoPE of q at the row's position (slices s and s + KS/2 pair)
     const int64_t r = a.rope.row(pos0 + my_row, D / 2) + 8 * lg;
 #pragma unroll
     for (int s = 0; s < KS / 2; ++s)
       rope_pair<scalar_t>(qb[s], qb[s + KS / 2], a.rope.cos + r + 32 * s, a.rope.sin + r + 32 * s);
   }
-  for (int c = c0; c < c_end; ++c) {   // workgroup-uniform trip count
+  auto iter = [&](int c, vec16 (&kr)[LPT], vec16 (&vr)[LPT]) {
     stage(kr, vr);
-    if (c + 1 < c_end) {   // the next chunk's loads are in flight during the compute
-      load_kv(c + 1, ids, kr, vr);
-      load_ids(c + 2, ids);
+    if (c + S::PF < c_end) {
+      load_kv(c + S::PF, ids, kr, vr);
+      load_ids(c + S::PF + 1, ids);
     }
     compute(c);
+  };
+  if constexpr (S::PF == 2) {
+    for (int c = c0; c < c_end; c += 2) {   // workgroup-uniform trip count
+      iter(c, kr0, vr0);
+      if (c + 1 < c_end) iter(c + 1, kr1, vr1);
+    }
+  } else {
+    for (int c = c0; c < c_end; ++c) iter(c, kr0, vr0);
   }
 
   const float l = sum_xor32(sum_xor16(l_part));
