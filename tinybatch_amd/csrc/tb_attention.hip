@@ -526,15 +526,14 @@ void paged_attn_mfma_kernel(const attn_args a) {
       for (int s = 0; s < KS; ++s)
         sc[t] = M::mfma(__builtin_bit_cast(vec8_t, kd[t][s]), __builtin_bit_cast(vec8_t, qb[s]), sc[t]);
     }
-    float cm = -INFINITY;
 #pragma unroll
     for (int t = 0; t < TILES; ++t)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float v = (wb + 16 * t + 4 * lg + j) < n_col ? sc[t][j] * a.scale_log2e : -INFINITY;
-        sc[t][j] = v;
-        cm = fmaxf(cm, v);
-      }
+      for (int j = 0; j < 4; ++j)
+        sc[t][j] = (wb + 16 * t + 4 * lg + j) < n_col ? sc[t][j] * a.scale_log2e : -INFINITY;
+    float cm = max_f32(sc[0][0], sc[0][1]);
+#pragma unroll
+    for (int e = 2; e < TILES * 4; e += 2) cm = max3_f32(cm, sc[e >> 2][e & 3], sc[e >> 2][(e & 3) + 1]);
     m_w = max_xor32(max_xor16(cm));
     // a column whose visible positions all lie before this wave's range gets p = 0
     const float m_safe = m_w == -INFINITY ? 0.f : m_w;
@@ -770,10 +769,17 @@ void paged_prefill_mfma_kernel(const attn_args a) {
   }
 
   float m = -INFINITY;       // reference max of row lc (scaled, base-2 domain)
-  float l_part = 0.f;        // this lane's share of row lc's sum, relative to m
   float4_t acc[NSL];         // O^T[16n + 4lg + j][row lc], relative to m
 #pragma unroll
   for (int nn = 0; nn < NSL; ++nn) acc[nn] = float4_t{0.f, 0.f, 0.f, 0.f};
+  // The row sums ride on the matrix unit: an A operand whose first row is all
+  // ones turns P into sum_k P[k][row] in element 0 of lanes 0..15 (D[0][row]),
+  // one MFMA per 32 positions instead of 16 adds per lane per chunk. The sum
+  // is of the rounded P that multiplies V.
+  float4_t acc_l = float4_t{0.f, 0.f, 0.f, 0.f};
+  vec8_t ones;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ones[j] = (scalar_t)(lc == 0 ? 1.f : 0.f);
 
   // stage one chunk (already in registers) in LDS
   auto stage = [&](const vec16 (&kr)[LPT], const vec16 (&vr)[LPT]) {
@@ -807,15 +813,15 @@ void paged_prefill_mfma_kernel(const attn_args a) {
         for (int j = 0; j < 4; ++j)
           if (cb + 16 * t + 4 * lg + j > my_pos) sc[t][j] = -INFINITY;
     }
-    float cm = fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3]));
+    float cm = max_f32(sc[0][0], sc[0][1]);
 #pragma unroll
-    for (int t = 1; t < 4; ++t) cm = fmaxf(cm, fmaxf(fmaxf(sc[t][0], sc[t][1]), fmaxf(sc[t][2], sc[t][3])));
+    for (int e = 2; e < 16; e += 2) cm = max3_f32(cm, sc[e >> 2][e & 3], sc[e >> 2][(e & 3) + 1]);
     cm = max_xor32(max_xor16(cm)) * a.scale_log2e;   // the row's chunk max, scaled (-inf if all masked)
     if (__any(cm > m + 8.f)) {   // some row outgrew its reference: move every row's reference up
       const float m_new = fmaxf(m, cm);
       const float alpha = fast_exp2(m - (m_new == -INFINITY ? 0.f : m_new));   // 0 while m = -inf
       m = m_new;
-      l_part *= alpha;
+      acc_l *= alpha;
 #pragma unroll
       for (int nn = 0; nn < NSL; ++nn) acc[nn] *= alpha;
     }
@@ -823,10 +829,7 @@ void paged_prefill_mfma_kernel(const attn_args a) {
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        sc[t][j] = fast_exp2(fmaf(sc[t][j], a.scale_log2e, neg_m));
-        l_part += sc[t][j];
-      }
+      for (int j = 0; j < 4; ++j) sc[t][j] = fast_exp2(fmaf(sc[t][j], a.scale_log2e, neg_m));
     // k index 8lg+j <-> position 32u + 4lg + j (j < 4) or 32u + 16 + 4lg + (j-4)
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
@@ -847,6 +850,7 @@ void paged_prefill_mfma_kernel(const attn_args a) {
         va.w[0] = lo.x; va.w[1] = lo.y; va.w[2] = hi.x; va.w[3] = hi.y;
         acc[nn] = M::mfma(__builtin_bit_cast(vec8_t, va), pb, acc[nn]);
       }
+      acc_l = M::mfma(ones, pb, acc_l);
     }
   };
 
@@ -884,7 +888,7 @@ void paged_prefill_mfma_kernel(const attn_args a) {
     for (int c = c0; c < c_end; ++c) iter(c, kr0, vr0);
   }
 
-  const float l = sum_xor32(sum_xor16(l_part));
+  const float l = __shfl(acc_l[0], lc);   // row lc's sum sits in lane lc
   if (my_row < nrows && part < nparts) {   // rows that end before this partition own no slot here
     const int row = row0 + my_row;
     if (nparts == 1) {           // the whole row: final output
