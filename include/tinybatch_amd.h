@@ -245,6 +245,36 @@ int32_t tb_linear(const void* x, int64_t x_row_stride, const void* w, const void
                   void* y, int64_t y_row_stride, int32_t rows, int32_t out_features,
                   int32_t in_features, int32_t dtype, hipStream_t stream);
 
+/* Split-K pieces of tb_linear (no bias) for a projection whose output goes
+ * straight into tb_rms_norm_partials (o_proj and down_proj, model.py:149,154):
+ * with S = in_features / 32 k-slices of 32, range s of the `splits` ranges
+ * (1 <= splits <= min(64, S)) holds slices [s*S/splits, (s+1)*S/splits) and
+ *   partials[s][r][n] = sum over range s of x[r][k] * w[n][k]   (fp32, unrounded).
+ * partials is float [splits][rows][out_features], contiguous. */
+int32_t tb_linear_partials(const void* x, int64_t x_row_stride, const void* w, float* partials,
+                           int32_t splits, int32_t rows, int32_t out_features, int32_t in_features,
+                           int32_t dtype, hipStream_t stream);
+
+/* gate/up projection fused with the SwiGLU gate (model.py:151-154):
+ * w_gate_up = [2 d_ff][in_features] (gate rows, then up rows);
+ *   y[r][c] = silu(T(g)) * T(u),  g = x[r] . w[c],  u = x[r] . w[d_ff + c],
+ * with the roundings of tb_linear followed by tb_silu_mul (the same bits for
+ * the same launch shape). d_ff % 16 == 0; other limits as tb_linear. */
+int32_t tb_linear_silu_mul(const void* x, int64_t x_row_stride, const void* w_gate_up, void* y,
+                           int64_t y_row_stride, int32_t rows, int32_t d_ff, int32_t in_features,
+                           int32_t dtype, hipStream_t stream);
+
+/* tb_rms_norm whose input is the projection output held as split-K partials
+ * (tb_linear_partials): x[r] = T(partials[0][r] + ... + partials[splits-1][r])
+ * (fp32 adds in split order, one rounding), then the residual add and RMSNorm
+ * of tb_rms_norm. fp16 / bf16; splits in {1, 2, 4, 8}; dim % 8 == 0,
+ * dim <= 4096; partials, residual, weight, out 16-byte aligned with row
+ * strides that are multiples of 8 elements. */
+int32_t tb_rms_norm_partials(const float* partials, int32_t splits, void* residual,
+                             int64_t residual_row_stride, const void* weight, void* out,
+                             int64_t out_row_stride, int32_t rows, int32_t dim, float eps,
+                             int32_t dtype, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

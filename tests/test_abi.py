@@ -109,3 +109,27 @@ def test_copy_rejects_bad_arguments_without_launching():
     assert L.tb_block_copy(f, 2, 16, f, f, 0, 4096, None) == _lib.TB_OK
     assert L.tb_block_gather(f, 16, f, 3, f, 0, None) == _lib.TB_ERR_INVALID_ARG
     assert L.tb_block_scatter(f, f, 0, f, 3, 4096, None) == _lib.TB_ERR_INVALID_ARG   # empty pool
+
+
+def test_layer_ops_reject_bad_arguments_without_launching():
+    L = _lib.lib()
+    f = ctypes.c_void_p(4096)
+    bf16 = 2
+    lp = L.tb_linear_partials
+    assert lp(f, 896, f, f, 0, 4, 896, 896, bf16, None) == _lib.TB_ERR_INVALID_ARG     # no K range
+    assert lp(f, 64, f, f, 3, 4, 896, 64, bf16, None) == _lib.TB_ERR_INVALID_ARG       # 3 ranges of 2 k-slices
+    assert lp(f, 896, f, f, 4, 65, 896, 896, bf16, None) == _lib.TB_ERR_UNSUPPORTED    # more than 64 rows
+    assert lp(f, 896, f, f, 4, 4, 896, 896, 0, None) == _lib.TB_ERR_UNSUPPORTED        # fp32
+    assert lp(f, 896, f, None, 4, 4, 896, 896, bf16, None) == _lib.TB_ERR_INVALID_ARG  # no output
+    assert lp(None, 896, None, None, 4, 0, 896, 896, bf16, None) == _lib.TB_OK         # zero rows
+    ls = L.tb_linear_silu_mul
+    assert ls(f, 896, f, f, 4864, 4, 4856, 896, bf16, None) == _lib.TB_ERR_UNSUPPORTED  # d_ff % 16
+    assert ls(f, 896, f, f, 100, 4, 4864, 896, bf16, None) == _lib.TB_ERR_INVALID_ARG   # short output rows
+    assert ls(ctypes.c_void_p(4104), 896, f, f, 4864, 4, 4864, 896, bf16, None) == _lib.TB_ERR_INVALID_ARG
+    rp = L.tb_rms_norm_partials
+    assert rp(f, 3, None, 0, f, f, 896, 4, 896, 1e-6, bf16, None) == _lib.TB_ERR_UNSUPPORTED      # 3 splits
+    assert rp(f, 4, None, 0, f, f, 900, 4, 900, 1e-6, bf16, None) == _lib.TB_ERR_UNSUPPORTED      # dim % 8
+    assert rp(f, 4, None, 0, f, f, 896, 4, 896, 1e-6, 0, None) == _lib.TB_ERR_UNSUPPORTED         # fp32
+    assert rp(f, 4, f, 900, f, f, 896, 4, 896, 1e-6, bf16, None) == _lib.TB_ERR_INVALID_ARG       # residual stride
+    assert rp(ctypes.c_void_p(4100), 4, None, 0, f, f, 896, 4, 896, 1e-6, bf16, None) == _lib.TB_ERR_INVALID_ARG
+    assert rp(None, 4, None, 0, None, None, 896, 0, 896, 1e-6, bf16, None) == _lib.TB_OK

@@ -54,6 +54,37 @@ def test_forward_logits_match_oracle_fp32_mixed_step():
         torch.testing.assert_close(cache.pools[layer].cpu(), pools[layer], atol=1e-5, rtol=1e-5)
 
 
+def test_fused_mlp_bf16_forward_as_close_to_the_oracle_as_the_library_path():
+    """Decode-sized bf16 batches (<= 32 rows) with the split-K o/down
+    projections and gate/up + SwiGLU fused (fused_mlp) against the same model
+    on the library GEMMs: both against the fp32 oracle of the same bf16
+    weights, the fused path no further off than twice the library path."""
+    mc = small_cfg(layers=2, heads=4, kv_heads=2)
+    model = Qwen2Paged(mc, DEV, torch.bfloat16, seed=11)
+    w = cpu_weights(model)
+    BS, NB = 16, 32
+    g = torch.Generator().manual_seed(12)
+    tables = [[5, 9], [11, 3]]
+    p0 = torch.randint(0, mc.vocab_size, (20,), generator=g).tolist()
+    p1 = torch.randint(0, mc.vocab_size, (10,), generator=g).tolist()
+    steps = [(p0 + p1, list(range(20)) + list(range(10)), [(0, 20), (20, 30)], [20, 10]),
+             ([7, 8], [20, 10], [(0, 1), (1, 2)], [21, 11])]
+    pools = [torch.zeros(NB, 2, mc.n_kv_heads, BS, mc.head_dim) for _ in range(mc.n_layers)]
+    want = [mref.forward(w, mc, torch.tensor(ids), torch.tensor(pos), sl, tables, ctx, pools, BS)
+            for ids, pos, sl, ctx in steps]
+    errs = {}
+    for fused in (False, True):
+        model.fused_mlp = fused
+        cache = PagedKVCache(mc.n_layers, NB, BS, mc.n_kv_heads, mc.head_dim, DEV, torch.bfloat16)
+        errs[fused] = 0.0
+        for (ids, pos, sl, ctx), ref in zip(steps, want):
+            got = model.forward(torch.tensor(ids, device=DEV), torch.tensor(pos, device=DEV), sl, tables, ctx, cache)
+            errs[fused] = max(errs[fused], float((got.cpu() - ref).abs().max()))
+    scale = max(float(r.abs().max()) for r in want)
+    assert errs[False] < 0.05 * scale, errs
+    assert errs[True] <= 2 * errs[False] + 1e-3 * scale, errs
+
+
 def oracle_generate(model, ecfg, prompts, max_new):
     """The engine loop with the CPU restatement as the forward pass."""
     mc = model.cfg

@@ -1,6 +1,7 @@
 """The fused layer kernels against the oracle's restatement of the reference
 ops (oracle/model_reference.py, CPU): RMSNorm with and without the residual
-add, RoPE of q and k from qkv rows, SiLU * up."""
+add, RoPE of q and k from qkv rows, SiLU * up; the weight-streaming
+projections against float32 products of the same 16-bit inputs."""
 import pytest
 import torch
 import torch.nn.functional as F
@@ -78,3 +79,66 @@ def test_linear_against_fp32_matmul(dtype, n, k):
         torch.testing.assert_close(got.cpu().float(), want - b.float(), atol=1e-2, rtol=1e-2)
     with pytest.raises(RuntimeError):   # more than 64 rows: not this kernel's shape
         layer_ops.linear(torch.zeros(65, k, dtype=dtype, device=DEV), w.to(DEV))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n,k,splits", [(896, 896, 4), (896, 4864, 8), (48, 64, 2), (64, 96, 3)])
+def test_linear_partials_are_the_products_of_their_k_ranges(dtype, n, k, splits):
+    """tb_linear_partials: piece s is the fp32 product over k-slices
+    [s*S/splits, (s+1)*S/splits) of the 16-bit inputs (S = k/32), so the pieces
+    sum to the whole product; rows 1..32, strided rows, both tile shapes."""
+    g = torch.Generator().manual_seed(n + k + splits)
+    w = (torch.randn(n, k, generator=g) * 0.05).to(dtype)
+    S = k // 32
+    for rows in (1, 9, 16, 32):
+        xs = torch.randn(rows, k + 32, generator=g).to(dtype)[:, 16:16 + k]     # strided rows
+        parts = layer_ops.linear_partials(xs.to(DEV), w.to(DEV), splits).cpu()
+        assert parts.shape == (splits, rows, n) and parts.dtype == torch.float32
+        for s in range(splits):
+            lo, hi = 32 * (s * S // splits), 32 * ((s + 1) * S // splits)
+            want = xs[:, lo:hi].float() @ w[:, lo:hi].float().t()
+            torch.testing.assert_close(parts[s], want, atol=1e-4, rtol=1e-4)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("d_ff,k", [(4864, 896), (48, 64)])
+def test_linear_silu_mul_bits_of_linear_then_silu_mul(dtype, d_ff, k):
+    """gate/up fused with the SwiGLU gate gives the bits of tb_linear followed by
+    tb_silu_mul (d_ff 4864: four tiles per workgroup; 48: two), and stays within
+    the dtype's tolerance of silu(gate) * up from one fp32 product."""
+    g = torch.Generator().manual_seed(d_ff + k)
+    w = (torch.randn(2 * d_ff, k, generator=g) * 0.05).to(dtype)
+    wd = w.to(DEV)
+    for rows in (1, 7, 16, 33, 64):
+        x = torch.randn(rows, k, generator=g).to(dtype)
+        got = layer_ops.linear_silu_mul(x.to(DEV), wd)
+        two_step = layer_ops.silu_mul(layer_ops.linear(x.to(DEV), wd), d_ff)
+        assert torch.equal(got.view(torch.int16), two_step.view(torch.int16)), rows
+        gu = (x.float() @ w.float().t()).to(dtype)                  # F.linear: one rounding
+        want = F.silu(gu[:, :d_ff]) * gu[:, d_ff:]
+        torch.testing.assert_close(got.cpu().float(), want.float(), **TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dim,splits", [(896, 4), (896, 8), (4096, 1), (136, 2)])
+def test_rms_norm_partials(dtype, dim, splits):
+    """x = one rounding of the fp32 pieces added in split order; the residual
+    sum is bit-exact (the tensor add of the reference layer) and the norm
+    within tolerance of the oracle's RMSNorm; 37 rows (not a multiple of the
+    four rows per workgroup)."""
+    g = torch.Generator().manual_seed(dim + splits)
+    rows = 37
+    parts = torch.randn(splits, rows, dim, generator=g) * 2
+    r = torch.randn(rows, dim, generator=g).to(dtype)
+    w = (1 + 0.1 * torch.randn(dim, generator=g)).to(dtype)
+    acc = parts[0].clone()
+    for s in range(1, splits):
+        acc = acc + parts[s]
+    x = acc.to(dtype)
+    res = r.to(DEV)
+    got = layer_ops.rms_norm_partials(parts.to(DEV), w.to(DEV), 1e-6, residual=res)
+    h = r + x
+    assert torch.equal(res.cpu(), h)
+    torch.testing.assert_close(got.cpu().float(), mref.rms_norm(h, w, 1e-6).float(), **TOL[dtype])
+    got = layer_ops.rms_norm_partials(parts.to(DEV), w.to(DEV), 1e-6)
+    torch.testing.assert_close(got.cpu().float(), mref.rms_norm(x, w, 1e-6).float(), **TOL[dtype])

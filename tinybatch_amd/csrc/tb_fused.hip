@@ -7,6 +7,8 @@
 //   tb_rms_norm  : [h = x + residual;] out = (h * rsqrt(mean(h^2) + eps)) * w  (model.py:65-69,149)
 //   tb_rope_qk   : rotate-half RoPE of q and k, straight from the qkv GEMM rows  (model.py:72-80,125)
 //   tb_silu_mul  : silu(gate) * up of the gate/up GEMM rows                       (model.py:151-154)
+//   tb_rms_norm_partials : tb_rms_norm whose x is the sum of split-K partials of
+//                  the projection before it (o_proj, down_proj: model.py:149,154)
 // Rounding follows the PyTorch ops they replace: the residual sum and silu(g)
 // are rounded to the element type before their next use.
 #include "tb_common.h"
@@ -66,6 +68,100 @@ __global__ __launch_bounds__(NORM_THREADS) void rms_norm_kernel(const T* x, int6
   for (int k = 0; k < NORM_MAX_PER_THREAD; ++k) {
     const int i = threadIdx.x + k * NORM_THREADS;
     if (i < dim) orow[i] = from_f<T>((h[k] * inv) * to_f(w[i]));
+  }
+}
+
+// ---- RMSNorm of split-K partial sums (+ residual add) ---------------------------
+// x = T(sum over s of partials[s][row]) is the projection output (the split-K
+// pieces of tb_linear_partials, added in split order and rounded once, like
+// F.linear's output); then the residual add and RMSNorm of rms_norm_kernel.
+// One wave per row, four rows per workgroup; lane owns the 8-element chunks
+// lane, lane + 64, ... (CH of them), every load issued before any use.
+template <typename T, int S, int CH>
+__global__ __launch_bounds__(256) void rms_norm_partials_kernel(const float* __restrict__ part, int rows, int dim,
+                                                                T* res, int64_t rs, const T* __restrict__ w,
+                                                                T* out, int64_t os, float eps) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  struct x8 {
+    T v[8];
+  };
+  const int chunks = dim >> 3;
+  const int64_t plane = (int64_t)rows * dim;
+  float4_t p[CH][S][2];
+  vec16 rv[CH], wv[CH];
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    const int c = min(lane + 64 * i, chunks - 1);       // lanes past the row repeat its last chunk, unused
+    const float* src = part + (int64_t)row * dim + 8 * c;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      p[i][s][0] = *reinterpret_cast<const float4_t*>(src + s * plane);
+      p[i][s][1] = *reinterpret_cast<const float4_t*>(src + s * plane + 4);
+    }
+    if (res) rv[i] = ld16(res + row * rs + 8 * c);
+    wv[i] = ld16(w + 8 * c);
+  }
+  float h[CH][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    const bool mine = lane + 64 * i < chunks;
+    const x8 r = __builtin_bit_cast(x8, rv[i]);
+    x8 sum;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float acc = p[i][0][e >> 2][e & 3];
+#pragma unroll
+      for (int s = 1; s < S; ++s) acc += p[i][s][e >> 2][e & 3];
+      float v = to_f(from_f<T>(acc));                  // the projection's output rounding
+      if (res) {
+        sum.v[e] = from_f<T>(v + to_f(r.v[e]));        // h = h + delta, rounded like the tensor add
+        v = to_f(sum.v[e]);
+      }
+      h[i][e] = v;
+      if (mine) ss += v * v;
+    }
+    if (res && mine) st16(res + row * rs + 8 * (lane + 64 * i), __builtin_bit_cast(vec16, sum));
+  }
+  ss += __shfl_xor(ss, 1);
+  ss += __shfl_xor(ss, 2);
+  ss += __shfl_xor(ss, 4);
+  ss += __shfl_xor(ss, 8);
+  ss += __shfl_xor(ss, 16);
+  ss += __shfl_xor(ss, 32);
+  const float inv = rsqrtf(ss / (float)dim + eps);
+#pragma unroll
+  for (int i = 0; i < CH; ++i) {
+    if (lane + 64 * i >= chunks) continue;
+    const x8 wt = __builtin_bit_cast(x8, wv[i]);
+    x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o.v[e] = from_f<T>((h[i][e] * inv) * to_f(wt.v[e]));
+    st16(out + row * os + 8 * (lane + 64 * i), __builtin_bit_cast(vec16, o));
+  }
+}
+
+template <typename T, int S>
+static void launch_norm_partials_ch(int ch, dim3 grid, const float* part, int rows, int dim, T* res, int64_t rs,
+                                    const T* w, T* out, int64_t os, float eps, hipStream_t stream) {
+  switch (ch) {
+    case 1: hipLaunchKernelGGL((rms_norm_partials_kernel<T, S, 1>), grid, dim3(256), 0, stream, part, rows, dim, res, rs, w, out, os, eps); break;
+    case 2: hipLaunchKernelGGL((rms_norm_partials_kernel<T, S, 2>), grid, dim3(256), 0, stream, part, rows, dim, res, rs, w, out, os, eps); break;
+    case 4: hipLaunchKernelGGL((rms_norm_partials_kernel<T, S, 4>), grid, dim3(256), 0, stream, part, rows, dim, res, rs, w, out, os, eps); break;
+    default: hipLaunchKernelGGL((rms_norm_partials_kernel<T, S, 8>), grid, dim3(256), 0, stream, part, rows, dim, res, rs, w, out, os, eps); break;
+  }
+}
+
+template <typename T>
+static void launch_norm_partials(int splits, int ch, const float* part, int rows, int dim, T* res, int64_t rs,
+                                 const T* w, T* out, int64_t os, float eps, hipStream_t stream) {
+  const dim3 grid((rows + 3) / 4);
+  switch (splits) {
+    case 1: launch_norm_partials_ch<T, 1>(ch, grid, part, rows, dim, res, rs, w, out, os, eps, stream); break;
+    case 2: launch_norm_partials_ch<T, 2>(ch, grid, part, rows, dim, res, rs, w, out, os, eps, stream); break;
+    case 4: launch_norm_partials_ch<T, 4>(ch, grid, part, rows, dim, res, rs, w, out, os, eps, stream); break;
+    default: launch_norm_partials_ch<T, 8>(ch, grid, part, rows, dim, res, rs, w, out, os, eps, stream); break;
   }
 }
 
@@ -195,5 +291,29 @@ extern "C" int32_t tb_silu_mul(const void* gate_up, int64_t row_stride, void* ou
       break;
     default: return TB_ERR_INVALID_ARG;
   }
+  TB_RETURN_LAUNCH_STATUS();
+}
+
+extern "C" int32_t tb_rms_norm_partials(const float* partials, int32_t splits, void* residual,
+                                        int64_t residual_row_stride, const void* weight, void* out,
+                                        int64_t out_row_stride, int32_t rows, int32_t dim, float eps, int32_t dtype,
+                                        hipStream_t stream) {
+  using namespace tb;
+  TB_CHECK_ARG(rows >= 0 && dim > 0);
+  if (dtype != TB_DTYPE_F16 && dtype != TB_DTYPE_BF16) return TB_ERR_UNSUPPORTED;
+  if (dim % 8 != 0 || dim > 64 * 8 * 8) return TB_ERR_UNSUPPORTED;
+  if (splits != 1 && splits != 2 && splits != 4 && splits != 8) return TB_ERR_UNSUPPORTED;
+  if (rows == 0) return TB_OK;
+  TB_CHECK_ARG(partials && weight && out && out_row_stride >= dim && out_row_stride % 8 == 0);
+  TB_CHECK_ARG(!residual || (residual_row_stride >= dim && residual_row_stride % 8 == 0));
+  TB_CHECK_ARG((((uintptr_t)partials | (uintptr_t)weight | (uintptr_t)out | (uintptr_t)residual) & 15u) == 0);
+  const int chunks = dim / 8;
+  const int ch = chunks <= 64 ? 1 : chunks <= 128 ? 2 : chunks <= 256 ? 4 : 8;
+  if (dtype == TB_DTYPE_F16)
+    launch_norm_partials<_Float16>(splits, ch, partials, rows, dim, (_Float16*)residual, residual_row_stride,
+                                   (const _Float16*)weight, (_Float16*)out, out_row_stride, eps, stream);
+  else
+    launch_norm_partials<__bf16>(splits, ch, partials, rows, dim, (__bf16*)residual, residual_row_stride,
+                                 (const __bf16*)weight, (__bf16*)out, out_row_stride, eps, stream);
   TB_RETURN_LAUNCH_STATUS();
 }

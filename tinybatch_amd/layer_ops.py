@@ -71,10 +71,7 @@ def silu_mul(gate_up: torch.Tensor, d_ff: int) -> torch.Tensor:
     return out
 
 
-def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None,
-           out: torch.Tensor | None = None) -> torch.Tensor:
-    """F.linear for decode-sized batches (rows <= 64, fp16/bf16; tb_linear): the
-    weight is streamed once, fp32 accumulation, one rounding (model.py:121-154)."""
+def _linear_operands(x: torch.Tensor, weight: torch.Tensor) -> tuple[int, int, int]:
     if x.dim() != 2 or weight.dim() != 2 or x.shape[1] != weight.shape[1]:
         raise ValueError("x must be [rows, in_features] and weight [out_features, in_features]")
     for name, t in (("x", x), ("weight", weight)):
@@ -83,14 +80,78 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
             raise ValueError(f"{name} must share x's dtype and have contiguous rows")
     if not weight.is_contiguous():
         raise ValueError("weight must be contiguous")
-    rows, (n, k) = x.shape[0], weight.shape
+    rows, k = x.shape
+    return rows, weight.shape[0], x.stride(0) if rows > 1 else k
+
+
+def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None,
+           out: torch.Tensor | None = None) -> torch.Tensor:
+    """F.linear for decode-sized batches (rows <= 64, fp16/bf16; tb_linear): the
+    weight is streamed once, fp32 accumulation, one rounding (model.py:121-154)."""
+    rows, n, xs = _linear_operands(x, weight)
+    k = x.shape[1]
     if bias is not None and (bias.dtype != x.dtype or bias.shape != (n,) or not bias.is_contiguous()):
         raise ValueError("bias must be a contiguous [out_features] tensor in x's dtype")
     if out is None:
         out = torch.empty(rows, n, device=x.device, dtype=x.dtype)
-    st = _lib.lib().tb_linear(x.data_ptr(), x.stride(0) if rows > 1 else k, weight.data_ptr(),
+    st = _lib.lib().tb_linear(x.data_ptr(), xs, weight.data_ptr(),
                               None if bias is None else bias.data_ptr(), out.data_ptr(),
                               out.stride(0) if rows > 1 else n, rows, n, k, _lib.DTYPE_CODE[x.dtype],
                               _lib.stream_handle(x.device))
     _lib.check(st, "tb_linear")
+    return out
+
+
+def linear_partials(x: torch.Tensor, weight: torch.Tensor, splits: int) -> torch.Tensor:
+    """Split-K pieces of F.linear(x, weight) (no bias; tb_linear_partials): float32
+    [splits, rows, out_features] whose sum over dim 0 is the product, for
+    rms_norm_partials to add, round and normalise (model.py:149,154)."""
+    rows, n, xs = _linear_operands(x, weight)
+    parts = torch.empty(splits, rows, n, device=x.device, dtype=torch.float32)
+    st = _lib.lib().tb_linear_partials(x.data_ptr(), xs, weight.data_ptr(), parts.data_ptr(), splits, rows, n,
+                                       x.shape[1], _lib.DTYPE_CODE[x.dtype], _lib.stream_handle(x.device))
+    _lib.check(st, "tb_linear_partials")
+    return parts
+
+
+def linear_silu_mul(x: torch.Tensor, w_gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """silu(x W_gate^T) * (x W_up^T) for the merged [2 d_ff, in] gate/up weight
+    (model.py:151-154; tb_linear_silu_mul): the bits of linear() then silu_mul()."""
+    rows, n, xs = _linear_operands(x, w_gate_up)
+    d_ff = n // 2
+    if n % 2:
+        raise ValueError("w_gate_up must hold gate and up rows (an even row count)")
+    if out is None:
+        out = torch.empty(rows, d_ff, device=x.device, dtype=x.dtype)
+    st = _lib.lib().tb_linear_silu_mul(x.data_ptr(), xs, w_gate_up.data_ptr(), out.data_ptr(),
+                                       out.stride(0) if rows > 1 else d_ff, rows, d_ff, x.shape[1],
+                                       _lib.DTYPE_CODE[x.dtype], _lib.stream_handle(x.device))
+    _lib.check(st, "tb_linear_silu_mul")
+    return out
+
+
+def rms_norm_partials(partials: torch.Tensor, weight: torch.Tensor, eps: float, *,
+                      residual: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """rms_norm() of x = partials.sum(0) rounded to weight's dtype (tb_rms_norm_partials):
+    the projection output of linear_partials, then the residual add and RMSNorm."""
+    _lib.require_gpu_tensor("partials", partials)
+    if partials.dim() != 3 or partials.dtype != torch.float32 or not partials.is_contiguous():
+        raise ValueError("partials must be a contiguous float32 [splits, rows, dim] tensor")
+    splits, rows, dim = partials.shape
+    _lib.require_gpu_tensor("weight", weight)
+    if weight.shape != (dim,) or not weight.is_contiguous():
+        raise ValueError("weight must be a contiguous [dim] tensor")
+    rs = 0
+    if residual is not None:
+        rs = _row_stride("residual", residual, dim)
+        if residual.shape != (rows, dim) or residual.dtype != weight.dtype:
+            raise ValueError("residual must be [rows, dim] in weight's dtype")
+    if out is None:
+        out = torch.empty(rows, dim, dtype=weight.dtype, device=weight.device)
+    os_ = _row_stride("out", out, dim)
+    st = _lib.lib().tb_rms_norm_partials(partials.data_ptr(), splits,
+                                         None if residual is None else residual.data_ptr(), rs,
+                                         weight.data_ptr(), out.data_ptr(), os_, rows, dim, float(eps),
+                                         _lib.DTYPE_CODE[weight.dtype], _lib.stream_handle(weight.device))
+    _lib.check(st, "tb_rms_norm_partials")
     return out

@@ -15,7 +15,11 @@ SwiGLU gate are one fused kernel each (layer_ops) instead of chains of tensor
 ops; the RoPE tables are built once for every position up to max_position;
 the LM head runs on the last rows only. With ``fused_rope`` (the default) the
 RoPE of q and k is folded into the paged kernels (K1 rotates k on its way to
-the pool, K2 rotates q as it loads it) instead of a launch of its own.
+the pool, K2 rotates q as it loads it) instead of a launch of its own. With
+``fused_mlp`` (the default) decode-sized batches of 16-bit rows take the
+weight-streaming projections: o_proj and down_proj as split-K partials that
+the residual add + RMSNorm launch after them adds up, gate/up fused with the
+SwiGLU gate.
 
 Weights are drawn from a seeded generator (no checkpoint exists offline):
 N(0, 0.02) for embeddings, projections and biases, ones for the norms.
@@ -97,6 +101,7 @@ class Qwen2Paged:
         self.cos, self.sin = rope_tables(c.head_dim, c.rope_theta, c.max_position, self.device)
         self.rope = ops.Rope(self.cos, self.sin)
         self.fused_rope = True
+        self.fused_mlp = True
 
     def reference_weights(self) -> dict[str, torch.Tensor]:
         """The weights under the reference's state-dict names (model.py:97-98,111-151)."""
@@ -116,11 +121,19 @@ class Qwen2Paged:
             w[p + "mlp.down_proj.weight"] = L["w_down"]
         return w
 
+    # Split-K ranges of the partial projections: o_proj (K = d_model) and
+    # down_proj (K = d_ff), measured at the 0.5B shapes for 1..32 rows.
+    O_SPLITS, DOWN_SPLITS = 4, 8
+
+    @staticmethod
+    def _streamed(x: torch.Tensor) -> bool:
+        """Decode-sized batches of 16-bit rows take the weight-streaming kernels
+        (measured faster than the library GEMM at these shapes for up to 32 rows)."""
+        return x.shape[0] <= 32 and x.dtype in (torch.float16, torch.bfloat16)
+
     def _proj(self, x: torch.Tensor, w: torch.Tensor, b: torch.Tensor | None = None) -> torch.Tensor:
-        """q/k/v and o projections: the weight-streaming tb_linear for decode-sized
-        batches of 16-bit rows (measured faster than the library GEMM at these shapes
-        for up to 32 rows), F.linear otherwise."""
-        if x.shape[0] <= 32 and x.dtype in (torch.float16, torch.bfloat16):
+        """q/k/v and o projections: tb_linear for decode-sized batches, F.linear otherwise."""
+        if self._streamed(x):
             return layer_ops.linear(x, w, b)
         return F.linear(x, w, b)
 
@@ -144,9 +157,16 @@ class Qwen2Paged:
                 q, k = layer_ops.rope_qk(qkv, positions, self.cos, self.sin, c.n_heads, c.n_kv_heads, c.head_dim)
             v = qkv[:, hq + hk:].view(T, c.n_kv_heads, c.head_dim)
             attn = attention(i, q, k, v)
+            nxt = self.layers[i + 1]["ln1"] if i + 1 < len(self.layers) else self.norm
+            if self.fused_mlp and self._streamed(x):
+                parts = layer_ops.linear_partials(attn, L["w_o"], self.O_SPLITS)
+                x = layer_ops.rms_norm_partials(parts, L["ln2"], c.rms_eps, residual=h)
+                act = layer_ops.linear_silu_mul(x, L["w_gu"])
+                parts = layer_ops.linear_partials(act, L["w_down"], self.DOWN_SPLITS)
+                x = layer_ops.rms_norm_partials(parts, nxt, c.rms_eps, residual=h)
+                continue
             x = layer_ops.rms_norm(self._proj(attn, L["w_o"]), L["ln2"], c.rms_eps, residual=h)
             act = layer_ops.silu_mul(F.linear(x, L["w_gu"]), c.d_ff)
-            nxt = self.layers[i + 1]["ln1"] if i + 1 < len(self.layers) else self.norm
             x = layer_ops.rms_norm(F.linear(act, L["w_down"]), nxt, c.rms_eps, residual=h)
         return x
 
