@@ -101,19 +101,27 @@ def test_linear_partials_are_the_products_of_their_k_ranges(dtype, n, k, splits)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("d_ff,k", [(4864, 896), (48, 64)])
-def test_linear_silu_mul_bits_of_linear_then_silu_mul(dtype, d_ff, k):
-    """gate/up fused with the SwiGLU gate gives the bits of tb_linear followed by
-    tb_silu_mul (d_ff 4864: four tiles per workgroup; 48: two), and stays within
-    the dtype's tolerance of silu(gate) * up from one fp32 product."""
+@pytest.mark.parametrize("d_ff,k", [(4864, 896), (48, 64), (64, 1024)])
+def test_linear_silu_mul_rounds_like_linear_then_silu_mul(dtype, d_ff, k):
+    """gate/up fused with the SwiGLU gate. Integer-valued inputs make every
+    product and sum exact in any order, which pins the epilogue bit for bit:
+    T(gate) and T(up) rounded once, then tb_silu_mul's arithmetic (and
+    tb_linear's one rounding of the same sums). Random inputs stay within the
+    dtype's tolerance of silu(gate) * up from one fp32 product. d_ff 4864:
+    four tiles per workgroup; 48: two; k 1024: two staging passes at 33+ rows."""
     g = torch.Generator().manual_seed(d_ff + k)
+    wi = torch.randint(-2, 3, (2 * d_ff, k), generator=g).to(dtype)
     w = (torch.randn(2 * d_ff, k, generator=g) * 0.05).to(dtype)
-    wd = w.to(DEV)
+    wid, wd = wi.to(DEV), w.to(DEV)
     for rows in (1, 7, 16, 33, 64):
+        xi = torch.randint(-2, 3, (rows, k), generator=g).to(dtype)
+        exact = (xi.float() @ wi.float().t()).to(dtype)             # exact integer sums, one rounding
+        got = layer_ops.linear_silu_mul(xi.to(DEV), wid)
+        want = layer_ops.silu_mul(exact.to(DEV), d_ff)
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), rows
+        assert torch.equal(layer_ops.linear(xi.to(DEV), wid).cpu().view(torch.int16), exact.view(torch.int16)), rows
         x = torch.randn(rows, k, generator=g).to(dtype)
         got = layer_ops.linear_silu_mul(x.to(DEV), wd)
-        two_step = layer_ops.silu_mul(layer_ops.linear(x.to(DEV), wd), d_ff)
-        assert torch.equal(got.view(torch.int16), two_step.view(torch.int16)), rows
         gu = (x.float() @ w.float().t()).to(dtype)                  # F.linear: one rounding
         want = F.silu(gu[:, :d_ff]) * gu[:, d_ff:]
         torch.testing.assert_close(got.cpu().float(), want.float(), **TOL[dtype])

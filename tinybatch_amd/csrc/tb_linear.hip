@@ -3,29 +3,33 @@
 // [N][K], K contiguous):
 //   Y[M][N] = X[M][K] . W[N][K]^T (+ bias[N]),   M <= 64.
 // At decode batch sizes the weight is the whole cost (N*K*2 bytes read once,
-// X and Y are a few KB), so the kernels are weight streams: a workgroup owns
-// NT tiles of 16 output columns and one K range, which its waves split; a wave
-// issues the loads of its whole K share (up to KB 32-wide k-slices per pass)
-// before its MFMAs.
-//   v_mfma_f32_16x16x32_{f16,bf16}: A = X rows (m-tile of 16), B = W rows read
-//   straight from HBM (lane l: W[n0 + l%16][k + 8(l/16) .. +8], 16 bytes),
+// X and Y are a few KB), so the kernels are weight streams. A workgroup of
+// four waves owns TW tiles of 16 output columns and one K range; the
+// 4 / TW waves of a tile split the range between them.
+//   v_mfma_f32_16x16x32_{f16,bf16}: A = X rows (m-tile of 16) from LDS,
+//   B = W rows straight from HBM (lane l: W[n0 + l%16][k + 8(l/16) .. +8]),
 //   C/D lane l: Y[m0 + 4(l/16) + j][n0 + l%16].
-// One load instruction reads 64 bytes of each of 16 W rows; the other half of
-// each 128-byte line is the next k-slice's load. W therefore goes through
-// plain loads that keep the line: non-temporal ones measured 5-25% slower
-// (the 151936 x 896 LM head at one row: 64.6 vs 50.6 us).
-// The waves' partial sums meet in LDS. Three epilogues:
+// X reaches LDS by row-contiguous direct loads (global_load_lds, consecutive
+// lanes along a row, whole 128-byte lines per instruction) and is read from
+// there in the MFMA layout; the row pitch is 1 mod 16 units of 16 bytes, so
+// the 16 rows one read touches fall in 16 different bank groups. Reading X
+// from memory in the MFMA layout (16 rows x 64 bytes per instruction, half of
+// each line) had cost as much as the weight stream itself: for the 9728 x 896
+// gate/up weight at 32 rows, 9.5 us against 6.1 us for the same bytes read
+// row-contiguously, 4.8 us for the weight alone (load-pattern probe).
+// W keeps the MFMA-layout loads into registers (all of a wave's loads for the
+// K range in flight at once); the other half of each of their lines is the
+// next k-slice's load, so they are plain loads that keep the line
+// (non-temporal ones measured 5-25% slower).
+// Three epilogues, after the tile's waves meet in LDS:
 //   round   : Y = T(sum + bias), one rounding as F.linear's single GEMM;
 //   partial : fp32 sums of one K range to partials[split][M][N] (the split-K
 //             pieces; tb_rms_norm_partials adds them in split order, rounds
 //             once and continues with the residual add and RMSNorm);
-//   silu    : the workgroup's two tiles are gate columns c and up columns
-//             d_ff + c of the merged gate/up weight; Y = silu(T(gate)) * T(up)
+//   silu    : tiles j < TW/2 are gate columns, tile j + TW/2 the up columns
+//             d_ff later (merged gate/up weight); Y = silu(T(gate)) * T(up)
 //             with the roundings of F.linear followed by tb_silu_mul
 //             (model.py:151-154).
-// A tile's sum does not depend on the epilogue or on NT: for equal K ranges
-// and wave counts the silu epilogue gives the bits of the round epilogue
-// followed by tb_silu_mul.
 #include "tb_common.h"
 
 namespace tb {
@@ -52,8 +56,24 @@ struct lin_math<bf16_t> {
   }
 };
 
-constexpr int LIN_KB = 8;   // k-slices of 32 loaded per pass
 enum { LIN_ROUND = 0, LIN_PARTIAL = 1, LIN_SILU = 2 };
+constexpr int LIN_WAVES = 4;
+
+// A workgroup walks its K range in windows of up to SP = 28 k-slices (d_model
+// 896 in one window): every wave issues all of its W loads for the window,
+// then X of the window is staged (one chunk up to 32 rows: staging it in two
+// halves to fit more workgroups on a CU measured slower, the second round
+// trip costing more than the occupancy gained; 33..64 rows in chunks of 14).
+constexpr int LIN_SP = 28;
+template <int MT>
+struct lin_pass {
+  static constexpr int CH = MT <= 2 ? 28 : 14;
+  static __host__ __device__ constexpr int pitch(int slices) { return (4 * slices + 15) / 16 * 16 + 1; }
+  static constexpr int lds_bytes(int nt) {
+    const int staged = (16 * MT * pitch(CH) + 63) / 64 * 1024;
+    return staged > 4096 * MT * nt ? staged : 4096 * MT * nt;
+  }
+};
 
 struct lin_args {
   const char* x;
@@ -65,125 +85,156 @@ struct lin_args {
   int M, N, K;                // K range s of gridDim.y: k-slices [s*K/32/splits, (s+1)*K/32/splits)
 };
 
-template <typename Tag, int MT, int NT, int WAVES, int MODE>
-__global__ __launch_bounds__(64 * WAVES) void linear_kernel(lin_args a) {
+// Four waves split the K range; each wave computes all NT tiles of the
+// workgroup over its share, reading its X fragment from LDS once for them.
+template <typename Tag, int MT, int NT, int MODE>
+__global__ __launch_bounds__(64 * LIN_WAVES) void linear_kernel(lin_args a) {
   using L = lin_math<Tag>;
+  using PS = lin_pass<MT>;
   typedef typename L::scalar_t T;
-  __shared__ float red[WAVES][MT][NT][64][4];
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lc = lane & 15, lg = lane >> 4;
-  // silu: tiles j < NT/2 are gate columns, tile j + NT/2 the up columns d_ff later
+  constexpr int KB = (LIN_SP + LIN_WAVES - 1) / LIN_WAVES;   // k-slices per wave per window
   constexpr int OUT_TILES = MODE == LIN_SILU ? NT / 2 : NT;
+  constexpr int ROWS = 16 * MT;
   static_assert(MODE != LIN_SILU || NT % 2 == 0, "silu pairs gate and up tiles");
+  __shared__ __align__(16) char lds[PS::lds_bytes(NT)];
+  // wave-uniform in a scalar register: the K-share tests below become scalar branches
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, lc = lane & 15, lg = lane >> 4;
   int n0[NT];
 #pragma unroll
   for (int j = 0; j < NT; ++j)
-    n0[j] = (j / OUT_TILES) * (a.N >> 1) + (blockIdx.x * OUT_TILES + j % OUT_TILES) * 16;
+    n0[j] = (MODE == LIN_SILU ? (j / OUT_TILES) * (a.N >> 1) : 0) + (blockIdx.x * OUT_TILES + j % OUT_TILES) * 16;
   const int slices = a.K / 32;
   const int k_begin = (int)blockIdx.y * slices / (int)gridDim.y;
-  const int k_end = ((int)blockIdx.y + 1) * slices / (int)gridDim.y;
-  const int per_wave = (k_end - k_begin + WAVES - 1) / WAVES;
-  const int s_begin = k_begin + wave * per_wave;
-  const int s_end = min(k_end, s_begin + per_wave);
-
-  const char* wrow[NT];       // B operand: this lane's W row, 8 k per slice
+  const int range = ((int)blockIdx.y + 1) * slices / (int)gridDim.y - k_begin;
+  const char* wrow[NT];
 #pragma unroll
-  for (int j = 0; j < NT; ++j) wrow[j] = a.w + (int64_t)(n0[j] + lc) * a.K * 2 + 16 * lg;
-  const char* xrow[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) xrow[mt] = a.x + (int64_t)min(16 * mt + lc, a.M - 1) * a.x_row_bytes + 16 * lg;
+  for (int j = 0; j < NT; ++j) wrow[j] = a.w + (int64_t)(n0[j] + lc) * a.K * 2 + (int64_t)k_begin * 64 + 16 * lg;
+  const char* const xk = a.x + (int64_t)k_begin * 64;
 
   float4_t acc[MT][NT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int j = 0; j < NT; ++j) acc[mt][j] = float4_t{0.f, 0.f, 0.f, 0.f};
-  for (int s0 = s_begin; s0 < s_end; s0 += LIN_KB) {
-    vec16 wb[NT][LIN_KB], xb[MT][LIN_KB];
+  for (int w0 = 0; w0 < range; w0 += LIN_SP) {         // windows and chunks: the same in every wave
+    const int wn = min(LIN_SP, range - w0);
+    const int per = (wn + LIN_WAVES - 1) / LIN_WAVES;
+    const int sb = wave * per, se = min(wn, sb + per);  // this wave's slices of the window
+    vec16 wb[NT][KB];
 #pragma unroll
-    for (int i = 0; i < LIN_KB; ++i) {
-      const int s = min(s0 + i, s_end - 1);          // past the range: a repeat that is not used
+    for (int i = 0; i < KB; ++i)
+      if (sb + i < se) {
 #pragma unroll
-      for (int j = 0; j < NT; ++j) wb[j][i] = ld16(wrow[j] + (int64_t)s * 64);
+        for (int j = 0; j < NT; ++j) wb[j][i] = ld16(wrow[j] + (int64_t)(w0 + sb + i) * 64);
+      }
+    for (int x0 = 0; x0 < wn; x0 += PS::CH) {
+      const int xn = min(PS::CH, wn - x0);
+      const int P = PS::pitch(xn), units = ROWS * P, used = 4 * xn;
+      if (w0 + x0 > 0) __syncthreads();                 // the last chunk's X reads are done
+      // X rows [0, ROWS) x the chunk's slices -> LDS unit r * P + c (unit = 16 bytes);
+      // load q covers units 64 q .. 64 q + 63, lane order along the rows.
+      {
+        int p = wave * 64 + lane;
+        int r = p / P, c = p - r * P;
+        const int dr = 256 / P, dc = 256 - dr * P;
+        const char* const xc = xk + (int64_t)(w0 + x0) * 64;
+        for (int q = wave; q * 64 < units; q += LIN_WAVES) {
+          const bool real = r < ROWS && c < used;
+          const char* src = real ? xc + (int64_t)min(r, a.M - 1) * a.x_row_bytes + 16 * c : a.x;
+          __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)src,
+                                           (__attribute__((address_space(3))) void*)(lds + 1024 * q), 16, 0, 0);
+          c += dc;
+          r += dr;
+          if (c >= P) {
+            c -= P;
+            ++r;
+          }
+        }
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      // the wave's X fragments of this chunk first (all LDS reads in flight), then the MFMAs
+      vec16 xa[KB][MT];
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) xb[mt][i] = ld16(xrow[mt] + (int64_t)s * 64);
-    }
+      for (int i = 0; i < KB; ++i) {
+        const int sl = sb + i;
+        if (sl < se && sl >= x0 && sl < x0 + xn) {
 #pragma unroll
-    for (int i = 0; i < LIN_KB; ++i) {
-      if (s0 + i < s_end) {
+          for (int mt = 0; mt < MT; ++mt)
+            xa[i][mt] = *reinterpret_cast<const vec16*>(lds + 16 * ((16 * mt + lc) * P + 4 * (sl - x0) + lg));
+        }
+      }
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
+      for (int i = 0; i < KB; ++i) {
+        const int sl = sb + i;
+        if (sl < se && sl >= x0 && sl < x0 + xn) {
 #pragma unroll
-          for (int j = 0; j < NT; ++j) acc[mt][j] = L::mfma(xb[mt][i], wb[j][i], acc[mt][j]);
+          for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int j = 0; j < NT; ++j) acc[mt][j] = L::mfma(xa[i][mt], wb[j][i], acc[mt][j]);
+        }
       }
     }
   }
+  __syncthreads();                                      // X reads done: the area holds the sums now
+  float* red = reinterpret_cast<float*>(lds);           // [wave][mt][tile][lane][4]
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int j = 0; j < NT; ++j)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) red[wave][mt][j][lane][e] = acc[mt][j][e];
+      for (int e = 0; e < 4; ++e) red[(((wave * MT + mt) * NT + j) * 64 + lane) * 4 + e] = acc[mt][j][e];
   __syncthreads();
-  // thread t: output element (row m, tile j, column c)
-  for (int t = threadIdx.x; t < MT * 256 * OUT_TILES; t += 64 * WAVES) {
+  // thread t: output element (row m, tile j, column c); the waves' K shares added in order
+  for (int t = threadIdx.x; t < MT * 256 * OUT_TILES; t += 64 * LIN_WAVES) {
     const int c = t & 15, j = (t >> 4) % OUT_TILES, m = t / (16 * OUT_TILES);
     if (m >= a.M) continue;
     const int mt = m >> 4, r = m & 15;
     const int l = 16 * (r >> 2) + c, e = r & 3;          // the D lane and element holding (r, c)
-    float v0 = 0.f, v1 = 0.f;
+    auto tile_sum = [&](int tile) {
+      float v = 0.f;
 #pragma unroll
-    for (int wv = 0; wv < WAVES; ++wv) v0 += red[wv][mt][j][l][e];
+      for (int wv = 0; wv < LIN_WAVES; ++wv) v += red[(((wv * MT + mt) * NT + tile) * 64 + l) * 4 + e];
+      return v;
+    };
+    const float v0 = tile_sum(j);
     if constexpr (MODE == LIN_ROUND) {
-      if (a.bias) v0 += (float)reinterpret_cast<const T*>(a.bias)[n0[j] + c];
-      reinterpret_cast<T*>(a.y)[(int64_t)m * a.y_row_stride + n0[j] + c] = (T)v0;
+      const float b = a.bias ? (float)reinterpret_cast<const T*>(a.bias)[n0[j] + c] : 0.f;
+      reinterpret_cast<T*>(a.y)[(int64_t)m * a.y_row_stride + n0[j] + c] = (T)(v0 + b);
     } else if constexpr (MODE == LIN_PARTIAL) {
       reinterpret_cast<float*>(a.y)[((int64_t)blockIdx.y * a.M + m) * a.N + n0[j] + c] = v0;
     } else {
-#pragma unroll
-      for (int wv = 0; wv < WAVES; ++wv) v1 += red[wv][mt][j + OUT_TILES][l][e];
-      const float g = (float)(T)v0, u = (float)(T)v1;    // the gate/up GEMM's roundings
+      const float g = (float)(T)v0, u = (float)(T)tile_sum(j + OUT_TILES);   // the gate/up GEMM's roundings
       const T act = (T)(g / (1.f + expf(-g)));           // F.silu, rounded to the element type
       reinterpret_cast<T*>(a.y)[(int64_t)m * a.y_row_stride + n0[j] + c] = (T)((float)act * u);
     }
   }
 }
 
-// Launch shape: NT tiles per workgroup, WAVES waves splitting each K range,
-// `splits` K ranges (partial epilogue only).
+// Launch shape: NT tiles per workgroup, `splits` K ranges (partial epilogue only).
 struct lin_shape {
-  int nt, waves, splits;
+  int tw, splits;
 };
 
-template <typename Tag, int MODE, int MT, int NT>
-static int launch_waves(const lin_args& a, dim3 grid, int waves, hipStream_t stream) {
-  if (waves == 8) {
-    if constexpr (8 * MT * NT <= 64) {
-      hipLaunchKernelGGL((linear_kernel<Tag, MT, NT, 8, MODE>), grid, dim3(512), 0, stream, a);
-      return 0;
-    }
-    return -1;
-  }
-  hipLaunchKernelGGL((linear_kernel<Tag, MT, NT, 4, MODE>), grid, dim3(256), 0, stream, a);
-  return 0;
-}
-
 template <typename Tag, int MODE, int MT>
-static int launch_nt(const lin_args& a, dim3 grid, const lin_shape& s, hipStream_t stream) {
-  if (s.nt == 4) return launch_waves<Tag, MODE, MT, 4>(a, grid, s.waves, stream);
-  if (s.nt == 2) return launch_waves<Tag, MODE, MT, 2>(a, grid, s.waves, stream);
-  if constexpr (MODE != LIN_SILU) return launch_waves<Tag, MODE, MT, 1>(a, grid, s.waves, stream);
-  return -1;
+static int launch_tw(const lin_args& a, dim3 grid, int tw, hipStream_t stream) {
+  if (tw == 4) hipLaunchKernelGGL((linear_kernel<Tag, MT, 4, MODE>), grid, dim3(256), 0, stream, a);
+  else if (tw == 2) hipLaunchKernelGGL((linear_kernel<Tag, MT, 2, MODE>), grid, dim3(256), 0, stream, a);
+  else if constexpr (MODE != LIN_SILU) hipLaunchKernelGGL((linear_kernel<Tag, MT, 1, MODE>), grid, dim3(256), 0, stream, a);
+  else return -1;
+  return 0;
 }
 
 template <typename Tag, int MODE>
 static int launch_linear(const lin_args& a, const lin_shape& s, hipStream_t stream) {
-  const int tiles = a.N / 16 / s.nt;
-  const dim3 grid(tiles, s.splits);
+  if (s.tw != 1 && s.tw != 2 && s.tw != 4) return -1;
+  const dim3 grid(a.N / 16 / s.tw, s.splits);
   switch ((a.M + 15) / 16) {
-    case 1: return launch_nt<Tag, MODE, 1>(a, grid, s, stream);
-    case 2: return launch_nt<Tag, MODE, 2>(a, grid, s, stream);
-    case 3: return launch_nt<Tag, MODE, 3>(a, grid, s, stream);
-    default: return launch_nt<Tag, MODE, 4>(a, grid, s, stream);
+    case 1: return launch_tw<Tag, MODE, 1>(a, grid, s.tw, stream);
+    case 2: return launch_tw<Tag, MODE, 2>(a, grid, s.tw, stream);
+    case 3: return launch_tw<Tag, MODE, 3>(a, grid, s.tw, stream);
+    default: return launch_tw<Tag, MODE, 4>(a, grid, s.tw, stream);
   }
 }
 
@@ -193,17 +244,21 @@ static int launch_dtype(const lin_args& a, const lin_shape& s, int32_t dtype, hi
   return launch_linear<bf16_t, MODE>(a, s, stream);
 }
 
-// Launch shapes measured at the engine's decode shapes (0.5B dims, 1..32 rows,
-// 24 layers of weights rotating). Every workgroup reads all of X (M x K) from
-// L2 for its NT tiles, so the X reads per weight byte are M / (16 NT): more
-// tiles per workgroup pay off once rows grow (gate/up at 32 rows: 12.2 us
-// with one tile, 10.7 with four), fewer and larger workgroups cost where the
-// grid gets small (gate/up at 1 row: 6.7 vs 8.1 us).
-static lin_shape round_shape() { return lin_shape{1, 4, 1}; }
-static lin_shape partial_shape(int M, int N, int splits) {
-  return lin_shape{M > 8 && (N / 16) % 2 == 0 ? 2 : 1, 4, splits};
+// Launch shapes, measured at the engine's decode shapes (0.5B dims, 1..32 rows,
+// 24 layers of weights rotating). The weight stream is bound by how evenly
+// the 16-column tiles spread over the 256 CUs, so one tile per workgroup
+// (the most workgroups) wins for q/k/v and for the split-K pieces up to 16
+// rows; with more rows every workgroup's X staging weighs more and two or
+// four tiles per workgroup share it (gate/up at 32 rows: 10.1 us with one
+// tile pair, 9.8 with two pairs; down 5.6 -> 5.2 us with two tiles).
+static lin_shape round_shape() { return lin_shape{1, 1}; }
+static lin_shape partial_shape(int M, int N, int K, int splits) {
+  const int range = K / 32 / splits;
+  return lin_shape{M > 16 && range >= 16 && (N / 16) % 2 == 0 ? 2 : 1, splits};
 }
-static lin_shape silu_shape(int d_ff) { return lin_shape{(d_ff / 16) % 2 == 0 ? 4 : 2, 4, 1}; }
+static lin_shape silu_shape(int M, int d_ff) {
+  return lin_shape{M > 16 && (d_ff / 16) % 2 == 0 ? 4 : 2, 1};
+}
 
 static int32_t check_common(const void* x, int64_t x_row_stride, const void* w, int32_t rows, int32_t out_features,
                             int32_t in_features, int32_t dtype) {
@@ -242,7 +297,7 @@ extern "C" int32_t tb_linear_partials(const void* x, int64_t x_row_stride, const
   TB_CHECK_ARG(partials);
   const lin_args a{(const char*)x, x_row_stride * 2, (const char*)w, nullptr, partials, 0,
                    rows, out_features, in_features};
-  if (launch_dtype<LIN_PARTIAL>(a, partial_shape(rows, out_features, splits), dtype, stream))
+  if (launch_dtype<LIN_PARTIAL>(a, partial_shape(rows, out_features, in_features, splits), dtype, stream))
     return TB_ERR_UNSUPPORTED;
   TB_RETURN_LAUNCH_STATUS();
 }
@@ -259,6 +314,6 @@ extern "C" int32_t tb_linear_silu_mul(const void* x, int64_t x_row_stride, const
   TB_CHECK_ARG(y && y_row_stride >= d_ff);
   const lin_args a{(const char*)x, x_row_stride * 2, (const char*)w_gate_up, nullptr, y, y_row_stride,
                    rows, 2 * d_ff, in_features};
-  if (launch_dtype<LIN_SILU>(a, silu_shape(d_ff), dtype, stream)) return TB_ERR_UNSUPPORTED;
+  if (launch_dtype<LIN_SILU>(a, silu_shape(rows, d_ff), dtype, stream)) return TB_ERR_UNSUPPORTED;
   TB_RETURN_LAUNCH_STATUS();
 }
