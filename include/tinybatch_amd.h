@@ -264,6 +264,17 @@ int32_t tb_linear_silu_mul(const void* x, int64_t x_row_stride, const void* w_ga
                            int64_t y_row_stride, int32_t rows, int32_t d_ff, int32_t in_features,
                            int32_t dtype, hipStream_t stream);
 
+/* LM head followed by greedy sampling (model.py:157-158, engine.py:145-151):
+ *   ids[r] = argmax_n T(x[r] . w[n])  (the rounded logits, as torch.argmax over
+ * F.linear's output: NaN above every number, -0 equal to +0, the first index
+ * among equal values), without writing the logits. `workspace` holds one
+ * 8-byte candidate per (row, 16 columns): tb_linear_argmax_workspace_bytes;
+ * 8-byte aligned. ids is int64 [rows]. Limits as tb_linear. */
+size_t tb_linear_argmax_workspace_bytes(int32_t rows, int32_t out_features);
+int32_t tb_linear_argmax(const void* x, int64_t x_row_stride, const void* w, int32_t rows,
+                         int32_t out_features, int32_t in_features, void* workspace,
+                         size_t workspace_bytes, int64_t* ids, int32_t dtype, hipStream_t stream);
+
 /* tb_rms_norm whose input is the projection output held as split-K partials
  * (tb_linear_partials): x[r] = T(partials[0][r] + ... + partials[splits-1][r])
  * (fp32 adds in split order, one rounding), then the residual add and RMSNorm

@@ -133,3 +133,11 @@ def test_layer_ops_reject_bad_arguments_without_launching():
     assert rp(f, 4, f, 900, f, f, 896, 4, 896, 1e-6, bf16, None) == _lib.TB_ERR_INVALID_ARG       # residual stride
     assert rp(ctypes.c_void_p(4100), 4, None, 0, f, f, 896, 4, 896, 1e-6, bf16, None) == _lib.TB_ERR_INVALID_ARG
     assert rp(None, 4, None, 0, None, None, 896, 0, 896, 1e-6, bf16, None) == _lib.TB_OK
+    la = L.tb_linear_argmax
+    need = L.tb_linear_argmax_workspace_bytes(4, 151936)
+    assert need == 4 * 9496 * 8
+    assert la(f, 896, f, 4, 151936, 896, f, need - 8, f, bf16, None) == _lib.TB_ERR_INVALID_ARG   # short workspace
+    assert la(f, 896, f, 4, 151936, 896, ctypes.c_void_p(4100), need, f, bf16, None) == _lib.TB_ERR_INVALID_ARG
+    assert la(f, 896, f, 4, 151936, 896, f, need, None, bf16, None) == _lib.TB_ERR_INVALID_ARG    # no ids
+    assert la(f, 896, f, 4, 151930, 896, f, need, f, bf16, None) == _lib.TB_ERR_UNSUPPORTED      # N % 16
+    assert la(None, 896, None, 0, 151936, 896, None, 0, None, bf16, None) == _lib.TB_OK

@@ -150,3 +150,34 @@ def test_rms_norm_partials(dtype, dim, splits):
     torch.testing.assert_close(got.cpu().float(), mref.rms_norm(h, w, 1e-6).float(), **TOL[dtype])
     got = layer_ops.rms_norm_partials(parts.to(DEV), w.to(DEV), 1e-6)
     torch.testing.assert_close(got.cpu().float(), mref.rms_norm(x, w, 1e-6).float(), **TOL[dtype])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows", [1, 5, 16, 32])
+def test_linear_argmax_is_the_argmax_of_the_rounded_logits(dtype, rows):
+    """The LM head with greedy sampling fused: the index torch.argmax picks from
+    tb_linear's rounded logits (the same sums), on a 151936-wide head (two and
+    four tiles per workgroup), with ties (the first index wins), a NaN column
+    (NaN is the maximum, as in torch.argmax), an all-zero head (index 0)."""
+    g = torch.Generator(device=DEV).manual_seed(rows)
+    V, K = 151936, 896
+    w = (torch.randn(V, K, generator=g, device=DEV) * 0.05).to(dtype)
+    x = torch.randn(rows, K, generator=g, device=DEV).to(dtype)
+    want = layer_ops.linear(x, w).argmax(dim=-1)
+    got = layer_ops.linear_argmax(x, w)
+    assert torch.equal(got, want)
+    # the pick holds the largest fp32 logit up to the logits' rounding
+    ref = x.float() @ w.float().t()
+    assert float((ref.max(-1).values - ref.gather(1, got[:, None])[:, 0]).abs().max()) < 0.1
+    # ties: a copy of every row's winning column placed earlier wins
+    w2 = w.clone()
+    w2[3] = w[int(got[0])]
+    w2[int(got[0])] = w[int(got[0])]
+    got2 = layer_ops.linear_argmax(x[:1], w2)
+    assert int(got2[0]) == 3 == int(layer_ops.linear(x[:1], w2).argmax(-1)[0])
+    # a NaN column is the maximum of every row
+    w2[77777] = float("nan")
+    assert torch.equal(layer_ops.linear_argmax(x, w2), torch.full((rows,), 77777, device=DEV))
+    assert torch.equal(layer_ops.linear(x, w2).argmax(-1), torch.full((rows,), 77777, device=DEV))
+    # all logits zero: the first index
+    assert torch.equal(layer_ops.linear_argmax(x, torch.zeros_like(w)), torch.zeros(rows, dtype=torch.int64, device=DEV))

@@ -33,6 +33,8 @@ SIGNATURES = {
     "tb_linear": (c_i32, [c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_i32, c_i32, c_i32, c_i32, c_vp]),
     "tb_linear_partials": (c_i32, [c_vp, c_i64, c_vp, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp]),
     "tb_linear_silu_mul": (c_i32, [c_vp, c_i64, c_vp, c_vp, c_i64, c_i32, c_i32, c_i32, c_i32, c_vp]),
+    "tb_linear_argmax_workspace_bytes": (c_sz, [c_i32, c_i32]),
+    "tb_linear_argmax": (c_i32, [c_vp, c_i64, c_vp, c_i32, c_i32, c_i32, c_vp, c_sz, c_vp, c_i32, c_vp]),
     "tb_rms_norm_partials": (c_i32, [c_vp, c_i32, c_vp, c_i64, c_vp, c_vp, c_i64, c_i32, c_i32, c_f32, c_i32,
                                      c_vp]),
     "tb_kv_gather": (c_i32, [c_vp, c_i64, c_vp, c_i32, c_vp, c_vp, c_i32, c_i32, c_i32, c_i32, c_vp]),

@@ -75,14 +75,17 @@ __global__ __launch_bounds__(NORM_THREADS) void rms_norm_kernel(const T* x, int6
 // x = T(sum over s of partials[s][row]) is the projection output (the split-K
 // pieces of tb_linear_partials, added in split order and rounded once, like
 // F.linear's output); then the residual add and RMSNorm of rms_norm_kernel.
-// One wave per row, four rows per workgroup; lane owns the 8-element chunks
-// lane, lane + 64, ... (CH of them), every load issued before any use.
+// One wave (one workgroup) per row, so that the row's partials (S x dim x 4
+// bytes, 28 KB for 8 pieces of 896) stream through a CU of their own: four
+// rows per workgroup measured 3.7 us a launch for 8 pieces of 32 rows, one
+// row 3.0 us.
+// Lane owns the 8-element chunks lane, lane + 64, ... (CH of them), every
+// load issued before any use.
 template <typename T, int S, int CH>
-__global__ __launch_bounds__(256) void rms_norm_partials_kernel(const float* __restrict__ part, int rows, int dim,
+__global__ __launch_bounds__(64) void rms_norm_partials_kernel(const float* __restrict__ part, int rows, int dim,
                                                                 T* res, int64_t rs, const T* __restrict__ w,
                                                                 T* out, int64_t os, float eps) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-  if (row >= rows) return;
+  const int row = blockIdx.x, lane = threadIdx.x;
   struct x8 {
     T v[8];
   };
@@ -146,17 +149,17 @@ template <typename T, int S>
 static void launch_norm_partials_ch(int ch, dim3 grid, const float* part, int rows, int dim, T* res, int64_t rs,
                                     const T* w, T* out, int64_t os, float eps, hipStream_t stream) {
   switch (ch) {
-    case 1: hipLaunchKernelGGL((rms_norm_partials_kernel<T, S, 1>), grid, dim3(256), 0, stream, part, rows, dim, res, rs, w, out, os, eps); break;
-    case 2: hipLaunchKernelGGL((rms_norm_partials_kernel<T, S, 2>), grid, dim3(256), 0, stream, part, rows, dim, res, rs, w, out, os, eps); break;
-    case 4: hipLaunchKernelGGL((rms_norm_partials_kernel<T, S, 4>), grid, dim3(256), 0, stream, part, rows, dim, res, rs, w, out, os, eps); break;
-    default: hipLaunchKernelGGL((rms_norm_partials_kernel<T, S, 8>), grid, dim3(256), 0, stream, part, rows, dim, res, rs, w, out, os, eps); break;
+    case 1: hipLaunchKernelGGL((rms_norm_partials_kernel<T, S, 1>), grid, dim3(64), 0, stream, part, rows, dim, res, rs, w, out, os, eps); break;
+    case 2: hipLaunchKernelGGL((rms_norm_partials_kernel<T, S, 2>), grid, dim3(64), 0, stream, part, rows, dim, res, rs, w, out, os, eps); break;
+    case 4: hipLaunchKernelGGL((rms_norm_partials_kernel<T, S, 4>), grid, dim3(64), 0, stream, part, rows, dim, res, rs, w, out, os, eps); break;
+    default: hipLaunchKernelGGL((rms_norm_partials_kernel<T, S, 8>), grid, dim3(64), 0, stream, part, rows, dim, res, rs, w, out, os, eps); break;
   }
 }
 
 template <typename T>
 static void launch_norm_partials(int splits, int ch, const float* part, int rows, int dim, T* res, int64_t rs,
                                  const T* w, T* out, int64_t os, float eps, hipStream_t stream) {
-  const dim3 grid((rows + 3) / 4);
+  const dim3 grid(rows);
   switch (splits) {
     case 1: launch_norm_partials_ch<T, 1>(ch, grid, part, rows, dim, res, rs, w, out, os, eps, stream); break;
     case 2: launch_norm_partials_ch<T, 2>(ch, grid, part, rows, dim, res, rs, w, out, os, eps, stream); break;

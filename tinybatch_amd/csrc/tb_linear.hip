@@ -29,7 +29,13 @@
 //   silu    : tiles j < TW/2 are gate columns, tile j + TW/2 the up columns
 //             d_ff later (merged gate/up weight); Y = silu(T(gate)) * T(up)
 //             with the roundings of F.linear followed by tb_silu_mul
-//             (model.py:151-154).
+//             (model.py:151-154);
+//   argmax  : the LM head followed by greedy sampling (model.py:157-158,
+//             engine.py:145-151): per row, the largest T(sum) of the
+//             workgroup's columns and its index go to a workspace slot, and
+//             argmax_rows_kernel picks each row's winner over the slots.
+//             Order: NaN above everything, -0 equal to +0, the first index
+//             among equals (torch.argmax over the rounded logits).
 #include "tb_common.h"
 
 namespace tb {
@@ -56,7 +62,7 @@ struct lin_math<bf16_t> {
   }
 };
 
-enum { LIN_ROUND = 0, LIN_PARTIAL = 1, LIN_SILU = 2 };
+enum { LIN_ROUND = 0, LIN_PARTIAL = 1, LIN_SILU = 2, LIN_ARGMAX = 3 };
 constexpr int LIN_WAVES = 4;
 
 // A workgroup walks its K range in windows of up to SP = 28 k-slices (d_model
@@ -74,6 +80,26 @@ struct lin_pass {
     return staged > 4096 * MT * nt ? staged : 4096 * MT * nt;
   }
 };
+
+// Argmax candidates as one 64-bit key: the value's order in the high word (a
+// total order of floats with NaN on top and -0 = +0), the complement of the
+// column in the low word, so that the larger key is the larger value and,
+// among equals, the smaller column.
+__device__ __forceinline__ uint64_t argmax_key(float v, int col) {
+  uint32_t k;
+  if (v != v) {
+    k = 0xFFFFFFFFu;
+  } else {
+    const int b = __float_as_int(v == 0.f ? 0.f : v);
+    k = (uint32_t)(b >= 0 ? b : b ^ 0x7FFFFFFF) ^ 0x80000000u;
+  }
+  return ((uint64_t)k << 32) | (uint32_t)(0xFFFFFFFFu - (uint32_t)col);
+}
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
+  const uint32_t lo = __shfl_xor((uint32_t)v, m), hi = __shfl_xor((uint32_t)(v >> 32), m);
+  return ((uint64_t)hi << 32) | lo;
+}
 
 struct lin_args {
   const char* x;
@@ -204,11 +230,34 @@ __global__ __launch_bounds__(64 * LIN_WAVES) void linear_kernel(lin_args a) {
       reinterpret_cast<T*>(a.y)[(int64_t)m * a.y_row_stride + n0[j] + c] = (T)(v0 + b);
     } else if constexpr (MODE == LIN_PARTIAL) {
       reinterpret_cast<float*>(a.y)[((int64_t)blockIdx.y * a.M + m) * a.N + n0[j] + c] = v0;
+    } else if constexpr (MODE == LIN_ARGMAX) {
+      // the row's 16 NT columns sit in 16 NT consecutive lanes (16 NT divides 64)
+      uint64_t key = argmax_key((float)(T)v0, n0[j] + c);
+#pragma unroll
+      for (int sh = 1; sh < 16 * NT; sh <<= 1) key = max_u64(key, shfl_xor_u64(key, sh));
+      if ((t & (16 * NT - 1)) == 0) reinterpret_cast<uint64_t*>(a.y)[(int64_t)m * gridDim.x + blockIdx.x] = key;
     } else {
       const float g = (float)(T)v0, u = (float)(T)tile_sum(j + OUT_TILES);   // the gate/up GEMM's roundings
       const T act = (T)(g / (1.f + expf(-g)));           // F.silu, rounded to the element type
       reinterpret_cast<T*>(a.y)[(int64_t)m * a.y_row_stride + n0[j] + c] = (T)((float)act * u);
     }
+  }
+}
+
+// Row r's winner over its n candidate keys (one workgroup per row).
+__global__ __launch_bounds__(256) void argmax_rows_kernel(const uint64_t* __restrict__ keys, int n,
+                                                          int64_t* __restrict__ ids) {
+  __shared__ uint64_t part[4];
+  const uint64_t* row = keys + (int64_t)blockIdx.x * n;
+  uint64_t best = 0;
+  for (int i = threadIdx.x; i < n; i += 256) best = max_u64(best, row[i]);
+#pragma unroll
+  for (int sh = 1; sh < 64; sh <<= 1) best = max_u64(best, shfl_xor_u64(best, sh));
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    best = max_u64(max_u64(part[0], part[1]), max_u64(part[2], part[3]));
+    ids[blockIdx.x] = (int64_t)(0xFFFFFFFFu - (uint32_t)best);
   }
 }
 
@@ -258,6 +307,12 @@ static lin_shape partial_shape(int M, int N, int K, int splits) {
 }
 static lin_shape silu_shape(int M, int d_ff) {
   return lin_shape{M > 16 && (d_ff / 16) % 2 == 0 ? 4 : 2, 1};
+}
+// LM head (151936 x 896): two tiles per workgroup up to 16 rows, four above.
+static lin_shape argmax_shape(int M, int N) {
+  const int tiles = N / 16;
+  if (M > 16 && tiles % 4 == 0) return lin_shape{4, 1};
+  return lin_shape{tiles % 2 == 0 ? 2 : 1, 1};
 }
 
 static int32_t check_common(const void* x, int64_t x_row_stride, const void* w, int32_t rows, int32_t out_features,
@@ -315,5 +370,27 @@ extern "C" int32_t tb_linear_silu_mul(const void* x, int64_t x_row_stride, const
   const lin_args a{(const char*)x, x_row_stride * 2, (const char*)w_gate_up, nullptr, y, y_row_stride,
                    rows, 2 * d_ff, in_features};
   if (launch_dtype<LIN_SILU>(a, silu_shape(rows, d_ff), dtype, stream)) return TB_ERR_UNSUPPORTED;
+  TB_RETURN_LAUNCH_STATUS();
+}
+
+extern "C" size_t tb_linear_argmax_workspace_bytes(int32_t rows, int32_t out_features) {
+  if (rows <= 0 || out_features <= 0) return 0;
+  return (size_t)rows * (size_t)(out_features / 16) * sizeof(uint64_t);
+}
+
+extern "C" int32_t tb_linear_argmax(const void* x, int64_t x_row_stride, const void* w, int32_t rows,
+                                    int32_t out_features, int32_t in_features, void* workspace,
+                                    size_t workspace_bytes, int64_t* ids, int32_t dtype, hipStream_t stream) {
+  using namespace tb;
+  const int32_t st = check_common(x, x_row_stride, w, rows, out_features, in_features, dtype);
+  if (st != TB_OK || rows == 0) return st;
+  TB_CHECK_ARG(workspace && ids && ((uintptr_t)workspace & 7u) == 0);
+  TB_CHECK_ARG(workspace_bytes >= tb_linear_argmax_workspace_bytes(rows, out_features));
+  const lin_shape shape = argmax_shape(rows, out_features);
+  const lin_args a{(const char*)x, x_row_stride * 2, (const char*)w, nullptr, workspace, 0,
+                   rows, out_features, in_features};
+  if (launch_dtype<LIN_ARGMAX>(a, shape, dtype, stream)) return TB_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL(argmax_rows_kernel, dim3(rows), dim3(256), 0, stream, (const uint64_t*)workspace,
+                     out_features / 16 / shape.tw, ids);
   TB_RETURN_LAUNCH_STATUS();
 }

@@ -11,7 +11,9 @@ graph, captured once, whose launches read fixed device buffers:
   have, partition offsets, split rows — plus the device counts the attention
   kernels read at run time (tb_paged_attention's device_counts), so a launch
   sized for the capacities only runs this step's work items;
-* the output token ids (argmax inside the graph).
+* the output token ids (argmax inside the graph; for 16-bit batches of up
+  to 32 rows the LM head and the argmax are one fused kernel that never
+  writes the logits).
 
 Per step the host packs the metadata (the same builder as the eager path)
 into one pinned staging buffer, copies it with one host-to-device copy, and
@@ -24,7 +26,7 @@ import numpy as np
 import torch
 import torch.nn.functional as F
 
-from . import ops
+from . import layer_ops, ops
 from .kv_cache import PagedKVCache
 from .metadata import StepMetadata, pad4, build_step_metadata
 from .model import Qwen2Paged
@@ -59,6 +61,11 @@ class DecodeGraphs:
         self.ids = torch.zeros(B, dtype=torch.int64, device=self.dev)
         ws_bytes = ops._lib.lib().tb_paged_attention_workspace_bytes(self.wcap, c.n_heads, c.head_dim)
         self.ws = torch.empty(max(int(ws_bytes), 16), dtype=torch.uint8, device=self.dev)
+        # the LM head with greedy sampling fused (streamed batches): its candidate slots
+        self.head_fused = (model.fused_mlp and model._streamed(torch.empty(B, 0, dtype=model.dtype))
+                           and c.vocab_size % 16 == 0 and c.d_model % 32 == 0)
+        head_bytes = ops._lib.lib().tb_linear_argmax_workspace_bytes(B, c.vocab_size) if self.head_fused else 0
+        self.head_ws = torch.empty(max(int(head_bytes), 16), dtype=torch.uint8, device=self.dev)
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
         self.pool = None    # graph memory pool shared by the buckets
 
@@ -112,7 +119,10 @@ class DecodeGraphs:
                                        workspace=self.ws, rope=rope)
 
         x = m.run_layers(self.tok[:Bp], self.pos[:Bp], attention, fused_rope=m.fused_rope)
-        self.ids[:Bp].copy_(F.linear(x, m.lm_head).argmax(dim=-1))
+        if self.head_fused:
+            layer_ops.linear_argmax(x, m.lm_head, out=self.ids[:Bp], workspace=self.head_ws)
+        else:
+            self.ids[:Bp].copy_(F.linear(x, m.lm_head).argmax(dim=-1))
 
     def bucket(self, B: int) -> int | None:
         for b in self.buckets:

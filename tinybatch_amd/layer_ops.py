@@ -130,6 +130,29 @@ def linear_silu_mul(x: torch.Tensor, w_gate_up: torch.Tensor, out: torch.Tensor 
     return out
 
 
+def linear_argmax(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor | None = None,
+                  workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """F.linear(x, weight).argmax(-1) (int64 [rows]) without the logits: the LM
+    head with greedy sampling fused (tb_linear_argmax; model.py:157-158,
+    engine.py:145-151)."""
+    rows, n, xs = _linear_operands(x, weight)
+    L = _lib.lib()
+    need = L.tb_linear_argmax_workspace_bytes(rows, n)
+    if workspace is None:
+        workspace = torch.empty(max(need, 8), dtype=torch.uint8, device=x.device)
+    if workspace.numel() * workspace.element_size() < need or not workspace.is_contiguous():
+        raise ValueError(f"workspace must be a contiguous tensor of >= {need} bytes")
+    if out is None:
+        out = torch.empty(rows, dtype=torch.int64, device=x.device)
+    if out.dtype != torch.int64 or out.shape != (rows,) or not out.is_contiguous():
+        raise ValueError("out must be a contiguous int64 [rows] tensor")
+    st = L.tb_linear_argmax(x.data_ptr(), xs, weight.data_ptr(), rows, n, x.shape[1], workspace.data_ptr(),
+                            workspace.numel() * workspace.element_size(), out.data_ptr(),
+                            _lib.DTYPE_CODE[x.dtype], _lib.stream_handle(x.device))
+    _lib.check(st, "tb_linear_argmax")
+    return out
+
+
 def rms_norm_partials(partials: torch.Tensor, weight: torch.Tensor, eps: float, *,
                       residual: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
     """rms_norm() of x = partials.sum(0) rounded to weight's dtype (tb_rms_norm_partials):
