@@ -11,50 +11,78 @@
 
 namespace tb {
 
-// Grid: (pairs, layers, slices). Each workgroup copies a 1/slices share of one
-// block of one layer; 256 threads x 16 bytes per step.
+// The copy is viewed as one run of 16-byte vectors: vector v of the round is
+// vector v % V of pair v / V (V = vectors per block). A workgroup moves
+// 256 x CU consecutive vectors of one layer; every thread issues its CU loads
+// before its first store. The host guarantees that no dst block is a src block
+// (and that dst blocks are distinct), so the loads may run ahead of the stores.
+// Measured on 24 pools x 1024 pairs of 8 KiB blocks (403 MB moved): 83.8 us
+// with CU = 2 and non-temporal loads and stores (4.81 TB/s), 84-89 us for
+// CU = 2..8 either way, 102-106 us at CU = 16; a plain contiguous device copy
+// of the same bytes takes 80.2 us (5.02 TB/s), the practical ceiling of mixed
+// read/write traffic here.
+constexpr int COPY_CU = 2;
+
+template <int CU, bool NT>
 __global__ __launch_bounds__(256) void block_copy_kernel(const uint64_t* __restrict__ layer_pools,
                                                          const int32_t* __restrict__ src,
                                                          const int32_t* __restrict__ dst,
-                                                         int64_t num_blocks, int64_t block_vecs,
-                                                         int64_t slice_vecs) {
-  const int pair = blockIdx.x;
-  const int layer = blockIdx.y;
-  char* base = reinterpret_cast<char*>(layer_pools[layer]);
-  const int64_t s = src[pair], d = dst[pair];
-  if (s < 0 || s >= num_blocks || d < 0 || d >= num_blocks) return;  // host validates
-  const char* from = base + s * block_vecs * 16;
-  char* to = base + d * block_vecs * 16;
-  const int64_t begin = (int64_t)blockIdx.z * slice_vecs;
-  const int64_t end = min(begin + slice_vecs, block_vecs);
-  for (int64_t v = begin + threadIdx.x; v < end; v += blockDim.x) st16(to + v * 16, ld16(from + v * 16));
+                                                         int64_t num_blocks, uint32_t block_vecs,
+                                                         uint32_t total_vecs) {
+  char* base = reinterpret_cast<char*>(layer_pools[blockIdx.y]);
+  const uint32_t first = blockIdx.x * (256u * CU) + threadIdx.x;
+  vec16 r[CU];
+  char* to[CU];
+#pragma unroll
+  for (int u = 0; u < CU; ++u) {
+    const uint32_t v = first + 256u * u;
+    to[u] = nullptr;
+    if (v < total_vecs) {
+      const uint32_t pair = v / block_vecs, off = v - pair * block_vecs;
+      const int64_t s = src[pair], d = dst[pair];
+      if (s >= 0 && s < num_blocks && d >= 0 && d < num_blocks) {   // host validates
+        const char* from = base + (s * block_vecs + off) * 16;
+        to[u] = base + (d * block_vecs + off) * 16;
+        r[u] = NT ? ld16_stream(from) : ld16(from);
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < CU; ++u) {
+    if (to[u]) {
+      if (NT) __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, r[u]), reinterpret_cast<u32x4_t*>(to[u]));
+      else st16(to[u], r[u]);
+    }
+  }
 }
 
 // staging[i] <- pool[blocks[i]]  (to_staging = 1)   or   pool[blocks[i]] <- staging[i]  (0)
 __global__ __launch_bounds__(256) void block_stage_kernel(char* __restrict__ pool,
                                                           char* __restrict__ staging,
                                                           const int32_t* __restrict__ blocks,
-                                                          int64_t num_blocks, int64_t block_vecs,
-                                                          int64_t slice_vecs, int to_staging) {
-  const int i = blockIdx.x;
-  const int64_t b = blocks[i];
-  if (b < 0 || b >= num_blocks) return;  // host validates
-  char* p = pool + b * block_vecs * 16;
-  char* s = staging + (int64_t)i * block_vecs * 16;
-  const int64_t begin = (int64_t)blockIdx.y * slice_vecs;
-  const int64_t end = min(begin + slice_vecs, block_vecs);
-  for (int64_t v = begin + threadIdx.x; v < end; v += blockDim.x) {
-    if (to_staging) st16(s + v * 16, ld16(p + v * 16));
-    else st16(p + v * 16, ld16(s + v * 16));
+                                                          int64_t num_blocks, uint32_t block_vecs,
+                                                          uint32_t total_vecs, int to_staging) {
+  const uint32_t first = blockIdx.x * (256u * COPY_CU) + threadIdx.x;
+  vec16 r[COPY_CU];
+  char* to[COPY_CU];
+#pragma unroll
+  for (int u = 0; u < COPY_CU; ++u) {
+    const uint32_t v = first + 256u * u;
+    to[u] = nullptr;
+    if (v < total_vecs) {
+      const uint32_t i = v / block_vecs, off = v - i * block_vecs;
+      const int64_t b = blocks[i];
+      if (b >= 0 && b < num_blocks) {   // host validates
+        char* p = pool + (b * block_vecs + off) * 16;
+        char* st = staging + ((int64_t)i * block_vecs + off) * 16;
+        r[u] = ld16(to_staging ? p : st);
+        to[u] = to_staging ? st : p;
+      }
+    }
   }
-}
-
-// 4096 16-byte vectors (64 KiB) per workgroup at most.
-static int64_t slices_for(int64_t block_vecs, int64_t* slice_vecs) {
-  const int64_t per = 4096;
-  const int64_t n = (block_vecs + per - 1) / per;
-  *slice_vecs = (block_vecs + n - 1) / n;
-  return n;
+#pragma unroll
+  for (int u = 0; u < COPY_CU; ++u)
+    if (to[u]) st16(to[u], r[u]);
 }
 
 }  // namespace tb
@@ -67,11 +95,11 @@ extern "C" int32_t tb_block_copy(const uint64_t* layer_pools, int32_t num_layers
   if (num_layers == 0 || num_pairs == 0) return TB_OK;
   TB_CHECK_ARG(layer_pools && src_blocks && dst_blocks);
   TB_CHECK_ARG(num_layers <= 65535);
-  int64_t slice_vecs = 0;
-  const int64_t slices = slices_for(block_bytes / 16, &slice_vecs);
-  TB_CHECK_ARG(slices <= 65535);
-  hipLaunchKernelGGL(block_copy_kernel, dim3(num_pairs, num_layers, (unsigned)slices), dim3(256), 0, stream,
-                     layer_pools, src_blocks, dst_blocks, num_blocks, block_bytes / 16, slice_vecs);
+  const int64_t total = (int64_t)num_pairs * (block_bytes / 16);
+  TB_CHECK_ARG(total < (int64_t)1 << 31);
+  const unsigned wgs = (unsigned)((total + 256 * COPY_CU - 1) / (256 * COPY_CU));
+  hipLaunchKernelGGL((block_copy_kernel<COPY_CU, true>), dim3(wgs, num_layers), dim3(256), 0, stream, layer_pools,
+                     src_blocks, dst_blocks, num_blocks, (uint32_t)(block_bytes / 16), (uint32_t)total);
   TB_RETURN_LAUNCH_STATUS();
 }
 
@@ -83,11 +111,11 @@ extern "C" int32_t tb_block_gather(const void* pool, int64_t num_blocks, const i
   if (num_blocks_to_move == 0) return TB_OK;
   TB_CHECK_ARG(pool && blocks && staging);
   TB_CHECK_ARG((((uintptr_t)pool | (uintptr_t)staging) & 15u) == 0);
-  int64_t slice_vecs = 0;
-  const int64_t slices = slices_for(block_bytes / 16, &slice_vecs);
-  TB_CHECK_ARG(slices <= 65535);
-  hipLaunchKernelGGL(block_stage_kernel, dim3(num_blocks_to_move, (unsigned)slices), dim3(256), 0, stream,
-                     (char*)pool, (char*)staging, blocks, num_blocks, block_bytes / 16, slice_vecs, 1);
+  const int64_t total = (int64_t)num_blocks_to_move * (block_bytes / 16);
+  TB_CHECK_ARG(total < (int64_t)1 << 31);
+  const unsigned wgs = (unsigned)((total + 256 * COPY_CU - 1) / (256 * COPY_CU));
+  hipLaunchKernelGGL(block_stage_kernel, dim3(wgs), dim3(256), 0, stream, (char*)pool, (char*)staging, blocks,
+                     num_blocks, (uint32_t)(block_bytes / 16), (uint32_t)total, 1);
   TB_RETURN_LAUNCH_STATUS();
 }
 
@@ -99,10 +127,10 @@ extern "C" int32_t tb_block_scatter(const void* staging, void* pool, int64_t num
   if (num_blocks_to_move == 0) return TB_OK;
   TB_CHECK_ARG(pool && blocks && staging);
   TB_CHECK_ARG((((uintptr_t)pool | (uintptr_t)staging) & 15u) == 0);
-  int64_t slice_vecs = 0;
-  const int64_t slices = slices_for(block_bytes / 16, &slice_vecs);
-  TB_CHECK_ARG(slices <= 65535);
-  hipLaunchKernelGGL(block_stage_kernel, dim3(num_blocks_to_move, (unsigned)slices), dim3(256), 0, stream,
-                     (char*)pool, (char*)staging, blocks, num_blocks, block_bytes / 16, slice_vecs, 0);
+  const int64_t total = (int64_t)num_blocks_to_move * (block_bytes / 16);
+  TB_CHECK_ARG(total < (int64_t)1 << 31);
+  const unsigned wgs = (unsigned)((total + 256 * COPY_CU - 1) / (256 * COPY_CU));
+  hipLaunchKernelGGL(block_stage_kernel, dim3(wgs), dim3(256), 0, stream, (char*)pool, (char*)staging, blocks,
+                     num_blocks, (uint32_t)(block_bytes / 16), (uint32_t)total, 0);
   TB_RETURN_LAUNCH_STATUS();
 }
