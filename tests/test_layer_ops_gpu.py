@@ -181,3 +181,23 @@ def test_linear_argmax_is_the_argmax_of_the_rounded_logits(dtype, rows):
     assert torch.equal(layer_ops.linear(x, w2).argmax(-1), torch.full((rows,), 77777, device=DEV))
     # all logits zero: the first index
     assert torch.equal(layer_ops.linear_argmax(x, torch.zeros_like(w)), torch.zeros(rows, dtype=torch.int64, device=DEV))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_norm_kernels_agree_bit_for_bit(dtype):
+    """tb_rms_norm and tb_rms_norm_partials (one piece holding x) on integer-valued
+    rows, whose sums of squares are exact in any order: the same bits, i.e. the
+    same mean rounding and the same two single-rounded products per element
+    (a contraction of the last product with the rounding to fp16 had made
+    rare elements differ by one ulp between the kernels)."""
+    g = torch.Generator().manual_seed(11)
+    k = 896
+    w = (1 + 0.1 * torch.randn(k, generator=g)).to(dtype).to(DEV)
+    for rows in (1, 16, 17, 37):
+        x = torch.randint(-3, 4, (rows, k), generator=g).to(dtype).to(DEV)
+        r = torch.randint(-3, 4, (rows, k), generator=g).to(dtype).to(DEV)
+        ra, rb = r.clone(), r.clone()
+        a = layer_ops.rms_norm(x, w, 1e-6, residual=ra)
+        b = layer_ops.rms_norm_partials(x.float()[None].contiguous(), w, 1e-6, residual=rb)
+        assert torch.equal(ra, rb)
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16)), rows

@@ -10,7 +10,11 @@
 //   tb_rms_norm_partials : tb_rms_norm whose x is the sum of split-K partials of
 //                  the projection before it (o_proj, down_proj: model.py:149,154)
 // Rounding follows the PyTorch ops they replace: the residual sum and silu(g)
-// are rounded to the element type before their next use.
+// are rounded to the element type before their next use. The norm's two
+// products are single v_mul_f32s (mul_rn): left to the compiler, the second
+// one and the rounding to fp16 fused into one mixed-precision FMA in some of
+// the norm kernels and not in others (one rounding instead of two, a 1-ulp
+// difference in rare elements).
 #include "tb_common.h"
 
 namespace tb {
@@ -62,12 +66,12 @@ __global__ __launch_bounds__(NORM_THREADS) void rms_norm_kernel(const T* x, int6
   float tot = 0.f;
 #pragma unroll
   for (int k = 0; k < NORM_THREADS / 64; ++k) tot += part[k];
-  const float inv = rsqrtf(tot / (float)dim + eps);
+  const float inv = rsqrtf(__fdiv_rn(tot, (float)dim) + eps);   // the mean correctly rounded (every norm kernel alike)
   T* orow = out + row * os;
 #pragma unroll
   for (int k = 0; k < NORM_MAX_PER_THREAD; ++k) {
     const int i = threadIdx.x + k * NORM_THREADS;
-    if (i < dim) orow[i] = from_f<T>((h[k] * inv) * to_f(w[i]));
+    if (i < dim) orow[i] = from_f<T>(mul_rn(mul_rn(h[k], inv), to_f(w[i])));
   }
 }
 
@@ -133,14 +137,14 @@ __global__ __launch_bounds__(64) void rms_norm_partials_kernel(const float* __re
   ss += __shfl_xor(ss, 8);
   ss += __shfl_xor(ss, 16);
   ss += __shfl_xor(ss, 32);
-  const float inv = rsqrtf(ss / (float)dim + eps);
+  const float inv = rsqrtf(__fdiv_rn(ss, (float)dim) + eps);    // the mean correctly rounded (every norm kernel alike)
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
     if (lane + 64 * i >= chunks) continue;
     const x8 wt = __builtin_bit_cast(x8, wv[i]);
     x8 o;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o.v[e] = from_f<T>((h[i][e] * inv) * to_f(wt.v[e]));
+    for (int e = 0; e < 8; ++e) o.v[e] = from_f<T>(mul_rn(mul_rn(h[i][e], inv), to_f(wt.v[e])));
     st16(out + row * os + 8 * (lane + 64 * i), __builtin_bit_cast(vec16, o));
   }
 }
