@@ -35,7 +35,12 @@ def test_work_items_cover_every_row_and_partition():
             row_ctx = c - n + i + 1
             for p in range((row_ctx + 3) // 4):
                 items.append((s + i, sl.index((s, e)), p, row_ctx))
-    assert [tuple(x) for x in m.work_np.tolist()] == items
+    got = [tuple(x) for x in m.work_np.tolist()]
+    assert sorted(got) == sorted(items)
+    # issued shortest partition first, row order among equals
+    lengths = [min(4, rc - 4 * p) for _, _, p, rc in got]
+    assert lengths == sorted(lengths)
+    assert got == sorted(items, key=lambda it: min(4, it[3] - 4 * it[2]))
     counts = np.diff(m.row_part_off_np)
     for r in range(len(pos)):
         assert counts[r] == sum(1 for it in items if it[0] == r)
