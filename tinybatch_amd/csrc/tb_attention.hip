@@ -342,8 +342,7 @@ struct mfma_shape {
 // read and scalar address arithmetic per tile); otherwise each lane looks its
 // block up in a per-lane copy of the partition's table entries.
 template <typename Tag, int D, bool UT>
-__global__ __launch_bounds__(64 * mfma_shape<D>::NW) __attribute__((amdgpu_waves_per_eu(5)))
-void paged_attn_mfma_kernel(const attn_args a) {
+__device__ __forceinline__ void decode_items_body(const attn_args& a, char* const lds, const int bx, const int bz) {
   using S = mfma_shape<D>;
   using M = math<Tag>;
   typedef typename M::vec8_t vec8_t;
@@ -351,7 +350,6 @@ void paged_attn_mfma_kernel(const attn_args a) {
   constexpr int RB = S::RB, KS = S::KS, NSL = S::NSL, P = S::P, CT = S::CT, NW = S::NW;
   constexpr int TILES = S::TILES, VCOLS = S::VCOLS, VT = S::VT, VLD = S::VLD;
 
-  __shared__ __align__(16) char lds[S::LDS];
   float2 (*const ml_lds)[16] = reinterpret_cast<float2 (*)[16]>(lds + NW * S::MERGE);
 
   const int wave = threadIdx.x >> 6;
@@ -363,13 +361,13 @@ void paged_attn_mfma_kernel(const attn_args a) {
   // The kv head varies fastest across the grid: the workgroups reading the K
   // and V tiles of the same blocks for the two (or more) kv heads run side by
   // side, so each block's bytes are fetched close together in time.
-  const int item = blockIdx.x / a.num_kv_heads;
-  const int kvh = blockIdx.x - item * a.num_kv_heads;
+  const int item = bx / a.num_kv_heads;
+  const int kvh = bx - item * a.num_kv_heads;
   const int4 wi = a.work[item];                  // the array holds the grid's capacity
   if (a.counts && item >= a.counts[0]) return;   // whole workgroup: beyond this step's items
   const int row0 = wi.x, seq = wi.y, part = wi.z & 0xFFFFFF, nrows = (wi.z >> 24) + 1, ctx0 = wi.w;
   const int R = a.group;                    // heads of this workgroup; nrows * R <= 16
-  const int head0 = kvh * a.rep + blockIdx.z * R;
+  const int head0 = kvh * a.rep + bz * R;
   const int p0 = part * P;
   const int n = min(P, ctx0 + nrows - 1 - p0);   // positions visible to the last row (>= 1)
   const int ctx = ctx0;                     // the single decode row's context (fused append)
@@ -479,7 +477,7 @@ void paged_attn_mfma_kernel(const attn_args a) {
   // block id.
   const int pbeg0 = a.row_part_off[row0];
   const int nparts = a.row_part_off[row0 + 1] - pbeg0;
-  const bool stores_new = fused && blockIdx.z == 0 && new_tau >= wb && new_tau < wb + CT;   // wave-uniform
+  const bool stores_new = fused && bz == 0 && new_tau >= wb && new_tau < wb + CT;   // wave-uniform
   int new_blk = 0;
   if (stores_new) {
     new_blk = a.block_tables[(int64_t)seq * a.max_nb + ((ctx - 1) >> a.log2_bs)];
@@ -645,6 +643,13 @@ void paged_attn_mfma_kernel(const attn_args a) {
   }
 }
 
+template <typename Tag, int D, bool UT>
+__global__ __launch_bounds__(64 * mfma_shape<D>::NW) __attribute__((amdgpu_waves_per_eu(5)))
+void paged_attn_mfma_kernel(const attn_args a) {
+  __shared__ __align__(16) char lds[mfma_shape<D>::LDS];
+  decode_items_body<Tag, D, UT>(a, lds, blockIdx.x, blockIdx.z);
+}
+
 // ---------------------------------------------------------------------------
 // Prefill tiles (16-bit). A workgroup of 4 waves owns up to 64 consecutive
 // query rows of one sequence (wave w: rows 16w .. 16w+15; lane column lc is
@@ -688,21 +693,19 @@ struct prefill_shape {
 };
 
 template <typename Tag, int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
-void paged_prefill_mfma_kernel(const attn_args a) {
+__device__ __forceinline__ void prefill_tiles_body(const attn_args& a, char* const lds, const int bx) {
   using S = prefill_shape<D>;
   using M = math<Tag>;
   typedef typename M::vec8_t vec8_t;
   typedef typename M::scalar_t scalar_t;
   constexpr int RB = S::RB, KS = S::KS, NSL = S::NSL, RS = S::RS, CK = S::CK, NCH = S::NCH;
   constexpr int VCOLS = S::VCOLS, LPT = S::LPT, RSV = S::RSV, EB = 2;
-  __shared__ __align__(16) char lds[S::LDS];
   char* const k_lds = lds;
   char* const v_lds = lds + CK * RS;
 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lc = lane & 15, lg = lane >> 4;
-  const int item = blockIdx.x / a.num_heads;
-  const int head = blockIdx.x - item * a.num_heads;
+  const int item = bx / a.num_heads;
+  const int head = bx - item * a.num_heads;
   const int4 ti = a.tiles[item];                 // the array holds the grid's capacity
   if (a.counts && item >= a.counts[2]) return;   // whole workgroup: beyond this step's tiles
   const int row0 = ti.x, seq = ti.y, nrows = ti.z & 0xFF, part = ti.z >> 8, pos0 = ti.w;
@@ -912,6 +915,29 @@ void paged_prefill_mfma_kernel(const attn_args a) {
   }
 }
 
+template <typename Tag, int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
+void paged_prefill_mfma_kernel(const attn_args a) {
+  __shared__ __align__(16) char lds[prefill_shape<D>::LDS];
+  prefill_tiles_body<Tag, D>(a, lds, blockIdx.x);
+}
+
+// One launch for a step that has both prefill tiles and decode work items
+// (head dim 64: both are workgroups of four waves): workgroups below
+// tile_wgs are prefill tiles (issued first, the longest work), the rest are
+// the decode items. The decode items are latency-bound and the tiles
+// VALU/latency-bound, so sharing the machine lets one hide the other instead
+// of running back to back.
+template <typename Tag, int D, bool UT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
+void paged_step_mfma_kernel(const attn_args a, const int tile_wgs) {
+  constexpr int L1 = mfma_shape<D>::LDS, L2 = prefill_shape<D>::LDS;
+  static_assert(mfma_shape<D>::NW == 4, "one workgroup shape for both");
+  __shared__ __align__(16) char lds[L1 > L2 ? L1 : L2];
+  if ((int)blockIdx.x < tile_wgs) prefill_tiles_body<Tag, D>(a, lds, blockIdx.x);
+  else decode_items_body<Tag, D, UT>(a, lds, blockIdx.x - tile_wgs, 0);
+}
+
 // ---------------------------------------------------------------------------
 // Log-sum-exp merge of the partials of one split row: workgroup (r, c) owns
 // 256 float4 columns (4 consecutive output dims each, head = column / (D/4))
@@ -1019,12 +1045,26 @@ static void launch_prefill(const attn_args& a, int num_tiles, hipStream_t stream
     hipLaunchKernelGGL((paged_prefill_mfma_kernel<Tag, D>), dim3(num_tiles * a.num_heads), dim3(256), 0, stream, a);
 }
 
+template <typename Tag, int D>
+static void launch_step(const attn_args& a, int num_work, int num_tiles, hipStream_t stream) {
+  const int tile_wgs = num_tiles * a.num_heads;
+  const dim3 grid(tile_wgs + num_work * a.num_kv_heads);
+  if (a.log2_bs >= 4)
+    hipLaunchKernelGGL((paged_step_mfma_kernel<Tag, D, true>), grid, dim3(256), 0, stream, a, tile_wgs);
+  else
+    hipLaunchKernelGGL((paged_step_mfma_kernel<Tag, D, false>), grid, dim3(256), 0, stream, a, tile_wgs);
+}
+
 template <typename Tag>
 static void launch_16bit(const attn_args& a, bool d64, int num_work, int num_tiles, int num_split_rows,
                          hipStream_t stream) {
   if (d64) {
-    if (num_work > 0) launch_mfma<Tag, 64>(a, num_work, stream);
-    launch_prefill<Tag, 64>(a, num_tiles, stream);
+    if (num_work > 0 && num_tiles > 0 && a.rep == a.group) {
+      launch_step<Tag, 64>(a, num_work, num_tiles, stream);
+    } else {
+      if (num_work > 0) launch_mfma<Tag, 64>(a, num_work, stream);
+      launch_prefill<Tag, 64>(a, num_tiles, stream);
+    }
     launch_combine<Tag, 64>(a, num_split_rows, stream);
   } else {
     if (num_work > 0) launch_mfma<Tag, 128>(a, num_work, stream);
