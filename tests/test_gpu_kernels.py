@@ -406,3 +406,14 @@ def test_prefill_tiles_split_over_tile_partitions_bf16():
     assert counts[1500] == 12                       # the decode row: 256-position partitions
     assert counts[1501:].max() == 3 and counts[:1500].max() == 2   # tile rows: 1024-position ones
     _attention_vs_oracle(c, 14, 2, torch.bfloat16)
+
+
+@pytest.mark.parametrize("BS", [8, 16])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_mixed_step_one_launch_tiles_and_decode_items(BS, dtype):
+    """A step with prefill tiles (rows of the 40- and 100-token sequences) and
+    decode items (single rows, a 33-row tail) runs as one launch of the
+    combined kernel; both block-id paths (block size 8: per-lane lookups; 16:
+    wave-uniform tiles); tolerance 2e-2 against the oracle."""
+    c = _mixed_case(41 + BS, 14, 2, 64, BS, dtype, qlens=[40, 1, 1, 100, 33, 1], cached=[0, 300, 2000, 200, 700, 17])
+    _attention_vs_oracle(c, 14, 2, dtype)
