@@ -3,7 +3,8 @@ import numpy as np
 import pytest
 import torch
 
-from tinybatch_amd.metadata import TILE_PARTITION, TILE_ROWS, build_step_metadata
+from tinybatch_amd.metadata import (TILE_PARTITION, TILE_ROWS, build_step_metadata, decode_staging_offsets,
+                                    pack_decode_step, pack_step)
 
 
 def _mixed():
@@ -169,3 +170,60 @@ def test_long_prefill_tiles_span_tile_partitions():
     assert len(items) == want
     assert m.max_parts_per_row == 3
     assert m.split_rows_np[:, 0].tolist() == [r for r in range(n) if r + 1 > TILE_PARTITION]
+
+
+def _decode_case(rng, B, BS, NB, extra_blocks=0):
+    ctx = [int(c) for c in rng.integers(1, 3000, B)]
+    ctx[:4] = [1, BS, BS + 1, 256][:B]
+    perm = rng.permutation(NB).tolist()
+    tables, at = [], 0
+    for c in ctx:
+        nb = (c + BS - 1) // BS + int(rng.integers(0, extra_blocks + 1))   # reserved blocks past the context
+        tables.append(perm[at:at + nb]); at += nb
+    return ctx, tables
+
+
+def _read_parts(h, o, Bp, max_nb, ctx, BS):
+    """What the kernels read of a packed decode step: every slot, the table entries
+    inside each context, the work items, offsets, split rows and counts."""
+    W, S = int(h[o[5]]), int(h[o[5] + 1])
+    tab = h[o[1]:o[1] + Bp * max_nb].reshape(Bp, max_nb)
+    used = [tab[b, :(c + BS - 1) // BS].tolist() for b, c in enumerate(ctx)]
+    return (h[o[0]:o[0] + Bp].tolist(), used, h[o[2]:o[2] + 4 * W].tolist(), h[o[3]:o[3] + Bp + 1].tolist(),
+            h[o[4]:o[4] + 4 * S].tolist(), h[o[5]:o[5] + 4].tolist())
+
+
+@pytest.mark.parametrize("BS,B,Bp", [(16, 32, 32), (16, 5, 8), (4, 9, 16), (32, 1, 1), (8, 64, 96)])
+def test_pack_decode_step_matches_the_general_builder(BS, B, Bp):
+    """The decode fast path writes what build_step_metadata + pack_step write
+    (stale staging contents beneath), work items in the same order."""
+    rng = np.random.default_rng(BS * 1000 + B)
+    NB, P, max_len = 16384, 256, 4096
+    max_nb, max_parts = max_len // BS, max_len // P
+    ctx, tables = _decode_case(rng, B, BS, NB, extra_blocks=2)
+    o = decode_staging_offsets(Bp, max_nb, max_parts)
+    fast = rng.integers(-5, 10**6, int(o[-1])).astype(np.int32)       # stale contents
+    ref = fast.copy()
+    assert pack_decode_step(fast, o, Bp, max_nb, ctx, tables, block_size=BS, num_blocks=NB, partition_tokens=P)
+    meta = build_step_metadata([c - 1 for c in ctx], [(i, i + 1) for i in range(B)], tables, ctx,
+                               block_size=BS, num_blocks=NB, partition_tokens=P)
+    pack_step(ref, o, Bp, max_nb, meta)
+    assert _read_parts(fast, o, Bp, max_nb, ctx, BS) == _read_parts(ref, o, Bp, max_nb, ctx, BS)
+
+
+def test_pack_decode_step_rejects_what_the_builder_rejects():
+    o = decode_staging_offsets(4, 8, 2)
+    h = np.zeros(int(o[-1]), np.int32)
+    kw = dict(block_size=16, num_blocks=10, partition_tokens=256)
+    with pytest.raises(IndexError):                      # table shorter than the context
+        pack_decode_step(h, o, 4, 8, [17], [[3]], **kw)
+    with pytest.raises(IndexError):                      # block outside the pool
+        pack_decode_step(h, o, 4, 8, [5], [[10]], **kw)
+    with pytest.raises(IndexError):
+        pack_decode_step(h, o, 4, 8, [5], [[-1]], **kw)
+    with pytest.raises(ValueError):                      # no position to attend to
+        pack_decode_step(h, o, 4, 8, [0], [[1]], **kw)
+    with pytest.raises(ValueError):                      # longer than the staging tables
+        pack_decode_step(h, o, 4, 8, [129], [list(range(9))], **dict(kw, num_blocks=20))
+    # two rows writing one slot: left to the general builder's last-writer rule
+    assert not pack_decode_step(h, o, 4, 8, [5, 5], [[2], [2]], **kw)

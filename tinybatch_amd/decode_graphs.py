@@ -15,8 +15,9 @@ graph, captured once, whose launches read fixed device buffers:
   to 32 rows the LM head and the argmax are one fused kernel that never
   writes the logits).
 
-Per step the host packs the metadata (the same builder as the eager path)
-into one pinned staging buffer, copies it with one host-to-device copy, and
+Per step the host packs the tokens, positions and metadata straight into one
+pinned staging buffer (pack_decode_step: the arrays build_step_metadata would
+give, built for decode rows only), copies it with one host-to-device copy, and
 replays. Padded rows get no work items and slot -1: they read nothing and
 write nothing, and their outputs are ignored.
 """
@@ -28,7 +29,8 @@ import torch.nn.functional as F
 
 from . import layer_ops, ops
 from .kv_cache import PagedKVCache
-from .metadata import StepMetadata, pad4, build_step_metadata
+from .metadata import (StepMetadata, build_step_metadata, decode_staging_offsets, pack_decode_step,
+                       pack_step)
 from .model import Qwen2Paged
 
 DEFAULT_BUCKETS = (1, 2, 4, 8, 16, 24, 32, 48, 64, 96, 128, 192, 256)
@@ -47,17 +49,18 @@ class DecodeGraphs:
         self.buckets = sorted({b for b in buckets if b < max_batch} | {max_batch})
         B = self.buckets[-1]
         self.wcap = B * self.max_parts
-        # int32 layout (each part 16-byte aligned): slot [B] | tables [B*max_nb] | work [wcap*4] |
-        # row_part_off [B+1] | split-row records [B*4] | counts [4]
-        sizes = [pad4(n) for n in (B, B * self.max_nb, self.wcap * 4, B + 1, B * 4, 4)]
-        self.offs = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
+        # one staging buffer, one copy per step: the int32 metadata (decode_staging_offsets)
+        # followed by the int64 tokens [B] and positions [B]
+        self.offs = decode_staging_offsets(B, self.max_nb, self.max_parts)
         n = int(self.offs[-1])
-        self.dev_i32 = torch.zeros(n, dtype=torch.int32, device=self.dev)
-        self.host_i32 = torch.zeros(n, dtype=torch.int32).pin_memory()
-        self.host_np = self.host_i32.numpy()
-        self.tok = torch.zeros(B, dtype=torch.int64, device=self.dev)
-        self.pos = torch.zeros(B, dtype=torch.int64, device=self.dev)
-        self.host_tp = torch.zeros(2, B, dtype=torch.int64).pin_memory()
+        nbytes = 4 * n + 16 * B
+        self.dev_buf = torch.zeros(nbytes, dtype=torch.uint8, device=self.dev)
+        self.host_buf = torch.zeros(nbytes, dtype=torch.uint8).pin_memory()
+        self.dev_i32 = self.dev_buf[:4 * n].view(torch.int32)
+        self.host_np = self.host_buf[:4 * n].view(torch.int32).numpy()
+        self.tok = self.dev_buf[4 * n:4 * n + 8 * B].view(torch.int64)
+        self.pos = self.dev_buf[4 * n + 8 * B:].view(torch.int64)
+        self.host_tp = self.host_buf[4 * n:].view(torch.int64).view(2, B).numpy()
         self.ids = torch.zeros(B, dtype=torch.int64, device=self.dev)
         ws_bytes = ops._lib.lib().tb_paged_attention_workspace_bytes(self.wcap, c.n_heads, c.head_dim)
         self.ws = torch.empty(max(int(ws_bytes), 16), dtype=torch.uint8, device=self.dev)
@@ -90,23 +93,6 @@ class DecodeGraphs:
         m.device_counts = self._view(5, 4)
         return m
 
-    def _pack(self, Bp: int, meta: StepMetadata) -> None:
-        """The step's metadata into the staging buffer, padded to bucket Bp."""
-        h, o = self.host_np, self.offs
-        B = meta.num_tokens
-        h[o[0]:o[0] + Bp] = -1
-        h[o[0]:o[0] + B] = meta.slot_mapping_np
-        tab = h[o[1]:o[1] + Bp * self.max_nb].reshape(Bp, self.max_nb)
-        nb = min(meta.block_tables_np.shape[1], self.max_nb)   # entries past the context are never read
-        tab[:B, :nb] = meta.block_tables_np[:B, :nb]
-        W = meta.num_work_items
-        h[o[2]:o[2] + W * 4] = meta.work_np.reshape(-1)
-        h[o[3]:o[3] + B + 1] = meta.row_part_off_np
-        h[o[3] + B + 1:o[3] + Bp + 1] = meta.row_part_off_np[-1]
-        S = meta.num_split_rows
-        h[o[4]:o[4] + 4 * S] = meta.split_rows_np.reshape(-1)
-        h[o[5]:o[5] + 4] = (W, S, 0, 0)
-
     # ---- the captured step -------------------------------------------------------
     @torch.inference_mode()
     def _forward(self, Bp: int, meta: StepMetadata) -> None:
@@ -133,7 +119,7 @@ class DecodeGraphs:
     def _capture(self, Bp: int) -> torch.cuda.CUDAGraph:
         meta = self._meta(Bp)
         self.host_np[self.offs[5]:self.offs[5] + 4] = 0            # no work: warm-up launches exit at once
-        self.dev_i32.copy_(self.host_i32)
+        self.dev_buf.copy_(self.host_buf)
         stream = torch.cuda.Stream(device=self.dev)
         stream.wait_stream(torch.cuda.current_stream(self.dev))
         with torch.cuda.stream(stream):
@@ -162,17 +148,17 @@ class DecodeGraphs:
             raise ValueError(f"batch {B} exceeds the largest bucket {self.buckets[-1]}")
         if max(context_lens) > self.max_nb * self.BS:
             raise ValueError("context longer than max_model_len")
-        meta = build_step_metadata(positions, [(i, i + 1) for i in range(B)], block_tables, context_lens,
-                                   block_size=self.BS, num_blocks=self.cache.num_blocks, partition_tokens=self.P)
         g = self.graphs.get(Bp)
         if g is None:
             g = self.graphs[Bp] = self._capture(Bp)
-        self._pack(Bp, meta)
-        self.host_tp[0, :B] = torch.tensor(tokens)
-        self.host_tp[1, :B] = torch.tensor(positions)
+        if not pack_decode_step(self.host_np, self.offs, Bp, self.max_nb, context_lens, block_tables,
+                                block_size=self.BS, num_blocks=self.cache.num_blocks, partition_tokens=self.P):
+            meta = build_step_metadata(positions, [(i, i + 1) for i in range(B)], block_tables, context_lens,
+                                       block_size=self.BS, num_blocks=self.cache.num_blocks, partition_tokens=self.P)
+            pack_step(self.host_np, self.offs, Bp, self.max_nb, meta)
+        self.host_tp[0, :B] = tokens
+        self.host_tp[1, :B] = positions
         self.host_tp[:, B:Bp] = 0
-        self.dev_i32.copy_(self.host_i32, non_blocking=True)
-        self.tok[:Bp].copy_(self.host_tp[0, :Bp], non_blocking=True)
-        self.pos[:Bp].copy_(self.host_tp[1, :Bp], non_blocking=True)
+        self.dev_buf.copy_(self.host_buf, non_blocking=True)
         g.replay()
         return self.ids[:B].cpu().tolist()

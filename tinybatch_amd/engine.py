@@ -98,7 +98,7 @@ class LLMEngine:
             context_lens.append(len(req.prompt_token_ids))
         for req in decode:
             start = len(token_ids)
-            token_ids.append(req.all_token_ids()[-1])
+            token_ids.append(req.last_token_id())
             positions.append(req.context_len() - 1)
             seq_slices.append((start, len(token_ids)))
             block_tables.append(req.block_table)

@@ -37,6 +37,7 @@ IndexError (kv_cache.py:35), a block id outside the pool raises IndexError
 """
 from __future__ import annotations
 
+import itertools
 from dataclasses import dataclass
 
 import numpy as np
@@ -291,3 +292,100 @@ def build_step_metadata(positions, seq_slices, block_tables, context_lens, *, bl
         prefill_tiles_np=tiles_np.astype(np.int32),
         split_rows_np=split_rows.astype(np.int32),
     )
+
+
+# ---- decode-only steps, packed for a captured graph ----------------------------
+# Staging layout of a decode graph (int32, each part 16-byte aligned): slot [B] |
+# block tables [B, max_nb] | work items [B * max_parts, 4] | row_part_off [B + 1] |
+# split-row records [B, 4] | counts (work items, split rows, tiles, 0).
+def decode_staging_offsets(max_batch: int, max_nb: int, max_parts: int) -> np.ndarray:
+    sizes = [pad4(n) for n in (max_batch, max_batch * max_nb, max_batch * max_parts * 4, max_batch + 1,
+                               max_batch * 4, 4)]
+    return np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
+
+
+def pack_step(h: np.ndarray, offs: np.ndarray, Bp: int, max_nb: int, meta: StepMetadata) -> None:
+    """A decode step's metadata (from build_step_metadata) into staging buffer h,
+    padded to Bp rows: padded rows get slot -1 and no work."""
+    o = offs
+    B = meta.num_tokens
+    h[o[0]:o[0] + Bp] = -1
+    h[o[0]:o[0] + B] = meta.slot_mapping_np
+    tab = h[o[1]:o[1] + Bp * max_nb].reshape(Bp, max_nb)
+    nb = min(meta.block_tables_np.shape[1], max_nb)   # entries past the context are never read
+    tab[:B, :nb] = meta.block_tables_np[:B, :nb]
+    W = meta.num_work_items
+    h[o[2]:o[2] + W * 4] = meta.work_np.reshape(-1)
+    h[o[3]:o[3] + B + 1] = meta.row_part_off_np
+    h[o[3] + B + 1:o[3] + Bp + 1] = meta.row_part_off_np[-1]
+    S = meta.num_split_rows
+    h[o[4]:o[4] + 4 * S] = meta.split_rows_np.reshape(-1)
+    h[o[5]:o[5] + 4] = (W, S, 0, 0)
+
+
+def pack_decode_step(h: np.ndarray, offs: np.ndarray, Bp: int, max_nb: int, context_lens, block_tables, *,
+                     block_size: int, num_blocks: int, partition_tokens: int) -> bool:
+    """Pack a decode-only step (row b = sequence b, one new token at position
+    context_lens[b] - 1) straight into staging buffer h: the arrays that
+    build_step_metadata + pack_step write, for a fraction of the host time (the
+    engine's per-step cost). Returns False, writing nothing that matters, when
+    two rows map to one slot (then the general builder's last-writer rule
+    applies); raises as the general builder does on block ids outside the pool
+    or tables shorter than their contexts."""
+    B = len(context_lens)
+    BS, P, o = int(block_size), int(partition_tokens), offs
+    ctx = np.fromiter(context_lens, np.int64, B)
+    lens = np.fromiter(map(len, block_tables), np.int64, B)
+    if B == 0 or ctx.min() < 1:
+        raise ValueError("a decode row needs a context of at least one position")
+    need = (ctx + BS - 1) // BS
+    short = need > lens
+    if short.any():
+        b = int(short.argmax())
+        raise IndexError(f"context_len {int(ctx[b])} of sequence {b} needs {int(need[b])} blocks "
+                         f"but its table has {int(lens[b])}")
+    if int(need.max()) > max_nb:
+        raise ValueError("context longer than the staging tables")
+    flat = np.fromiter(itertools.chain.from_iterable(block_tables), np.int64, int(lens.sum()))
+    if flat.min() < 0 or flat.max() >= num_blocks:
+        i = int(((flat < 0) | (flat >= num_blocks)).argmax())
+        b = int(np.searchsorted(np.cumsum(lens), i, side="right"))
+        raise IndexError(f"block id {int(flat[i])} of sequence {b} is outside the pool of {num_blocks} blocks")
+    # table entries the kernels read: the first need[b] of each row
+    first = np.cumsum(lens) - lens
+    tot = int(need.sum())
+    row = np.repeat(np.arange(B, dtype=np.int64), need)
+    col = np.arange(tot, dtype=np.int64) - np.repeat(np.cumsum(need) - need, need)
+    tab = h[o[1]:o[1] + Bp * max_nb].reshape(Bp, max_nb)
+    tab[row, col] = flat[np.repeat(first, need) + col]
+    last = ctx - 1
+    slots = flat[first + last // BS] * BS + last % BS
+    if len(set(slots.tolist())) != B:
+        return False
+    h[o[0]:o[0] + Bp] = -1
+    h[o[0]:o[0] + B] = slots
+    # work items, shortest partition first (stable), as build_step_metadata orders them
+    nparts = (ctx + P - 1) // P
+    W = int(nparts.sum())
+    wrow = np.repeat(np.arange(B, dtype=np.int64), nparts)
+    part = np.arange(W, dtype=np.int64) - np.repeat(np.cumsum(nparts) - nparts, nparts)
+    wctx = ctx[wrow]
+    order = np.argsort(np.minimum(P, wctx - P * part), kind="stable")
+    work = h[o[2]:o[2] + W * 4].reshape(W, 4)
+    work[:, 0] = wrow[order]
+    work[:, 1] = wrow[order]
+    work[:, 2] = part[order]
+    work[:, 3] = wctx[order]
+    rpo = h[o[3]:o[3] + Bp + 1]
+    rpo[0] = 0
+    np.cumsum(nparts, out=rpo[1:B + 1])
+    rpo[B + 1:] = W
+    split = np.nonzero(nparts > 1)[0]
+    S = int(split.size)
+    rec = h[o[4]:o[4] + 4 * S].reshape(S, 4)
+    rec[:, 0] = split
+    rec[:, 1] = rpo[split]
+    rec[:, 2] = nparts[split]
+    rec[:, 3] = 0
+    h[o[5]:o[5] + 4] = (W, S, 0, 0)
+    return True

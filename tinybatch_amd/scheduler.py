@@ -65,6 +65,9 @@ class Request:
     def context_len(self) -> int:
         return len(self.prompt_token_ids) + len(self.output_token_ids)
 
+    def last_token_id(self) -> int:
+        return self.output_token_ids[-1] if self.output_token_ids else self.prompt_token_ids[-1]
+
 
 @dataclass
 class ScheduledBatch:
