@@ -253,7 +253,7 @@ def bench_e2e(args, dev) -> int:
         for r in reqs:
             r.arrival_time = start
         dec_time = dec_tokens = 0.0
-        while eng.scheduler.has_work():
+        while eng.has_work():
             ts = time.perf_counter()
             outs_ = eng.step()
             dt = time.perf_counter() - ts

@@ -124,7 +124,7 @@ def test_engine_generation_matches_oracle_token_for_token_fp32(graphs):
     max_new = [12, 7, 20, 15, 30, 9]
     eng = LLMEngine(ecfg, model=model)
     reqs = [eng.add_request(p, max_new_tokens=m) for p, m in zip(prompts, max_new)]
-    while eng.scheduler.has_work():
+    while eng.has_work():
         eng.step()
     want, hit_rate = oracle_generate(model, ecfg, prompts, max_new)
     assert [r.output_token_ids for r in reqs] == want
@@ -212,7 +212,7 @@ def test_swap_preemption_gives_the_tokens_of_an_unpressured_run(graphs):
                             max_running=5, decode_graphs=graphs, preemption=preemption)
         eng = LLMEngine(ecfg, model=model)
         reqs = [eng.add_request(p, max_new_tokens=m) for p, m in zip(prompts, max_new)]
-        while eng.scheduler.has_work():
+        while eng.has_work():
             eng.step()
         return [r.output_token_ids for r in reqs], eng, reqs
 
@@ -224,3 +224,46 @@ def test_swap_preemption_gives_the_tokens_of_an_unpressured_run(graphs):
     assert sum(r.preemptions for r in reqs) == eng.swap_outs
     got_rc, eng_rc, reqs_rc = run(16, "recompute")
     assert got_rc == want and sum(r.preemptions for r in reqs_rc) > 0
+
+
+@pytest.mark.parametrize("dtype", ["float32", "bfloat16"])
+def test_pipelined_decode_streams_match_synchronous_steps(dtype):
+    """Decode steps queued ahead of their tokens (pipeline_decode) give every
+    request the same token stream, finished flags included, as synchronous
+    steps: with budget ends, a request arriving mid-run (the pipeline drains
+    for its prefill) and a stop token that ends requests while a later step
+    is already queued for them."""
+    mc = small_cfg(layers=2, heads=4, kv_heads=2)
+    model = Qwen2Paged(mc, DEV, getattr(torch, dtype), seed=21)
+    g = torch.Generator().manual_seed(22)
+    prompts = [torch.randint(0, mc.vocab_size, (n,), generator=g).tolist() for n in (30, 17, 45, 8)]
+    late = torch.randint(0, mc.vocab_size, (25,), generator=g).tolist()
+    max_new = [40, 12, 33, 25]
+
+    def run(pipeline, stop=()):
+        ecfg = EngineConfig(dtype=dtype, num_blocks=128, block_size=16, max_batch_tokens=256, max_running=8,
+                            pipeline_decode=pipeline, stop_token_ids=tuple(stop))
+        eng = LLMEngine(ecfg, model=model)
+        reqs = [eng.add_request(p, max_new_tokens=m) for p, m in zip(prompts, max_new)]
+        streams, calls = {}, 0
+        while eng.has_work():
+            for o in eng.step():
+                streams.setdefault(o.req_id, []).append((o.token_id, o.finished))
+            calls += 1
+            if calls == 6:
+                reqs.append(eng.add_request(late, max_new_tokens=20))
+        assert eng._inflight is None and not any(-1 in r.output_token_ids for r in reqs)
+        return [r.output_token_ids for r in reqs], [streams[r.req_id] for r in reqs], eng
+
+    want, want_streams, e0 = run(False)
+    got, got_streams, e1 = run(True)
+    assert e0.pipelined_steps == 0 and e1.pipelined_steps > 20
+    assert got == want and got_streams == want_streams
+    assert [len(t) for t in want] == max_new + [20]
+    assert all(s[-1][1] and not any(f for _, f in s[:-1]) for s in want_streams)
+    # a stop token taken from the middle of one request's output
+    stop = want[2][len(want[2]) // 2]
+    want_s, want_streams_s, _ = run(False, (stop,))
+    got_s, got_streams_s, e2 = run(True, (stop,))
+    assert got_s == want_s and got_streams_s == want_streams_s and e2.pipelined_steps > 0
+    assert any(t[-1] == stop and len(t) < m for t, m in zip(want_s, max_new + [20]))

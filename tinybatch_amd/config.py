@@ -32,6 +32,9 @@ class EngineConfig:
     stop_token_ids: tuple = field(default_factory=tuple)
     # decode-only steps replay a captured HIP graph per batch-size bucket
     decode_graphs: bool = True
+    # steady greedy decode queues step N+1 before step N's tokens reach the host
+    # (the host's scheduling and packing then overlap the GPU's step)
+    pipeline_decode: bool = True
     # random-init weights
     seed: int = 0
 

@@ -18,7 +18,12 @@ graph, captured once, whose launches read fixed device buffers:
 Per step the host packs the tokens, positions and metadata straight into one
 pinned staging buffer (pack_decode_step: the arrays build_step_metadata would
 give, built for decode rows only), copies it with one host-to-device copy, and
-replays. Padded rows get no work items and slot -1: they read nothing and
+replays. ``launch`` returns without waiting: the step's token ids come back
+through a pinned buffer and an event (``collect``), and a row may take its
+input token from the previous step's ids still on the device (its source row),
+so the host can queue step N+1 while step N runs. Two staging and two id
+buffers alternate; a step's buffers are reused two launches later, after its
+ids were collected. Padded rows get no work items and slot -1: they read nothing and
 write nothing, and their outputs are ignored.
 """
 from __future__ import annotations
@@ -50,18 +55,22 @@ class DecodeGraphs:
         B = self.buckets[-1]
         self.wcap = B * self.max_parts
         # one staging buffer, one copy per step: the int32 metadata (decode_staging_offsets)
-        # followed by the int64 tokens [B] and positions [B]
+        # followed by int64 tokens [B], positions [B] and source rows [B] (-1: the token
+        # comes from the host; r >= 0: row r of the previous step's ids)
         self.offs = decode_staging_offsets(B, self.max_nb, self.max_parts)
         n = int(self.offs[-1])
-        nbytes = 4 * n + 16 * B
+        nbytes = 4 * n + 24 * B
         self.dev_buf = torch.zeros(nbytes, dtype=torch.uint8, device=self.dev)
-        self.host_buf = torch.zeros(nbytes, dtype=torch.uint8).pin_memory()
+        self.host_bufs = [torch.zeros(nbytes, dtype=torch.uint8).pin_memory() for _ in range(2)]
         self.dev_i32 = self.dev_buf[:4 * n].view(torch.int32)
-        self.host_np = self.host_buf[:4 * n].view(torch.int32).numpy()
-        self.tok = self.dev_buf[4 * n:4 * n + 8 * B].view(torch.int64)
-        self.pos = self.dev_buf[4 * n + 8 * B:].view(torch.int64)
-        self.host_tp = self.host_buf[4 * n:].view(torch.int64).view(2, B).numpy()
+        self.host_nps = [h[:4 * n].view(torch.int32).numpy() for h in self.host_bufs]
+        self.host_tps = [h[4 * n:].view(torch.int64).view(3, B).numpy() for h in self.host_bufs]
+        tail = self.dev_buf[4 * n:].view(torch.int64).view(3, B)
+        self.tok, self.pos, self.src = tail[0], tail[1], tail[2]
         self.ids = torch.zeros(B, dtype=torch.int64, device=self.dev)
+        self.host_ids = [torch.zeros(B, dtype=torch.int64).pin_memory() for _ in range(2)]
+        self.turn = 0       # which staging / id buffer the next launch uses
+        self.last_use = [None, None]   # the event of the launch that last used each buffer
         ws_bytes = ops._lib.lib().tb_paged_attention_workspace_bytes(self.wcap, c.n_heads, c.head_dim)
         self.ws = torch.empty(max(int(ws_bytes), 16), dtype=torch.uint8, device=self.dev)
         # the LM head with greedy sampling fused (streamed batches): its candidate slots
@@ -104,7 +113,9 @@ class DecodeGraphs:
             return ops.paged_attention(q, self.cache.pools[i], meta, num_heads=c.n_heads, k_new=k, v_new=v,
                                        workspace=self.ws, rope=rope)
 
-        x = m.run_layers(self.tok[:Bp], self.pos[:Bp], attention, fused_rope=m.fused_rope)
+        src = self.src[:Bp]
+        tok = torch.where(src >= 0, self.ids.index_select(0, src.clamp(min=0)), self.tok[:Bp])
+        x = m.run_layers(tok, self.pos[:Bp], attention, fused_rope=m.fused_rope)
         if self.head_fused:
             layer_ops.linear_argmax(x, m.lm_head, out=self.ids[:Bp], workspace=self.head_ws)
         else:
@@ -118,8 +129,10 @@ class DecodeGraphs:
 
     def _capture(self, Bp: int) -> torch.cuda.CUDAGraph:
         meta = self._meta(Bp)
-        self.host_np[self.offs[5]:self.offs[5] + 4] = 0            # no work: warm-up launches exit at once
-        self.dev_buf.copy_(self.host_buf)
+        torch.cuda.synchronize(self.dev)                            # no step in flight reads the buffers
+        self.dev_i32[int(self.offs[5]):int(self.offs[5]) + 4].zero_()   # no work: warm-up launches exit at once
+        self.src.zero_()                                            # in-range source rows for the warm-up
+        ids = self.ids.clone()          # the last step's tokens, which the next launch may read
         stream = torch.cuda.Stream(device=self.dev)
         stream.wait_stream(torch.cuda.current_stream(self.dev))
         with torch.cuda.stream(stream):
@@ -128,6 +141,7 @@ class DecodeGraphs:
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=stream, pool=self.pool):
             self._forward(Bp, meta)
+        self.ids.copy_(ids)             # the warm-up overwrote them
         torch.cuda.synchronize(self.dev)
         if self.pool is None:
             self.pool = g.pool()
@@ -139,9 +153,11 @@ class DecodeGraphs:
             if b not in self.graphs:
                 self.graphs[b] = self._capture(b)
 
-    def run(self, tokens: list[int], positions: list[int], block_tables: list[list[int]],
-            context_lens: list[int]) -> list[int]:
-        """Greedy next token of each decode row (one row per sequence)."""
+    def launch(self, tokens: list[int], positions: list[int], block_tables: list[list[int]],
+               context_lens: list[int], src_rows: list[int] | None = None):
+        """Queue one decode step (one row per sequence) without waiting for it. Row i's
+        input token is tokens[i], or, where src_rows[i] >= 0, the id the previous launch
+        produced for its row src_rows[i]. Returns the handle ``collect`` takes."""
         B = len(tokens)
         Bp = self.bucket(B)
         if Bp is None:
@@ -151,14 +167,36 @@ class DecodeGraphs:
         g = self.graphs.get(Bp)
         if g is None:
             g = self.graphs[Bp] = self._capture(Bp)
-        if not pack_decode_step(self.host_np, self.offs, Bp, self.max_nb, context_lens, block_tables,
+        k = self.turn
+        self.turn ^= 1
+        if self.last_use[k] is not None:
+            self.last_use[k].synchronize()   # its copies are done before the buffers are rewritten
+        h, tp = self.host_nps[k], self.host_tps[k]
+        if not pack_decode_step(h, self.offs, Bp, self.max_nb, context_lens, block_tables,
                                 block_size=self.BS, num_blocks=self.cache.num_blocks, partition_tokens=self.P):
             meta = build_step_metadata(positions, [(i, i + 1) for i in range(B)], block_tables, context_lens,
                                        block_size=self.BS, num_blocks=self.cache.num_blocks, partition_tokens=self.P)
-            pack_step(self.host_np, self.offs, Bp, self.max_nb, meta)
-        self.host_tp[0, :B] = tokens
-        self.host_tp[1, :B] = positions
-        self.host_tp[:, B:Bp] = 0
-        self.dev_buf.copy_(self.host_buf, non_blocking=True)
+            pack_step(h, self.offs, Bp, self.max_nb, meta)
+        tp[0, :B] = tokens
+        tp[1, :B] = positions
+        tp[2, :B] = -1 if src_rows is None else src_rows
+        tp[0:2, B:Bp] = 0
+        tp[2, B:Bp] = -1
+        self.dev_buf.copy_(self.host_bufs[k], non_blocking=True)
         g.replay()
-        return self.ids[:B].cpu().tolist()
+        self.host_ids[k][:Bp].copy_(self.ids[:Bp], non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        self.last_use[k] = ev
+        return (B, k, ev)
+
+    def collect(self, handle) -> list[int]:
+        """The token ids of a launched step (waits for that step only)."""
+        B, k, ev = handle
+        ev.synchronize()
+        return self.host_ids[k][:B].tolist()
+
+    def run(self, tokens: list[int], positions: list[int], block_tables: list[list[int]],
+            context_lens: list[int]) -> list[int]:
+        """Greedy next token of each decode row (one row per sequence)."""
+        return self.collect(self.launch(tokens, positions, block_tables, context_lens))

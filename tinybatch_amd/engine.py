@@ -14,6 +14,20 @@ are sampled by one batched argmax and one device-to-host copy instead of one
 ``int()`` synchronisation per sequence; greedy decode-only steps replay a
 captured HIP graph of the whole forward (DecodeGraphs) instead of issuing
 its launches one by one.
+
+Pipelined decode (EngineConfig.pipeline_decode): while the batch is steady -
+nothing waiting or swapped, every running request greedy, a free block for
+each - a graph step is queued before the previous one's tokens are on the
+host. Its rows read their input tokens from the previous step's ids on the
+device; on the host each request gets a placeholder token (PENDING) that the
+previous step's ids replace once collected, one step later, so the scheduler
+sees the right context lengths throughout. A request that reaches its token
+budget finishes at launch (its last token is on the way; blocks freed now are
+only reused by later steps, which the stream orders behind this one). A stop
+token seen at collection ends its request there and drops the placeholder of
+the step already queued for it (that step computed one row more than a
+synchronous run would have; rows do not interact). Anything else drains the
+pipeline first and runs the synchronous step.
 """
 from __future__ import annotations
 
@@ -27,7 +41,9 @@ from .config import EngineConfig
 from .decode_graphs import DecodeGraphs
 from .kv_cache import PagedKVCache
 from .model import ModelConfig, Qwen2Paged
-from .scheduler import Request, Scheduler
+from .scheduler import Request, Scheduler, Status
+
+PENDING = -1    # placeholder of a token still on the device
 
 
 @dataclass
@@ -55,11 +71,13 @@ class LLMEngine:
         self.steps = 0
         self.last_step_prefills = 0
         self.graph_steps = 0
+        self.pipelined_steps = 0
         self.graphs = (DecodeGraphs(self.model, self.kv_cache, self.cfg.max_running, self.cfg.max_model_len)
                        if self.cfg.decode_graphs else None)
         self.swap_outs = 0
         self.swap_ins = 0
         self._swap_reads: list[torch.Tensor] = []   # host copies read by the last step's swap-ins
+        self._inflight: dict | None = None           # the queued graph step whose tokens are not collected
 
     # ---- API -----------------------------------------------------------------
     def add_request(self, prompt_token_ids: list[int], *, max_new_tokens: int | None = None,
@@ -76,7 +94,7 @@ class LLMEngine:
 
     def generate(self, prompts: list[list[int]], **kw) -> list[list[int]]:
         reqs = [self.add_request(p, **kw) for p in prompts]
-        while self.scheduler.has_work():
+        while self.has_work():
             self.step()
         return [r.output_token_ids for r in reqs]
 
@@ -123,7 +141,74 @@ class LLMEngine:
             req.swap_staging = None
             self.swap_ins += 1
 
+    def has_work(self) -> bool:
+        return self.scheduler.has_work() or self._inflight is not None
+
     def step(self) -> list[StepOutput]:
+        """One iteration. Pipelined decode steps return the outputs of the step
+        queued before them (tokens arrive one call late); other steps first
+        collect a queued step and return its outputs ahead of their own."""
+        if self._can_pipeline():
+            return self._step_pipelined()
+        outs = self._collect(self._inflight) if self._inflight is not None else []
+        return outs + self._step_sync()
+
+    def _can_pipeline(self) -> bool:
+        sch = self.scheduler
+        return (self.cfg.pipeline_decode and self.graphs is not None and not sch.waiting and not sch.swapped
+                and bool(sch.running) and self.graphs.bucket(len(sch.running)) is not None
+                and self.block_manager.num_free() >= len(sch.running)      # no preemption this step
+                and all(r.temperature <= 0.0 for r in sch.running))
+
+    def _step_pipelined(self) -> list[StepOutput]:
+        batch = self.scheduler.schedule()
+        if batch.prefill or batch.swap_out or batch.swap_in or len(batch.decode) != len(self.scheduler.running):
+            raise RuntimeError("a steady decode batch was expected")
+        ordered = batch.decode
+        prev = self._inflight
+        row_of = prev["row_of"] if prev is not None else {}
+        src = [row_of.get(r.req_id, -1) for r in ordered]
+        tokens = [0 if s >= 0 else r.last_token_id() for r, s in zip(ordered, src)]
+        ctx = [r.context_len() for r in ordered]
+        handle = self.graphs.launch(tokens, [c - 1 for c in ctx], [r.block_table for r in ordered], ctx,
+                                    src_rows=src)
+        self.graph_steps += 1
+        self.pipelined_steps += 1
+        self.last_step_prefills = 0
+        idx = []
+        for r in ordered:
+            r.output_token_ids.append(PENDING)
+            idx.append(len(r.output_token_ids) - 1)
+            if len(r.output_token_ids) >= r.max_new_tokens or r.context_len() >= self.cfg.max_model_len:
+                self.scheduler.finish(r)
+        self._inflight = {"reqs": ordered, "handle": handle, "idx": idx,
+                          "row_of": {r.req_id: i for i, r in enumerate(ordered)}}
+        return self._collect(prev) if prev is not None else []
+
+    def _collect(self, rec: dict) -> list[StepOutput]:
+        """A queued step's tokens into its requests' placeholders."""
+        ids = self.graphs.collect(rec["handle"])
+        if self._inflight is rec:
+            self._inflight = None
+        now = time.perf_counter()
+        outputs = []
+        for r, i, t in zip(rec["reqs"], rec["idx"], ids):
+            if i >= len(r.output_token_ids):
+                continue                      # dropped: the request stopped at an earlier step
+            r.output_token_ids[i] = t
+            if r.first_token_time is None:
+                r.first_token_time = now
+            finished = r.status is Status.FINISHED and i == len(r.output_token_ids) - 1
+            if t in self.eos_ids:
+                del r.output_token_ids[i + 1:]   # the step queued after this one computed past the stop
+                if not finished:
+                    self.scheduler.finish(r)
+                finished = True
+            outputs.append(StepOutput(r.req_id, t, finished, r))
+        self.steps += 1
+        return outputs
+
+    def _step_sync(self) -> list[StepOutput]:
         batch = self.scheduler.schedule()
         self._swap(batch)
         if batch.is_empty():
@@ -181,4 +266,4 @@ class LLMEngine:
         return {"kv_pool_mb": round(self.kv_cache.memory_bytes() / 2**20, 1), "free_blocks": bm.num_free(),
                 "prefix_hit_rate": round(bm.hit_rate(), 3), "running": len(self.scheduler.running),
                 "waiting": len(self.scheduler.waiting), "swapped": len(self.scheduler.swapped), "steps": self.steps,
-                "graph_steps": self.graph_steps, "swap_outs": self.swap_outs, "swap_ins": self.swap_ins}
+                "graph_steps": self.graph_steps, "pipelined_steps": self.pipelined_steps, "swap_outs": self.swap_outs, "swap_ins": self.swap_ins}
