@@ -107,8 +107,9 @@ def test_linear_silu_mul_rounds_like_linear_then_silu_mul(dtype, d_ff, k):
     product and sum exact in any order, which pins the epilogue bit for bit:
     T(gate) and T(up) rounded once, then tb_silu_mul's arithmetic (and
     tb_linear's one rounding of the same sums). Random inputs stay within the
-    dtype's tolerance of silu(gate) * up from one fp32 product. d_ff 4864:
-    four tiles per workgroup; 48: two; k 1024: two staging passes at 33+ rows."""
+    dtype's tolerance of silu(gate) * up from one fp32 product. Up to 16 rows:
+    8 features per workgroup (gate and up rows in one tile); above: d_ff 4864
+    four tiles per workgroup, 48 two; k 1024: two staging passes at 33+ rows."""
     g = torch.Generator().manual_seed(d_ff + k)
     wi = torch.randint(-2, 3, (2 * d_ff, k), generator=g).to(dtype)
     w = (torch.randn(2 * d_ff, k, generator=g) * 0.05).to(dtype)

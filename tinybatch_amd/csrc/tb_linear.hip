@@ -30,6 +30,9 @@
 //             d_ff later (merged gate/up weight); Y = silu(T(gate)) * T(up)
 //             with the roundings of F.linear followed by tb_silu_mul
 //             (model.py:151-154);
+//   silu8   : the same with 8 features per workgroup: lanes 0-7 of the one
+//             tile load gate rows, lanes 8-15 the up rows of the same
+//             features, so twice the workgroups share the weight stream;
 //   argmax  : the LM head followed by greedy sampling (model.py:157-158,
 //             engine.py:145-151): per row, the largest T(sum) of the
 //             workgroup's columns and its index go to a workspace slot, and
@@ -62,7 +65,7 @@ struct lin_math<bf16_t> {
   }
 };
 
-enum { LIN_ROUND = 0, LIN_PARTIAL = 1, LIN_SILU = 2, LIN_ARGMAX = 3 };
+enum { LIN_ROUND = 0, LIN_PARTIAL = 1, LIN_SILU = 2, LIN_ARGMAX = 3, LIN_SILU8 = 4 };
 constexpr int LIN_WAVES = 4;
 
 // A workgroup walks its K range in windows of up to SP = 28 k-slices (d_model
@@ -122,6 +125,8 @@ __global__ __launch_bounds__(64 * LIN_WAVES) void linear_kernel(lin_args a) {
   constexpr int OUT_TILES = MODE == LIN_SILU ? NT / 2 : NT;
   constexpr int ROWS = 16 * MT;
   static_assert(MODE != LIN_SILU || NT % 2 == 0, "silu pairs gate and up tiles");
+  constexpr bool HALF = MODE == LIN_SILU8;
+  static_assert(!HALF || NT == 1, "silu8: one tile of 8 gate and 8 up columns");
   __shared__ __align__(16) char lds[PS::lds_bytes(NT)];
   // wave-uniform in a scalar register: the K-share tests below become scalar branches
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -129,13 +134,17 @@ __global__ __launch_bounds__(64 * LIN_WAVES) void linear_kernel(lin_args a) {
   int n0[NT];
 #pragma unroll
   for (int j = 0; j < NT; ++j)
-    n0[j] = (MODE == LIN_SILU ? (j / OUT_TILES) * (a.N >> 1) : 0) + (blockIdx.x * OUT_TILES + j % OUT_TILES) * 16;
+    n0[j] = HALF ? (int)blockIdx.x * 8
+                 : (MODE == LIN_SILU ? (j / OUT_TILES) * (a.N >> 1) : 0) + (blockIdx.x * OUT_TILES + j % OUT_TILES) * 16;
   const int slices = a.K / 32;
   const int k_begin = (int)blockIdx.y * slices / (int)gridDim.y;
   const int range = ((int)blockIdx.y + 1) * slices / (int)gridDim.y - k_begin;
   const char* wrow[NT];
 #pragma unroll
-  for (int j = 0; j < NT; ++j) wrow[j] = a.w + (int64_t)(n0[j] + lc) * a.K * 2 + (int64_t)k_begin * 64 + 16 * lg;
+  for (int j = 0; j < NT; ++j) {
+    const int wr = HALF ? (lc < 8 ? n0[j] + lc : (a.N >> 1) + n0[j] + lc - 8) : n0[j] + lc;   // this lane's W row
+    wrow[j] = a.w + (int64_t)wr * a.K * 2 + (int64_t)k_begin * 64 + 16 * lg;
+  }
   const char* const xk = a.x + (int64_t)k_begin * 64;
 
   float4_t acc[MT][NT];
@@ -212,6 +221,25 @@ __global__ __launch_bounds__(64 * LIN_WAVES) void linear_kernel(lin_args a) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) red[(((wave * MT + mt) * NT + j) * 64 + lane) * 4 + e] = acc[mt][j][e];
   __syncthreads();
+  if constexpr (HALF) {
+    // thread t: output (row m, feature n0 + c); gate in column c, up in column c + 8
+    for (int t = threadIdx.x; t < MT * 128; t += 64 * LIN_WAVES) {
+      const int c = t & 7, m = t >> 3;
+      if (m >= a.M) continue;
+      const int mt = m >> 4, r = m & 15;
+      const int l = 16 * (r >> 2) + c, e = r & 3;
+      float gs = 0.f, us = 0.f;
+#pragma unroll
+      for (int wv = 0; wv < LIN_WAVES; ++wv) {
+        gs += red[((wv * MT + mt) * 64 + l) * 4 + e];
+        us += red[((wv * MT + mt) * 64 + l + 8) * 4 + e];
+      }
+      const float g = (float)(T)gs, u = (float)(T)us;   // the gate/up GEMM's roundings
+      const T act = (T)(g / (1.f + expf(-g)));
+      reinterpret_cast<T*>(a.y)[(int64_t)m * a.y_row_stride + n0[0] + c] = (T)((float)act * u);
+    }
+    return;
+  }
   // thread t: output element (row m, tile j, column c); the waves' K shares added in order
   for (int t = threadIdx.x; t < MT * 256 * OUT_TILES; t += 64 * LIN_WAVES) {
     const int c = t & 15, j = (t >> 4) % OUT_TILES, m = t / (16 * OUT_TILES);
@@ -268,10 +296,15 @@ struct lin_shape {
 
 template <typename Tag, int MODE, int MT>
 static int launch_tw(const lin_args& a, dim3 grid, int tw, hipStream_t stream) {
-  if (tw == 4) hipLaunchKernelGGL((linear_kernel<Tag, MT, 4, MODE>), grid, dim3(256), 0, stream, a);
-  else if (tw == 2) hipLaunchKernelGGL((linear_kernel<Tag, MT, 2, MODE>), grid, dim3(256), 0, stream, a);
-  else if constexpr (MODE != LIN_SILU) hipLaunchKernelGGL((linear_kernel<Tag, MT, 1, MODE>), grid, dim3(256), 0, stream, a);
-  else return -1;
+  if constexpr (MODE == LIN_SILU8) {
+    if (tw != 1) return -1;
+    hipLaunchKernelGGL((linear_kernel<Tag, MT, 1, MODE>), grid, dim3(256), 0, stream, a);
+  } else {
+    if (tw == 4) hipLaunchKernelGGL((linear_kernel<Tag, MT, 4, MODE>), grid, dim3(256), 0, stream, a);
+    else if (tw == 2) hipLaunchKernelGGL((linear_kernel<Tag, MT, 2, MODE>), grid, dim3(256), 0, stream, a);
+    else if constexpr (MODE != LIN_SILU) hipLaunchKernelGGL((linear_kernel<Tag, MT, 1, MODE>), grid, dim3(256), 0, stream, a);
+    else return -1;
+  }
   return 0;
 }
 
@@ -299,7 +332,10 @@ static int launch_dtype(const lin_args& a, const lin_shape& s, int32_t dtype, hi
 // (the most workgroups) wins for q/k/v and for the split-K pieces up to 16
 // rows; with more rows every workgroup's X staging weighs more and two or
 // four tiles per workgroup share it (gate/up at 32 rows: 10.1 us with one
-// tile pair, 9.8 with two pairs; down 5.6 -> 5.2 us with two tiles).
+// tile pair, 9.8 with two pairs; down 5.6 -> 5.2 us with two tiles). Gate/up
+// up to 16 rows takes 8 features per workgroup (silu8: 608 workgroups instead
+// of 304 at d_ff 4864, 8.6 -> 7.0 us at 1 row, 9.0 -> 7.7 at 16); above 16
+// rows the doubled X staging makes it slower (9.8 -> 10.2 us at 32).
 static lin_shape round_shape() { return lin_shape{1, 1}; }
 static lin_shape partial_shape(int M, int N, int K, int splits) {
   const int range = K / 32 / splits;
@@ -369,7 +405,9 @@ extern "C" int32_t tb_linear_silu_mul(const void* x, int64_t x_row_stride, const
   TB_CHECK_ARG(y && y_row_stride >= d_ff);
   const lin_args a{(const char*)x, x_row_stride * 2, (const char*)w_gate_up, nullptr, y, y_row_stride,
                    rows, 2 * d_ff, in_features};
-  if (launch_dtype<LIN_SILU>(a, silu_shape(rows, d_ff), dtype, stream)) return TB_ERR_UNSUPPORTED;
+  const int st8 = rows <= 16 ? launch_dtype<LIN_SILU8>(a, lin_shape{1, 1}, dtype, stream)
+                             : launch_dtype<LIN_SILU>(a, silu_shape(rows, d_ff), dtype, stream);
+  if (st8) return TB_ERR_UNSUPPORTED;
   TB_RETURN_LAUNCH_STATUS();
 }
 
