@@ -5,7 +5,8 @@ time (24 layers of norm, projections, RoPE, fused append + paged attention,
 MLP); only the metadata changes. Each batch-size bucket (B padded up) gets one
 graph, captured once, whose launches read fixed device buffers:
 
-* tokens and positions [Bmax];
+* tokens, positions and source rows [Bmax] (row i's input token is the
+  previous step's id of row src[i] where src[i] >= 0, else tokens[i]);
 * the step metadata at fixed capacities — slot mapping, block tables
   [Bmax, ceil(max_model_len / BS)], work items for every partition a row can
   have, partition offsets, split rows — plus the device counts the attention
@@ -22,9 +23,10 @@ replays. ``launch`` returns without waiting: the step's token ids come back
 through a pinned buffer and an event (``collect``), and a row may take its
 input token from the previous step's ids still on the device (its source row),
 so the host can queue step N+1 while step N runs. Two staging and two id
-buffers alternate; a step's buffers are reused two launches later, after its
-ids were collected. Padded rows get no work items and slot -1: they read nothing and
-write nothing, and their outputs are ignored.
+buffers alternate; a step's buffers are reused two launches later, so each
+launch is collected before the launch after next. Padded rows get no work
+items and slot -1: they read nothing and write nothing, and their outputs are
+ignored.
 """
 from __future__ import annotations
 
@@ -191,7 +193,8 @@ class DecodeGraphs:
         return (B, k, ev)
 
     def collect(self, handle) -> list[int]:
-        """The token ids of a launched step (waits for that step only)."""
+        """The token ids of a launched step (waits for that step only). Call it
+        before the launch after next, which reuses the step's id buffer."""
         B, k, ev = handle
         ev.synchronize()
         return self.host_ids[k][:B].tolist()
