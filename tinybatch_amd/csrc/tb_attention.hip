@@ -940,18 +940,22 @@ void paged_step_mfma_kernel(const attn_args a, const int tile_wgs) {
 
 // ---------------------------------------------------------------------------
 // Log-sum-exp merge of the partials of one split row: workgroup (r, c) owns
-// 256 float4 columns (4 consecutive output dims each, head = column / (D/4))
-// of split row r, starting at column 256 c:
+// COMBINE_THREADS float4 columns (4 consecutive output dims each, head =
+// column / (D/4)) of split row r, starting at column COMBINE_THREADS * c. One
+// wave per workgroup: a row's partials are read by several CUs at once instead
+// of streaming through one.
+constexpr int COMBINE_THREADS = 64;
+//
 //   out = sum_p 2^(m_p - M) acc_p / sum_p 2^(m_p - M) l_p.
 // The row's record (row, first partial, count) is one 16-byte load, issued
 // together with the device count; the partials follow in batches of 16 whose
 // loads are all in flight (one batch for a row of up to 16 partitions).
 template <typename Tag, int D>
-__global__ __launch_bounds__(256) void combine_partials_kernel(const attn_args a) {
+__global__ __launch_bounds__(COMBINE_THREADS) void combine_partials_kernel(const attn_args a) {
   constexpr int EB = elem<Tag>::bytes;
   constexpr int QPH = D / 4;                       // float4 columns per head
   constexpr int BATCH = 16;
-  const int col = threadIdx.x + 256 * blockIdx.y;
+  const int col = threadIdx.x + COMBINE_THREADS * blockIdx.y;
   if (col >= a.num_heads * QPH) return;
   const int4 rec = a.split_rows[blockIdx.x];       // the array holds the grid's capacity
   if (a.counts && (int)blockIdx.x >= a.counts[1]) return;   // beyond this step's split rows
@@ -1035,8 +1039,9 @@ static void launch_mfma(const attn_args& a, int num_work, hipStream_t stream) {
 template <typename Tag, int D>
 static void launch_combine(const attn_args& a, int num_split_rows, hipStream_t stream) {
   if (num_split_rows > 0)
-    hipLaunchKernelGGL((combine_partials_kernel<Tag, D>), dim3(num_split_rows, (a.num_heads * (D / 4) + 255) / 256),
-                       dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((combine_partials_kernel<Tag, D>),
+                       dim3(num_split_rows, (a.num_heads * (D / 4) + COMBINE_THREADS - 1) / COMBINE_THREADS),
+                       dim3(COMBINE_THREADS), 0, stream, a);
 }
 
 template <typename Tag, int D>
