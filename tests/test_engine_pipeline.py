@@ -127,3 +127,18 @@ def test_block_pressure_drains_to_synchronous_steps():
     assert got == want
     assert 0 < eng.pipelined_steps < eng.steps
     assert sum(r.preemptions for r in eng.requests) > 0
+
+
+@pytest.mark.parametrize("back", [1, 2, 3])
+def test_stop_token_at_the_end_of_a_budget(back):
+    """A stop token among a request's last budgeted tokens: with back = 2 the
+    request's budget ends with the step queued after the stop's step (finished at
+    that launch), so collecting the stop must not finish it a second time."""
+    tokens, _ = run(make_engine(False), PROMPTS, MAX_NEW)
+    for r in range(len(PROMPTS)):
+        stop = tokens[r][MAX_NEW[r] - back]
+        want = run(make_engine(False, stop=[stop]), PROMPTS, MAX_NEW)
+        eng = make_engine(True, stop=[stop])
+        got = run(eng, PROMPTS, MAX_NEW)
+        assert got == want, f"request {r}, stop {stop}"
+        assert eng.block_manager.num_free() == make_engine(False).block_manager.num_free()

@@ -201,7 +201,8 @@ class LLMEngine:
             finished = r.status is Status.FINISHED and i == len(r.output_token_ids) - 1
             if t in self.eos_ids:
                 del r.output_token_ids[i + 1:]   # the step queued after this one computed past the stop
-                if not finished:
+                # a request whose budget ends with the queued step was finished at that launch
+                if r.status is not Status.FINISHED:
                     self.scheduler.finish(r)
                 finished = True
             outputs.append(StepOutput(r.req_id, t, finished, r))
