@@ -77,17 +77,82 @@ def cpu_baseline(wl, reps: int, budget_s: float) -> dict:
                       f"{med * 1e3:.1f} ms, torch CPU ({cpu_model()})"}
 
 
+def cpu_baseline_mixed(wl, reps: int, budget_s: float) -> dict:
+    """The oracle on the mixed step, on the host's cores: the prefill rows' attention
+    alone (the line's value, TFLOP/s) and the whole layer step (append of all 4152
+    new rows, then attention of every row: 8 causal prefills and 56 decodes)."""
+    import torch
+
+    from oracle import reference_path as ref
+
+    threads = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(threads)
+    pre = wl.part("prefill")
+    pos = torch.tensor(wl.positions, dtype=torch.int64)
+
+    def timed(fn):
+        times, t_start = [], time.perf_counter()
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+            if time.perf_counter() - t_start > budget_s / 2:
+                break
+        times.sort()
+        return times[len(times) // 2], len(times)
+
+    t_pre, n_pre = timed(lambda: ref.attention(pre.q, pre.pool, pre.seq_slices, pre.block_tables,
+                                               pre.context_lens, pre.num_heads, pre.num_kv_heads))
+
+    def whole():
+        ref.kv_write(wl.pool, wl.k_new, wl.v_new, pos, wl.seq_slices, wl.block_tables, wl.block_size)
+        ref.attention(wl.q, wl.pool, wl.seq_slices, wl.block_tables, wl.context_lens, wl.num_heads,
+                      wl.num_kv_heads)
+
+    t_all, n_all = timed(whole)
+    b = wl.algorithmic_bytes()
+    return {"value": round(pre.flops() / t_pre / 1e12, 5), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "step_ms": round(t_all * 1e3, 2),
+            "step_algorithmic_GBps": round((b["append"] + b["attention"]) / t_all / 1e9, 4),
+            "sample": f"prefill attention of the 8 x 512 rows: {n_pre} reps, median {t_pre * 1e3:.1f} ms; "
+                      f"whole layer step (append + attention of {wl.num_tokens} rows): {n_all} reps, median "
+                      f"{t_all * 1e3:.1f} ms; torch CPU ({cpu_model()})"}
+
+
+def kernel_source_hash() -> str:
+    """sha256 (first 16 hex digits) of the HIP sources and the C header: the kernels a
+    profile was measured on."""
+    import hashlib
+
+    h = hashlib.sha256()
+    csrc = os.path.join(ROOT, "tinybatch_amd", "csrc")
+    for name in sorted(os.listdir(csrc)):
+        if name.endswith((".hip", ".h", ".cpp")):
+            with open(os.path.join(csrc, name), "rb") as f:
+                h.update(name.encode() + b"\0" + f.read())
+    with open(os.path.join(ROOT, "include", "tinybatch_amd.h"), "rb") as f:
+        h.update(f.read())
+    return h.hexdigest()[:16]
+
+
 def load_traffic(workload: str, mode: str):
     """HBM bytes per call measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, calibrated
-    against a plain device copy) in the committed profile summary, or None."""
+    against a plain device copy) in the committed profile summary, or None when there is
+    none or it was measured on other kernel sources than these (its kernel_source_sha)."""
     path = os.path.join(ROOT, "profiles", f"paged_decode_{workload}_{mode}.md")
     if not os.path.exists(path):
         return None
+    traffic = sha = None
     with open(path) as f:
         for line in f:
             if line.startswith("traffic_bytes_per_call:"):
-                return int(line.split(":", 1)[1])
-    return None
+                traffic = int(line.split(":", 1)[1])
+            elif line.startswith("kernel_source_sha:"):
+                sha = line.split(":", 1)[1].strip()
+    if sha != kernel_source_hash():
+        _log(f"profile {os.path.basename(path)} was measured on other kernel sources; traffic not reported")
+        return None
+    return traffic
 
 
 def time_step(step, dev, args) -> tuple[float, bool]:
@@ -178,9 +243,24 @@ def bench_mixed(args, dev) -> int:
         ms, graph = time_step(step, dev, args)
         results[which] = (ms / L, w)
         _log(f"{which}: {ms / L * 1e3:.2f} us per layer")
+    # the append kernel alone: the step's 4152 new K/V rows into every layer pool
+    meta = build_step_metadata(wl.positions, wl.seq_slices, wl.block_tables, wl.context_lens,
+                               block_size=wl.block_size, num_blocks=wl.num_blocks, partition_tokens=P).to(dev)
+    k_all, v_all = wl.k_new.to(dev), wl.v_new.to(dev)
+
+    def append_only():
+        for pool in pools:
+            ops.kv_append(pool, k_all, v_all, meta.slot_mapping)
+
+    ms_append, _ = time_step(append_only, dev, args)
+    _log(f"append: {ms_append / L * 1e3:.2f} us per layer")
     plan = ops.BlockCopyPlan(pools, wl.copy_src, wl.copy_dst)
     ms_copy, _ = time_step(plan.launch, dev, args)
     _log(f"copy: {ms_copy * 1e3:.2f} us for {L} layer pools")
+    cpu = None
+    if not args.no_cpu:
+        _log("timing the CPU baseline (oracle) ...")
+        cpu = cpu_baseline_mixed(wl, args.cpu_reps, args.cpu_budget)
 
     step_ms, _ = results["step"]
     b = wl.algorithmic_bytes()
@@ -190,6 +270,7 @@ def bench_mixed(args, dev) -> int:
     dec_ms, dec = results["decode"]
     dec_gbs = dec.algorithmic_bytes()["attention"] / (dec_ms * 1e-3) / 1e9
     copy_gbs = b["copy"] * L / (ms_copy * 1e-3) / 1e9
+    append_gbs = b["append"] / (ms_append / L * 1e-3) / 1e9
     line = {
         "metric": "mixed step: prefill attention TFLOP/s (MFMA), decode attention and block copy GB/s",
         "value": round(pre_tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
@@ -215,17 +296,23 @@ def bench_mixed(args, dev) -> int:
                             "frac": round(dec_gbs / HBM_PEAK_GBS, 4)},
         "copy_roofline": {"bound": "hbm", "achieved": round(copy_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(copy_gbs / HBM_PEAK_GBS, 4), "kernel": "block_copy_kernel"},
-        "cpu_baseline": None,
+        "append_us_per_layer": round(ms_append / L * 1e3, 3),
+        "append_roofline": {"bound": "hbm", "achieved": round(append_gbs, 2), "peak": HBM_PEAK_GBS,
+                            "unit": "GB/s", "frac": round(append_gbs / HBM_PEAK_GBS, 4),
+                            "bytes_per_layer": b["append"], "kernel": "kv_append_kernel"},
+        "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
     return 0
 
 
-def bench_e2e(args, dev) -> int:
+def run_e2e(dev, warmup: int) -> dict:
     """Continuous batching of 32 random-token requests on a random-init Qwen2 at
     0.5B dimensions (bf16), 75% sharing a 400-token prefix, greedy outputs of
-    U{16..256} tokens, everything submitted at t = 0. Reports output tokens per
-    second of wall time, decode-only-step token rate, and TTFT mean / p99."""
+    U{16..256} tokens, everything submitted at t = 0. Returns output tokens per
+    second of wall time, decode-only-step token rate, TTFT mean / p99 (first
+    token time - submit time, the reference's engine.py:131-132) and the run's
+    configuration."""
     import statistics
 
     import torch
@@ -263,28 +350,42 @@ def bench_e2e(args, dev) -> int:
         wall = time.perf_counter() - start
         return eng, reqs, wall, dec_tokens, dec_time
 
-    for _ in range(max(args.warmup, 1)):           # untimed: kernels, GEMM heuristics, allocator
+    for _ in range(max(warmup, 1)):                # untimed: kernels, GEMM heuristics, allocator
         run(wl.prompts[:4], [8] * 4)
     eng, reqs, wall, dec_tokens, dec_time = run(wl.prompts, wl.max_new_tokens)
     out_tokens = sum(len(r.output_token_ids) for r in reqs)
     ttft = sorted(r.first_token_time - r.arrival_time for r in reqs)
-    line = {
-        "metric": "e2e decode tok/s (continuous batching, random-init Qwen2 0.5B dims)",
-        "value": round(out_tokens / wall, 1), "unit": "tok/s", "n_gpus": 1, "steps": eng.steps, "warmup": args.warmup,
-        "ms_per_step": round(wall / max(eng.steps, 1) * 1e3, 3), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic (random token ids; seeded random-init weights; 24/32 requests share a 400-token prefix)",
-        "config": {"workload": f"{wl.name}: 32 requests, prompts U{{32..512}} (sharing ones U{{401..512}}), "
-                               f"outputs U{{16..256}}, greedy", "params": mc.num_params(), "layers": mc.n_layers,
-                   "num_blocks": ecfg.num_blocks, "max_batch_tokens": ecfg.max_batch_tokens,
-                   "max_running": ecfg.max_running, "rope_theta": mc.rope_theta, "rms_eps": mc.rms_eps},
-        "output_tokens": out_tokens, "wall_s": round(wall, 4),
+    res = {
+        "tok_s": round(out_tokens / wall, 1), "output_tokens": out_tokens, "wall_s": round(wall, 4),
+        "steps": eng.steps, "graph_steps": eng.graph_steps, "pipelined_steps": eng.pipelined_steps,
         "decode_only_tok_s": round(dec_tokens / dec_time, 1) if dec_time else None,
         "ttft_mean_ms": round(statistics.mean(ttft) * 1e3, 2),
         "ttft_p99_ms": round(ttft[int(0.99 * (len(ttft) - 1))] * 1e3, 2),
         "prefix_hit_rate": round(eng.block_manager.hit_rate(), 3),
         "preemptions": sum(r.preemptions for r in reqs),
-        "graph_steps": eng.graph_steps,
+        "workload": f"{wl.name}: 32 requests, prompts U{{32..512}} (sharing ones U{{401..512}}), "
+                    f"outputs U{{16..256}}, greedy",
+        "config": {"params": mc.num_params(), "layers": mc.n_layers, "num_blocks": ecfg.num_blocks,
+                   "max_batch_tokens": ecfg.max_batch_tokens, "max_running": ecfg.max_running,
+                   "rope_theta": mc.rope_theta, "rms_eps": mc.rms_eps},
+    }
+    del eng, model
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_e2e(args, dev) -> int:
+    """The end-to-end serving workload alone (run_e2e) as its own JSON line."""
+    r = run_e2e(dev, args.warmup)
+    line = {
+        "metric": "e2e decode tok/s (continuous batching, random-init Qwen2 0.5B dims)",
+        "value": r["tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": r["steps"], "warmup": args.warmup,
+        "ms_per_step": round(r["wall_s"] / max(r["steps"], 1) * 1e3, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random token ids; seeded random-init weights; 24/32 requests share a 400-token prefix)",
+        "config": dict(workload=r["workload"], **r["config"]),
+        **{k: r[k] for k in ("output_tokens", "wall_s", "decode_only_tok_s", "ttft_mean_ms", "ttft_p99_ms",
+                              "prefix_hit_rate", "preemptions", "graph_steps", "pipelined_steps")},
         "cpu_baseline": None,
     }
     print(json.dumps(line), flush=True)
@@ -303,6 +404,8 @@ def main() -> int:
     ap.add_argument("--cpu-reps", type=int, default=5)
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (profiling runs)")
+    ap.add_argument("--no-e2e", action="store_true",
+                    help="headline: skip the end-to-end serving run whose tok/s and TTFT join the line")
     ap.add_argument("--partition", type=int, default=0)
     ap.add_argument("--no-tiles", action="store_true", help="mixed step: prefill rows as row groups, not tiles")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -399,6 +502,15 @@ def main() -> int:
         if big:
             cpu["sample"] += " (first 16 sequences of the workload)"
 
+    e2e = None
+    if not args.no_e2e and args.workload == "qwen-fp16-b64":
+        # the metric's second half: the serving workload through the engine, same invocation
+        del storage, pools
+        torch.cuda.empty_cache()
+        _log("end-to-end serving run ...")
+        e2e = run_e2e(dev, 1)
+        _log(f"e2e: {e2e['tok_s']} tok/s, TTFT mean {e2e['ttft_mean_ms']} ms, p99 {e2e['ttft_p99_ms']} ms")
+
     attn = "paged_attn_valu_kernel" if wl.dtype == torch.float32 else "paged_attn_mfma_kernel"
     kernel = attn + " + combine_partials_kernel" + ("" if fused else " + kv_append_kernel")
     line = {
@@ -430,6 +542,11 @@ def main() -> int:
         },
         "cpu_baseline": cpu,
     }
+    if e2e is not None:
+        line["e2e_tok_s"] = e2e["tok_s"]
+        line["ttft_mean_ms"] = e2e["ttft_mean_ms"]
+        line["ttft_p99_ms"] = e2e["ttft_p99_ms"]
+        line["e2e"] = e2e
     print(json.dumps(line), flush=True)
     return 0
 

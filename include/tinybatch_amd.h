@@ -31,6 +31,7 @@ extern "C" {
 #define TB_ERR_INVALID_ARG (-1)  /* null pointer, bad size, inconsistent shape */
 #define TB_ERR_UNSUPPORTED (-2)  /* shape/dtype combination with no compiled kernel */
 #define TB_ERR_LAUNCH (-3)       /* hipLaunchKernel reported an error */
+#define TB_ERR_INDEX (-5)        /* a block table too short for a context, or a block id outside the pool */
 
 /* element type of q / k / v / pool / out */
 #define TB_DTYPE_F32 0
@@ -142,8 +143,13 @@ int32_t tb_kv_gather(const void* pool, int64_t num_blocks,
  * Fused decode append (k_new != NULL): each row's own newest position
  * row_ctx-1 is read from k_new/v_new ([num_rows][num_kv_heads][head_dim]) and
  * written to its slot in the pool by the same kernel, replacing a separate
- * tb_kv_append. Valid only when no row reads another row's newest slot, which
- * holds for a batch of decode rows (one new token per sequence).
+ * tb_kv_append. Valid only for decode rows (one new token per sequence) whose
+ * newest positions map to distinct pool slots: each row stores and attends to
+ * its own new K/V, where the reference's sequential write would let the last
+ * row in batch order win a shared slot for every row that reads it
+ * (src/tinybatch/kv_cache.py:33-38). A step with a shared slot must use
+ * tb_kv_append (its slot_mapping marks the superseded rows -1) and then this
+ * call without k_new. The kernels do not read slot_mapping and cannot detect it.
  * RoPE in the prologue (rope_cos != NULL, the tables of tb_kv_append_rope):
  * q holds the projections before rotation; every query row is rotated at its
  * position row_ctx - 1 as it is loaded (the engine's _rope of q,
@@ -151,6 +157,51 @@ int32_t tb_kv_gather(const void* pool, int64_t num_blocks,
  * of k_new. NULL: q (and k_new) are already rotated.
  */
 int32_t tb_attention_partition_tokens(int32_t dtype, int32_t head_dim);
+
+/* ---------------------------------------------------------------------------
+ * Host-side builder of a step's metadata (no device call, nothing allocated).
+ * Takes the step as the reference's forward pass receives it
+ * (src/tinybatch/model.py:101-109, built by LLMEngine.step, engine.py:99-126):
+ *   query_start_loc [num_seqs + 1]: sequence b's new rows are the flat rows
+ *     query_start_loc[b] .. query_start_loc[b+1]-1 (its seq_slices entry),
+ *     non-decreasing, query_start_loc[num_seqs] <= num_tokens;
+ *   context_lens [num_seqs]: positions each sequence has after the step;
+ *   positions [num_tokens] (int64, may be NULL): row i of sequence b must be
+ *     at context_lens[b] - q_len[b] + i (engine.py:110,117), which the mask
+ *     of model.py:139-145 assumes; checked when given;
+ *   block_tables [num_seqs][max_blocks_per_seq]: physical block ids, padded;
+ *     the first ceil(context_lens[b] / block_size) entries are read.
+ * Writes, for tb_kv_append and tb_paged_attention:
+ *   slot_mapping [num_tokens]: slot of every new row (kv_cache.py:34-38), -1
+ *     outside every sequence and for every row whose slot a later row also
+ *     writes (the reference's sequential write lets the last one win);
+ *   row_part_offsets [num_tokens + 1], work_items [W][4], prefill_tiles [N][4]
+ *     (rows of sequences with >= 16 new rows and a context <= 4096 or <= 16x
+ *     those rows, when tile_prefill != 0), split_rows [S][4]: the arrays
+ *     tb_paged_attention documents, work items ordered by partition length
+ *     (shortest first) and tiles by positions covered (most first), both
+ *     stable, rows_per_item (1..16) consecutive rows grouped per item;
+ *   counts [5] (int64): W, N, S, total_partitions, max_parts_per_row.
+ * tb_step_metadata_counts gives the counts alone (the sizes to provide).
+ * Capacities below the counts: TB_ERR_INVALID_ARG (counts still written).
+ * A table shorter than a context or a block id outside [0, num_blocks):
+ * TB_ERR_INDEX (the reference's IndexError, kv_cache.py:35,43). partition_tokens
+ * <= 8192. Replaces the per-layer host-to-device table copies and the mask
+ * loop of the reference (kv_cache.py:35,43; model.py:142-145). */
+int32_t tb_step_metadata_counts(const int32_t* query_start_loc, int32_t num_seqs,
+                                const int32_t* context_lens, int32_t num_tokens,
+                                int32_t block_size, int32_t partition_tokens,
+                                int32_t rows_per_item, int32_t tile_prefill, int64_t* counts);
+
+int32_t tb_build_step_metadata(const int32_t* query_start_loc, int32_t num_seqs,
+                               const int32_t* context_lens, const int64_t* positions,
+                               int32_t num_tokens, const int32_t* block_tables,
+                               int32_t max_blocks_per_seq, int64_t num_blocks, int32_t block_size,
+                               int32_t partition_tokens, int32_t rows_per_item, int32_t tile_prefill,
+                               int32_t* slot_mapping, int32_t* row_part_offsets,
+                               int32_t* work_items, int32_t work_capacity,
+                               int32_t* prefill_tiles, int32_t tile_capacity,
+                               int32_t* split_rows, int32_t split_capacity, int64_t* counts);
 
 /* Prefill tile shape: rows per tile, positions per tile partition. */
 #define TB_PREFILL_TILE_ROWS 64

@@ -267,3 +267,20 @@ def test_pipelined_decode_streams_match_synchronous_steps(dtype):
     got_s, got_streams_s, e2 = run(True, (stop,))
     assert got_s == want_s and got_streams_s == want_streams_s and e2.pipelined_steps > 0
     assert any(t[-1] == stop and len(t) < m for t, m in zip(want_s, max_new + [20]))
+
+
+def test_decode_graphs_refuse_a_step_with_a_shared_slot():
+    """The captured step appends inside attention, each row its own K/V; a step
+    whose rows share their newest slot is not queued (launch returns None) and
+    the engine runs it with the separate append."""
+    from tinybatch_amd.decode_graphs import DecodeGraphs
+
+    mc = small_cfg(layers=2, heads=4, kv_heads=2)
+    model = Qwen2Paged(mc, DEV, torch.bfloat16, seed=5)
+    cache = PagedKVCache(mc.n_layers, 16, 16, mc.n_kv_heads, mc.head_dim, DEV, torch.bfloat16)
+    graphs = DecodeGraphs(model, cache, max_batch=4, max_model_len=128)
+    ctx = [20, 36]
+    assert graphs.launch([1, 2], [19, 35], [[3, 6], [0, 5, 6]], ctx) is None
+    assert graphs.run([1, 2], [19, 35], [[3, 6], [0, 5, 6]], ctx) is None
+    ids = graphs.run([1, 2], [19, 35], [[3, 6], [0, 5, 7]], ctx)
+    assert len(ids) == 2 and all(0 <= t < mc.vocab_size for t in ids)

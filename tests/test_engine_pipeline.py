@@ -21,14 +21,19 @@ class StandInGraphs:
     """launch/collect/run of DecodeGraphs on the host: row i's input token is the
     previous launch's id of row src[i] where src[i] >= 0."""
 
-    def __init__(self):
+    def __init__(self, refuse=()):
         self.prev: list[int] = []
         self.launches = 0
+        self.calls = 0
+        self.refuse = set(refuse)   # launch calls refused as a step with two rows on one slot
 
     def bucket(self, B):
         return next((b for b in (1, 2, 4, 8) if b >= B), None)
 
     def launch(self, tokens, positions, block_tables, context_lens, src_rows=None):
+        self.calls += 1
+        if self.calls in self.refuse:
+            return None
         src = src_rows if src_rows is not None else [-1] * len(tokens)
         inputs = [self.prev[s] if s >= 0 else t for t, s in zip(tokens, src)]
         assert all(t >= 0 for t in inputs), "a placeholder reached the model"
@@ -41,10 +46,11 @@ class StandInGraphs:
         return list(handle)
 
     def run(self, tokens, positions, block_tables, context_lens):
-        return self.collect(self.launch(tokens, positions, block_tables, context_lens))
+        h = self.launch(tokens, positions, block_tables, context_lens)
+        return None if h is None else self.collect(h)
 
 
-def make_engine(pipeline: bool, *, num_blocks=64, stop=(), max_running=4):
+def make_engine(pipeline: bool, *, num_blocks=64, stop=(), max_running=4, refuse=()):
     cfg = EngineConfig(num_blocks=num_blocks, block_size=4, max_batch_tokens=48, max_running=max_running,
                        pipeline_decode=pipeline, stop_token_ids=tuple(stop))
     eng = LLMEngine.__new__(LLMEngine)          # no model, cache or device: the steps are stood in for
@@ -56,24 +62,15 @@ def make_engine(pipeline: bool, *, num_blocks=64, stop=(), max_running=4):
     eng.swap_outs = eng.swap_ins = 0
     eng._swap_reads = []
     eng._inflight = None
-    eng.graphs = StandInGraphs()
+    eng.graphs = StandInGraphs(refuse)
+    eng.eager_steps = 0
 
-    def step_sync():
-        # LLMEngine._step_sync with the forward replaced by the rule
-        batch = eng.scheduler.schedule()
-        if batch.is_empty():
-            return []
-        ordered = batch.prefill + batch.decode
-        eng.last_step_prefills = len(batch.prefill)
-        ids, pos, slices, tables, ctx = LLMEngine.build_step(batch.prefill, batch.decode)
-        if not batch.prefill and eng.graphs.bucket(len(ordered)) is not None:
-            nxt = eng.graphs.run(ids, pos, tables, ctx)
-            eng.graph_steps += 1
-        else:
-            nxt = [rule(ids[e - 1], pos[e - 1]) for s, e in slices]
-        return eng._finish_step(ordered, nxt)
+    def forward_eager(ordered, ids, pos, slices, tables, ctx):
+        # LLMEngine._forward_eager with the model replaced by the rule
+        eng.eager_steps += 1
+        return [rule(ids[e - 1], pos[e - 1]) for s, e in slices]
 
-    eng._step_sync = step_sync
+    eng._forward_eager = forward_eager
     return eng
 
 
@@ -142,3 +139,16 @@ def test_stop_token_at_the_end_of_a_budget(back):
         got = run(eng, PROMPTS, MAX_NEW)
         assert got == want, f"request {r}, stop {stop}"
         assert eng.block_manager.num_free() == make_engine(False).block_manager.num_free()
+
+
+@pytest.mark.parametrize("pipeline", [False, True])
+def test_steps_the_graphs_refuse_run_eagerly(pipeline):
+    """A decode step whose rows share a pool slot is refused by the graphs (their
+    fused append cannot give the reference's last-writer-wins result): the engine
+    then runs the step's rows eagerly, draining a queued step first, with the
+    same token streams."""
+    want = run(make_engine(False), PROMPTS, MAX_NEW)
+    eng = make_engine(pipeline, refuse=(3, 7, 8, 15))
+    got = run(eng, PROMPTS, MAX_NEW)
+    assert got == want
+    assert eng.graphs.calls > 15 and eng.eager_steps >= 4 + 1   # the refused steps and the first prefill

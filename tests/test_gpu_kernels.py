@@ -97,6 +97,38 @@ def test_append_duplicate_slot_last_writer_wins():
     assert torch.equal(_bits(gp.cpu()), _bits(want))
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_decode_rows_sharing_a_slot_last_writer_wins(dtype):
+    """Rows 0 and 2 of a decode step have their newest positions on one pool slot
+    (block 6, offset 3). The reference writes the whole batch first, row 2 last,
+    and both rows then read row 2's K/V there (kv_cache.py:33-38). The fused
+    append cannot give that and is refused; append + attention match the oracle."""
+    g = torch.Generator().manual_seed(21)
+    Hq, Hkv, D, BS, NB = 8, 2, 64, 16, 12
+    pool = torch.randn(NB, 2, Hkv, BS, D, generator=g).to(dtype)
+    tables = [[3, 6], [1, 2, 4], [0, 5, 6]]
+    ctx = [20, 40, 36]                        # newest positions 19, 39, 35: slots 6*16+3, 4*16+7, 6*16+3
+    pos = [c - 1 for c in ctx]
+    slices = [(i, i + 1) for i in range(3)]
+    q = torch.randn(3, Hq, D, generator=g).to(dtype)
+    k = torch.randn(3, Hkv, D, generator=g).to(dtype)
+    v = torch.randn(3, Hkv, D, generator=g).to(dtype)
+    want_pool = pool.clone()
+    ref.kv_write(want_pool, k, v, torch.tensor(pos), slices, tables, BS)
+    want = ref.attention(q, want_pool, slices, tables, ctx, Hq, Hkv)
+    meta = _meta(pos, slices, tables, ctx, BS, NB, P=ops.partition_tokens(dtype, D))
+    assert meta.slot_mapping_np.tolist() == [-1, 4 * 16 + 7, 6 * 16 + 3]
+    gp = pool.to(DEV)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    with pytest.raises(ValueError, match="one pool slot"):
+        ops.paged_attention(qd, gp, meta, num_heads=Hq, k_new=kd, v_new=vd)
+    ops.kv_append(gp, kd, vd, meta.slot_mapping)
+    out = ops.paged_attention(qd, gp, meta, num_heads=Hq)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(gp.cpu()), _bits(want_pool))
+    torch.testing.assert_close(out.cpu().float(), want.float(), **TOL[dtype])
+
+
 # ---------------------------------------------------------------- gather
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_gather_bit_exact(dtype):

@@ -19,6 +19,7 @@ TB_OK = 0
 TB_ERR_INVALID_ARG = -1
 TB_ERR_UNSUPPORTED = -2
 TB_ERR_LAUNCH = -3
+TB_ERR_INDEX = -5
 
 DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 
@@ -57,6 +58,15 @@ SIGNATURES = {
         c_vp,                   # device_counts
         c_vp, c_vp, c_i32,      # rope_cos, rope_sin, rope_max_position
         c_vp,                   # stream
+    ]),
+    "tb_step_metadata_counts": (c_i32, [c_vp, c_i32, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp]),
+    "tb_build_step_metadata": (c_i32, [
+        c_vp, c_i32, c_vp, c_vp, c_i32,      # query_start_loc, num_seqs, context_lens, positions, num_tokens
+        c_vp, c_i32, c_i64, c_i32,           # block_tables, max_blocks_per_seq, num_blocks, block_size
+        c_i32, c_i32, c_i32,                 # partition_tokens, rows_per_item, tile_prefill
+        c_vp, c_vp,                          # slot_mapping, row_part_offsets
+        c_vp, c_i32, c_vp, c_i32, c_vp, c_i32,   # work items, tiles, split rows (+ capacities)
+        c_vp,                                # counts
     ]),
     "tb_block_copy": (c_i32, [c_vp, c_i32, c_i64, c_vp, c_vp, c_i32, c_i64, c_vp]),
     "tb_block_gather": (c_i32, [c_vp, c_i64, c_vp, c_i32, c_vp, c_i64, c_vp]),

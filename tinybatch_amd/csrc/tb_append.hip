@@ -232,6 +232,7 @@ extern "C" const char* tb_status_string(int32_t status) {
     case TB_ERR_INVALID_ARG: return "invalid argument";
     case TB_ERR_UNSUPPORTED: return "unsupported shape or dtype (no compiled kernel)";
     case TB_ERR_LAUNCH: return "kernel launch failed";
+    case TB_ERR_INDEX: return "block table too short for a context, or a block id outside the pool";
     default: return "unknown status";
   }
 }

@@ -1110,23 +1110,24 @@ extern "C" size_t tb_paged_attention_workspace_bytes(int32_t total_partitions, i
   return (size_t)total_partitions * num_heads * ((size_t)head_dim + 2) * sizeof(float);
 }
 
-extern "C" int32_t tb_paged_attention(const void* q, int64_t q_row_stride, void* pool,
-                                      int64_t num_blocks, void* out, int64_t out_row_stride,
-                                      const int32_t* block_tables, int32_t max_blocks_per_seq,
-                                      const int32_t* work_items, int32_t num_work_items,
-                                      const int32_t* prefill_tiles, int32_t num_prefill_tiles,
-                                      const int32_t* row_part_offsets, int32_t num_rows,
-                                      const int32_t* split_rows, int32_t num_split_rows,
-                                      int32_t max_parts_per_row, int32_t partition_tokens,
-                                      int32_t total_partitions, int32_t num_heads,
-                                      int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
-                                      float scale, int32_t dtype, const void* k_new,
-                                      int64_t k_row_stride, const void* v_new, int64_t v_row_stride,
-                                      void* workspace, size_t workspace_bytes,
-                                      const int32_t* device_counts, const float* rope_cos,
-                                      const float* rope_sin, int32_t rope_max_position,
-                                      hipStream_t stream) {
-  using namespace tb;
+namespace tb {
+
+static int32_t paged_attention_impl(const void* q, int64_t q_row_stride, void* pool,
+                                    int64_t num_blocks, void* out, int64_t out_row_stride,
+                                    const int32_t* block_tables, int32_t max_blocks_per_seq,
+                                    const int32_t* work_items, int32_t num_work_items,
+                                    const int32_t* prefill_tiles, int32_t num_prefill_tiles,
+                                    const int32_t* row_part_offsets, int32_t num_rows,
+                                    const int32_t* split_rows, int32_t num_split_rows,
+                                    int32_t max_parts_per_row, int32_t partition_tokens,
+                                    int32_t total_partitions, int32_t num_heads,
+                                    int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                    float scale, int32_t dtype, const void* k_new,
+                                    int64_t k_row_stride, const void* v_new, int64_t v_row_stride,
+                                    void* workspace, size_t workspace_bytes,
+                                    const int32_t* device_counts, const float* rope_cos,
+                                    const float* rope_sin, int32_t rope_max_position,
+                                    hipStream_t stream) {
   const int eb = elem_bytes(dtype);
   TB_CHECK_ARG(eb > 0);
   TB_CHECK_ARG(num_heads > 0 && num_kv_heads > 0 && num_heads % num_kv_heads == 0);
@@ -1219,4 +1220,31 @@ extern "C" int32_t tb_paged_attention(const void* q, int64_t q_row_stride, void*
   }
   if (st != TB_OK) return st;
   TB_RETURN_LAUNCH_STATUS();
+}
+
+}  // namespace tb
+
+extern "C" int32_t tb_paged_attention(const void* q, int64_t q_row_stride, void* pool,
+                                      int64_t num_blocks, void* out, int64_t out_row_stride,
+                                      const int32_t* block_tables, int32_t max_blocks_per_seq,
+                                      const int32_t* work_items, int32_t num_work_items,
+                                      const int32_t* prefill_tiles, int32_t num_prefill_tiles,
+                                      const int32_t* row_part_offsets, int32_t num_rows,
+                                      const int32_t* split_rows, int32_t num_split_rows,
+                                      int32_t max_parts_per_row, int32_t partition_tokens,
+                                      int32_t total_partitions, int32_t num_heads,
+                                      int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                      float scale, int32_t dtype, const void* k_new,
+                                      int64_t k_row_stride, const void* v_new, int64_t v_row_stride,
+                                      void* workspace, size_t workspace_bytes,
+                                      const int32_t* device_counts, const float* rope_cos,
+                                      const float* rope_sin, int32_t rope_max_position,
+                                      hipStream_t stream) {
+  return tb::paged_attention_impl(q, q_row_stride, pool, num_blocks, out, out_row_stride, block_tables,
+                                  max_blocks_per_seq, work_items, num_work_items, prefill_tiles,
+                                  num_prefill_tiles, row_part_offsets, num_rows, split_rows, num_split_rows,
+                                  max_parts_per_row, partition_tokens, total_partitions, num_heads,
+                                  num_kv_heads, head_dim, block_size, scale, dtype, k_new, k_row_stride, v_new,
+                                  v_row_stride, workspace, workspace_bytes, device_counts, rope_cos, rope_sin,
+                                  rope_max_position, stream);
 }

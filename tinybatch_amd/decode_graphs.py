@@ -36,8 +36,7 @@ import torch.nn.functional as F
 
 from . import layer_ops, ops
 from .kv_cache import PagedKVCache
-from .metadata import (StepMetadata, build_step_metadata, decode_staging_offsets, pack_decode_step,
-                       pack_step)
+from .metadata import StepMetadata, decode_staging_offsets, pack_decode_step
 from .model import Qwen2Paged
 
 DEFAULT_BUCKETS = (1, 2, 4, 8, 16, 24, 32, 48, 64, 96, 128, 192, 256)
@@ -92,7 +91,8 @@ class DecodeGraphs:
         m = StepMetadata(num_tokens=Bp, num_seqs=Bp, block_size=self.BS, partition_tokens=self.P,
                          max_blocks_per_seq=self.max_nb, num_work_items=Bp * self.max_parts,
                          total_partitions=Bp * self.max_parts, max_parts_per_row=self.max_parts,
-                         decode_only=True, rows_per_item=1, num_prefill_tiles=0, num_split_rows=Bp,
+                         decode_only=True, rows_per_item=1, num_prefill_tiles=0,
+                         num_split_rows=Bp if self.max_parts > 1 else 0,   # rows of one partition never split
                          slot_mapping_np=e, block_tables_np=e, work_np=e, row_part_off_np=e, row_ctx_np=e,
                          prefill_tiles_np=e, split_rows_np=e)
         m.slot_mapping = self._view(0, Bp)
@@ -159,7 +159,9 @@ class DecodeGraphs:
                context_lens: list[int], src_rows: list[int] | None = None):
         """Queue one decode step (one row per sequence) without waiting for it. Row i's
         input token is tokens[i], or, where src_rows[i] >= 0, the id the previous launch
-        produced for its row src_rows[i]. Returns the handle ``collect`` takes."""
+        produced for its row src_rows[i]. Returns the handle ``collect`` takes, or None
+        when two rows' newest positions map to one pool slot (nothing is queued: such a
+        step needs the separate append, whose last writer wins, before attention)."""
         B = len(tokens)
         Bp = self.bucket(B)
         if Bp is None:
@@ -176,9 +178,12 @@ class DecodeGraphs:
         h, tp = self.host_nps[k], self.host_tps[k]
         if not pack_decode_step(h, self.offs, Bp, self.max_nb, context_lens, block_tables,
                                 block_size=self.BS, num_blocks=self.cache.num_blocks, partition_tokens=self.P):
-            meta = build_step_metadata(positions, [(i, i + 1) for i in range(B)], block_tables, context_lens,
-                                       block_size=self.BS, num_blocks=self.cache.num_blocks, partition_tokens=self.P)
-            pack_step(h, self.offs, Bp, self.max_nb, meta)
+            # Two rows write one slot. The reference appends the whole batch first, the
+            # last row in batch order winning, and then both rows attend to the winner's
+            # K/V; the fused append of the captured step would have each row store and
+            # read its own. Nothing is queued: the caller runs this step unfused.
+            self.turn ^= 1
+            return None
         tp[0, :B] = tokens
         tp[1, :B] = positions
         tp[2, :B] = -1 if src_rows is None else src_rows
@@ -201,5 +206,7 @@ class DecodeGraphs:
 
     def run(self, tokens: list[int], positions: list[int], block_tables: list[list[int]],
             context_lens: list[int]) -> list[int]:
-        """Greedy next token of each decode row (one row per sequence)."""
-        return self.collect(self.launch(tokens, positions, block_tables, context_lens))
+        """Greedy next token of each decode row (one row per sequence), or None for a
+        step with two rows on one slot (see ``launch``)."""
+        handle = self.launch(tokens, positions, block_tables, context_lens)
+        return None if handle is None else self.collect(handle)

@@ -128,9 +128,8 @@ class LLMEngine:
         read blocks that this step may hand to others, swap-ins fill the blocks the
         resumed sequences decode from (K3 gather / scatter to pinned host memory)."""
         self._swap_reads = []          # the previous step ended with a synchronising copy
-        L = self.model.cfg.n_layers
         for req, blocks in batch.swap_out:
-            staging = torch.empty((L, len(blocks)) + tuple(self.kv_cache.pools[0].shape[1:]),
+            staging = torch.empty((self.model.cfg.n_layers, len(blocks)) + tuple(self.kv_cache.pools[0].shape[1:]),
                                   dtype=self.dtype, pin_memory=True)
             self.kv_cache.swap_out(blocks, list(staging))
             req.swap_staging = staging
@@ -172,6 +171,11 @@ class LLMEngine:
         ctx = [r.context_len() for r in ordered]
         handle = self.graphs.launch(tokens, [c - 1 for c in ctx], [r.block_table for r in ordered], ctx,
                                     src_rows=src)
+        if handle is None:
+            # two rows on one slot (the graph's fused append cannot serve it): collect the
+            # queued step, whose tokens these rows take as input, then run the rows unfused
+            outs = self._collect(prev) if prev is not None else []
+            return outs + self._run([], [r for r in ordered if r.status is Status.RUNNING], graphs=False)
         self.graph_steps += 1
         self.pipelined_steps += 1
         self.last_step_prefills = 0
@@ -214,22 +218,35 @@ class LLMEngine:
         self._swap(batch)
         if batch.is_empty():
             return []
-        ordered = batch.prefill + batch.decode
-        self.last_step_prefills = len(batch.prefill)
-        token_ids, positions, seq_slices, block_tables, context_lens = self.build_step(batch.prefill, batch.decode)
-        if (self.graphs is not None and not batch.prefill and all(r.temperature <= 0.0 for r in ordered)
+        return self._run(batch.prefill, batch.decode)
+
+    def _run(self, prefill: list[Request], decode: list[Request], graphs: bool = True) -> list[StepOutput]:
+        """Forward and sample the scheduled rows: a graph replay for greedy
+        decode-only steps the graphs accept, the eager forward otherwise."""
+        ordered = prefill + decode
+        self.last_step_prefills = len(prefill)
+        if not ordered:
+            return []
+        token_ids, positions, seq_slices, block_tables, context_lens = self.build_step(prefill, decode)
+        if (graphs and self.graphs is not None and not prefill and all(r.temperature <= 0.0 for r in ordered)
                 and self.graphs.bucket(len(ordered)) is not None):
             next_ids = self.graphs.run(token_ids, positions, block_tables, context_lens)
-            self.graph_steps += 1
-            return self._finish_step(ordered, next_ids)
+            if next_ids is not None:
+                self.graph_steps += 1
+                return self._finish_step(ordered, next_ids)
+        next_ids = self._forward_eager(ordered, token_ids, positions, seq_slices, block_tables, context_lens)
+        return self._finish_step(ordered, next_ids)
+
+    def _forward_eager(self, ordered, token_ids, positions, seq_slices, block_tables, context_lens) -> list[int]:
+        """Launch by launch: per layer the separate append (its last writer wins on
+        a shared slot) then attention, as the reference's forward orders them."""
         tok = torch.tensor(token_ids, dtype=torch.int64).pin_memory().to(self.device, non_blocking=True)
         pos = torch.tensor(positions, dtype=torch.int64).pin_memory().to(self.device, non_blocking=True)
         # the step's metadata, built from the host lists (no device round trip) and shared by every layer
         self.kv_cache.step_metadata(pos, seq_slices, block_tables, context_lens,
                                     self.kv_cache.rows_per_item(self.model.cfg.n_heads), host_positions=positions)
         logits = self.model.forward(tok, pos, seq_slices, block_tables, context_lens, self.kv_cache)
-        next_ids = self._sample(logits, ordered)
-        return self._finish_step(ordered, next_ids)
+        return self._sample(logits, ordered)
 
     def _finish_step(self, ordered: list[Request], next_ids: list[int]) -> list[StepOutput]:
         now = time.perf_counter()

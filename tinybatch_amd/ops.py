@@ -208,6 +208,12 @@ def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, 
             raise ValueError("k_new and v_new go together")
         if not meta.decode_only or meta.num_prefill_tiles:
             raise ValueError("fused append needs a decode-only step (one query row per sequence)")
+        sm = meta.slot_mapping_np
+        if sm.size and np.any((sm < 0) & (meta.row_ctx_np > 0)):
+            # a superseded writer of a shared slot: the kernel would store and read each
+            # row's own K/V where the reference's last writer wins (kv_cache.py:33-38)
+            raise ValueError("two decode rows write one pool slot; the fused append cannot serve the "
+                             "step: append with kv_append, then call paged_attention without k_new")
         for name, t in (("k_new", k_new), ("v_new", v_new)):
             _lib.require_gpu_tensor(name, t)
             if t.dtype != pool.dtype or t.shape[0] != T:
@@ -215,23 +221,22 @@ def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, 
         ks = _rows_view("k_new", k_new, hkv, d)
         vs = _rows_view("v_new", v_new, hkv, d)
         ksp, vsp = k_new.data_ptr(), v_new.data_ptr()
+    head = (q.data_ptr(), qs, pool.data_ptr(), nb, out.data_ptr(), os_,
+            meta.block_tables.data_ptr(), meta.max_blocks_per_seq,
+            meta.work.data_ptr(), meta.num_work_items,
+            meta.prefill_tiles.data_ptr(), meta.num_prefill_tiles,
+            meta.row_part_off.data_ptr(), T,
+            meta.split_rows.data_ptr(), meta.num_split_rows,
+            max(meta.max_parts_per_row, 1), meta.partition_tokens, meta.total_partitions,
+            num_heads, hkv, d, bs, float(scale), _lib.DTYPE_CODE[q.dtype], ksp, ks, vsp, vs)
+    tail = (_ptr(meta.device_counts),
+            None if rope is None else rope.cos.data_ptr(), None if rope is None else rope.sin.data_ptr(),
+            0 if rope is None else rope.max_position, _lib.stream_handle(q.device))
     if workspace is None:
         workspace = workspace_for(meta, num_heads, d, q.device)
     ws = workspace
     ws_bytes = 0 if ws is None else ws.numel() * ws.element_size()
-    st = _lib.lib().tb_paged_attention(
-        q.data_ptr(), qs, pool.data_ptr(), nb, out.data_ptr(), os_,
-        meta.block_tables.data_ptr(), meta.max_blocks_per_seq,
-        meta.work.data_ptr(), meta.num_work_items,
-        meta.prefill_tiles.data_ptr(), meta.num_prefill_tiles,
-        meta.row_part_off.data_ptr(), T,
-        meta.split_rows.data_ptr(), meta.num_split_rows,
-        max(meta.max_parts_per_row, 1), meta.partition_tokens, meta.total_partitions,
-        num_heads, hkv, d, bs, float(scale), _lib.DTYPE_CODE[q.dtype],
-        ksp, ks, vsp, vs, _ptr(ws), ws_bytes, _ptr(meta.device_counts),
-        None if rope is None else rope.cos.data_ptr(), None if rope is None else rope.sin.data_ptr(),
-        0 if rope is None else rope.max_position, _lib.stream_handle(q.device))
-    _lib.check(st, "tb_paged_attention")
+    _lib.check(_lib.lib().tb_paged_attention(*head, _ptr(ws), ws_bytes, *tail), "tb_paged_attention")
     return out
 
 
