@@ -31,6 +31,7 @@ extern "C" {
 #define TB_ERR_INVALID_ARG (-1)  /* null pointer, bad size, inconsistent shape */
 #define TB_ERR_UNSUPPORTED (-2)  /* shape/dtype combination with no compiled kernel */
 #define TB_ERR_LAUNCH (-3)       /* hipLaunchKernel reported an error */
+#define TB_ERR_SCRATCH (-4)      /* tb_paged_attention_noalloc: partials exceed its scratch */
 #define TB_ERR_INDEX (-5)        /* a block table too short for a context, or a block id outside the pool */
 
 /* element type of q / k / v / pool / out */
@@ -228,6 +229,40 @@ int32_t tb_paged_attention(const void* q, int64_t q_row_stride,
                            const int32_t* device_counts,
                            const float* rope_cos, const float* rope_sin, int32_t rope_max_position,
                            hipStream_t stream);
+
+/* tb_paged_attention without a workspace: the split-row partials go to a
+ * static device array of TB_NOALLOC_SCRATCH_BYTES that the library holds on
+ * every GPU it runs on, until the process ends. No counterpart in the
+ * reference (which allocates per call): this entry point is for callers that
+ * cannot allocate device memory, such as code under HIP graph capture, tight
+ * serving loops or harnesses that forbid hipMalloc; it calls no hipMalloc,
+ * hipFree or allocating library routine. Arguments and results are those of
+ * tb_paged_attention (the same kernels). A call whose partials need more than
+ * TB_NOALLOC_SCRATCH_BYTES (tb_paged_attention_workspace_bytes of its
+ * total_partitions) returns TB_ERR_SCRATCH and launches nothing. `stream` must
+ * belong to the current device. Every call on a GPU shares that GPU's array,
+ * so calls that may overlap in time on one GPU race (issue them on one
+ * stream); nothing in it needs to start at zero, each partial a call reads
+ * being written by that call first. */
+#define TB_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+int32_t tb_paged_attention_noalloc(const void* q, int64_t q_row_stride,
+                                   void* pool, int64_t num_blocks,
+                                   void* out, int64_t out_row_stride,
+                                   const int32_t* block_tables, int32_t max_blocks_per_seq,
+                                   const int32_t* work_items, int32_t num_work_items,
+                                   const int32_t* prefill_tiles, int32_t num_prefill_tiles,
+                                   const int32_t* row_part_offsets, int32_t num_rows,
+                                   const int32_t* split_rows, int32_t num_split_rows,
+                                   int32_t max_parts_per_row, int32_t partition_tokens,
+                                   int32_t total_partitions,
+                                   int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                   int32_t block_size, float scale, int32_t dtype,
+                                   const void* k_new, int64_t k_row_stride,
+                                   const void* v_new, int64_t v_row_stride,
+                                   const int32_t* device_counts,
+                                   const float* rope_cos, const float* rope_sin, int32_t rope_max_position,
+                                   hipStream_t stream);
 
 /* ---------------------------------------------------------------------------
  * K3 — block copy across every layer pool in one launch.

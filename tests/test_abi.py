@@ -95,6 +95,25 @@ def test_attention_rejects_bad_arguments_without_launching():
     assert call(split=f, ns=3, nr=2, mpr=2, ws=f, wsb=1 << 20) == _lib.TB_ERR_INVALID_ARG   # more split rows than rows
 
 
+def test_noalloc_attention_rejects_partials_beyond_its_scratch_without_launching():
+    L = _lib.lib()
+    f = ctypes.c_void_p(4096)
+    cap = 32 << 20
+    per_part = 32 * 130 * 4                    # Llama geometry: 32 heads x (128 + 2) floats
+    fits, over = cap // per_part, cap // per_part + 1
+
+    def call(tp, mpr=2, nw=2):
+        return L.tb_paged_attention_noalloc(f, 4096, f, 64, f, 4096, f, 4, f, nw, None, 0, f, 2, None, 0, mpr, 256,
+                                            tp, 32, 8, 128, 16, 0.0884, 2, None, 0, None, 0, None, None, None, 0,
+                                            None)
+
+    assert L.tb_paged_attention_workspace_bytes(fits, 32, 128) <= cap
+    assert call(over) == _lib.TB_ERR_SCRATCH
+    assert b"scratch" in L.tb_status_string(_lib.TB_ERR_SCRATCH)
+    assert call(10**6) == _lib.TB_ERR_SCRATCH
+    assert call(2, mpr=1, nw=0) == _lib.TB_OK                    # nothing to launch, no scratch needed
+
+
 def test_workspace_size_formula():
     L = _lib.lib()
     assert L.tb_paged_attention_workspace_bytes(10, 14, 64) == 10 * 14 * 66 * 4

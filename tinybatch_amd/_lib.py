@@ -19,6 +19,7 @@ TB_OK = 0
 TB_ERR_INVALID_ARG = -1
 TB_ERR_UNSUPPORTED = -2
 TB_ERR_LAUNCH = -3
+TB_ERR_SCRATCH = -4
 TB_ERR_INDEX = -5
 
 DTYPE_CODE = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
@@ -67,6 +68,12 @@ SIGNATURES = {
         c_vp, c_vp,                          # slot_mapping, row_part_offsets
         c_vp, c_i32, c_vp, c_i32, c_vp, c_i32,   # work items, tiles, split rows (+ capacities)
         c_vp,                                # counts
+    ]),
+    "tb_paged_attention_noalloc": (c_i32, [
+        c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_i32, c_vp, c_i32, c_vp, c_i32, c_vp, c_i32, c_vp, c_i32,
+        c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_f32, c_i32, c_vp, c_i64, c_vp, c_i64,
+        c_vp,                   # device_counts (no workspace arguments)
+        c_vp, c_vp, c_i32, c_vp,
     ]),
     "tb_block_copy": (c_i32, [c_vp, c_i32, c_i64, c_vp, c_vp, c_i32, c_i64, c_vp]),
     "tb_block_gather": (c_i32, [c_vp, c_i64, c_vp, c_i32, c_vp, c_i64, c_vp]),

@@ -233,6 +233,7 @@ extern "C" const char* tb_status_string(int32_t status) {
     case TB_ERR_UNSUPPORTED: return "unsupported shape or dtype (no compiled kernel)";
     case TB_ERR_LAUNCH: return "kernel launch failed";
     case TB_ERR_INDEX: return "block table too short for a context, or a block id outside the pool";
+    case TB_ERR_SCRATCH: return "the call needs more scratch than the allocation-free entry point holds";
     default: return "unknown status";
   }
 }

@@ -33,6 +33,9 @@
 // Positions >= the row's context are never loaded from the pool (stale slots
 // may hold any bits, NaN included): their scores are -inf, so p = 0, and what
 // stands in for their V rows is finite.
+#include <atomic>
+#include <mutex>
+
 #include "tb_common.h"
 
 namespace tb {
@@ -1222,6 +1225,38 @@ static int32_t paged_attention_impl(const void* q, int64_t q_row_stride, void* p
   TB_RETURN_LAUNCH_STATUS();
 }
 
+// ---- scratch of the allocation-free entry point ------------------------------
+// The split-row partials of tb_paged_attention_noalloc live in this array: one
+// copy per GPU, resident from the code object's load until the process ends.
+// Its device address is looked up once per device (hipGetSymbolAddress with
+// that device current) and only that address reaches a kernel or a copy.
+static __device__ __align__(256) char scratch[TB_NOALLOC_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+static std::atomic<void*> scratch_ptr[MAX_DEVICES];
+static std::mutex scratch_mu;
+
+static int32_t scratch_address(hipStream_t stream, void** ptr) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return TB_ERR_LAUNCH;
+  if (stream != nullptr) {   // the stream must belong to the current device, whose copy is used
+    hipDevice_t sdev = -1;
+    if (hipStreamGetDevice(stream, &sdev) != hipSuccess) return TB_ERR_INVALID_ARG;
+    if ((int)sdev != dev) return TB_ERR_INVALID_ARG;
+  }
+  void* p = scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    p = scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) return TB_ERR_LAUNCH;
+      scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *ptr = p;
+  return TB_OK;
+}
+
 }  // namespace tb
 
 extern "C" int32_t tb_paged_attention(const void* q, int64_t q_row_stride, void* pool,
@@ -1246,5 +1281,38 @@ extern "C" int32_t tb_paged_attention(const void* q, int64_t q_row_stride, void*
                                   max_parts_per_row, partition_tokens, total_partitions, num_heads,
                                   num_kv_heads, head_dim, block_size, scale, dtype, k_new, k_row_stride, v_new,
                                   v_row_stride, workspace, workspace_bytes, device_counts, rope_cos, rope_sin,
+                                  rope_max_position, stream);
+}
+
+extern "C" int32_t tb_paged_attention_noalloc(const void* q, int64_t q_row_stride, void* pool,
+                                              int64_t num_blocks, void* out, int64_t out_row_stride,
+                                              const int32_t* block_tables, int32_t max_blocks_per_seq,
+                                              const int32_t* work_items, int32_t num_work_items,
+                                              const int32_t* prefill_tiles, int32_t num_prefill_tiles,
+                                              const int32_t* row_part_offsets, int32_t num_rows,
+                                              const int32_t* split_rows, int32_t num_split_rows,
+                                              int32_t max_parts_per_row, int32_t partition_tokens,
+                                              int32_t total_partitions, int32_t num_heads,
+                                              int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                              float scale, int32_t dtype, const void* k_new,
+                                              int64_t k_row_stride, const void* v_new,
+                                              int64_t v_row_stride, const int32_t* device_counts,
+                                              const float* rope_cos, const float* rope_sin,
+                                              int32_t rope_max_position, hipStream_t stream) {
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+  if (max_parts_per_row > 1) {   // partials are only written for rows of more than one partition
+    const size_t need = tb_paged_attention_workspace_bytes(total_partitions, num_heads, head_dim);
+    if (need > (size_t)TB_NOALLOC_SCRATCH_BYTES) return TB_ERR_SCRATCH;
+    const int32_t st = tb::scratch_address(stream, &ws);
+    if (st != TB_OK) return st;
+    ws_bytes = TB_NOALLOC_SCRATCH_BYTES;
+  }
+  return tb::paged_attention_impl(q, q_row_stride, pool, num_blocks, out, out_row_stride, block_tables,
+                                  max_blocks_per_seq, work_items, num_work_items, prefill_tiles,
+                                  num_prefill_tiles, row_part_offsets, num_rows, split_rows, num_split_rows,
+                                  max_parts_per_row, partition_tokens, total_partitions, num_heads,
+                                  num_kv_heads, head_dim, block_size, scale, dtype, k_new, k_row_stride, v_new,
+                                  v_row_stride, ws, ws_bytes, device_counts, rope_cos, rope_sin,
                                   rope_max_position, stream);
 }

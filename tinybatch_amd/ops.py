@@ -161,7 +161,8 @@ def workspace_for(meta: StepMetadata, num_heads: int, head_dim: int,
 def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, num_heads: int,
                     scale: float | None = None, out: torch.Tensor | None = None,
                     k_new: torch.Tensor | None = None, v_new: torch.Tensor | None = None,
-                    workspace: torch.Tensor | None = None, rope: Rope | None = None) -> torch.Tensor:
+                    workspace: torch.Tensor | None = None, rope: Rope | None = None,
+                    noalloc: bool = False) -> torch.Tensor:
     """K2: paged attention of every query row of the step (reference model.py:130-147).
 
     q: [T, num_heads, head_dim]; returns out [T, num_heads * head_dim] in q's dtype
@@ -170,6 +171,9 @@ def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, 
     K/V (fused append); this requires a decode-only step. With ``rope`` q (and
     k_new) hold the projections before rotation: each row is rotated at its
     position row_ctx - 1 inside the kernels (model.py:72-80,125 folded in).
+    With ``noalloc`` the call allocates nothing on the device: ``out`` must be
+    given and the split-row partials go to the library's static per-GPU scratch
+    (tb_paged_attention_noalloc; calls that overlap in time on one GPU race).
     """
     nb, hkv, bs, d = _check_pool(pool)
     _lib.require_gpu_tensor("q", q)
@@ -184,6 +188,8 @@ def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, 
     if T != meta.num_tokens:
         raise ValueError(f"q has {T} rows, metadata describes {meta.num_tokens}")
     if out is None:
+        if noalloc:
+            raise ValueError("noalloc: pass the output buffer (out=...)")
         out = torch.empty(T, num_heads * d, device=q.device, dtype=q.dtype)
     else:
         _lib.require_gpu_tensor("out", out)
@@ -232,6 +238,11 @@ def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, 
     tail = (_ptr(meta.device_counts),
             None if rope is None else rope.cos.data_ptr(), None if rope is None else rope.sin.data_ptr(),
             0 if rope is None else rope.max_position, _lib.stream_handle(q.device))
+    if noalloc:
+        if workspace is not None:
+            raise ValueError("noalloc takes no workspace")
+        _lib.check(_lib.lib().tb_paged_attention_noalloc(*head, *tail), "tb_paged_attention_noalloc")
+        return out
     if workspace is None:
         workspace = workspace_for(meta, num_heads, d, q.device)
     ws = workspace
