@@ -400,6 +400,8 @@ def main() -> int:
     ap.add_argument("--workload", default="qwen-fp16-b64")
     ap.add_argument("--layers", type=int, default=0, help="layer pools to rotate (0 = auto)")
     ap.add_argument("--mode", choices=["fused", "split"], default="fused")
+    ap.add_argument("--kernel", choices=["decode", "items"], default="items",
+                    help="decode: persistent tile-stream kernel (tb_paged_decode); items: work-item kernel")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--cpu-reps", type=int, default=5)
     ap.add_argument("--cpu-budget", type=float, default=20.0)
@@ -463,7 +465,10 @@ def main() -> int:
     pools = [storage[l] for l in range(L)]
     P = args.partition or ops.partition_tokens(wl.dtype, wl.head_dim)
     meta = build_step_metadata(wl.positions, wl.seq_slices, wl.block_tables, wl.context_lens,
-                               block_size=wl.block_size, num_blocks=wl.num_blocks, partition_tokens=P).to(dev)
+                               block_size=wl.block_size, num_blocks=wl.num_blocks, partition_tokens=P)
+    decode_kernel = args.kernel == "decode" and ops.attach_decode_plan(
+        meta, num_heads=wl.num_heads, num_kv_heads=wl.num_kv_heads, head_dim=wl.head_dim, dtype=wl.dtype, device=dev)
+    meta.to(dev)
     q = wl.q.to(dev)
     k = wl.k_new.to(dev)
     v = wl.v_new.to(dev)
@@ -490,6 +495,10 @@ def main() -> int:
     per_launch_ms = ms / L
     achieved = bytes_layer["total"] / (per_launch_ms * 1e-3) / 1e9
     traffic = load_traffic(wl.name, args.mode)
+    if decode_kernel:
+        viol = int(ops.decode_device(dev).violations.item())
+        if viol:
+            raise RuntimeError(f"{viol} units merged across XCDs: the workgroup placement assumption failed")
 
     cpu = None
     if not args.no_cpu:
@@ -511,8 +520,12 @@ def main() -> int:
         e2e = run_e2e(dev, 1)
         _log(f"e2e: {e2e['tok_s']} tok/s, TTFT mean {e2e['ttft_mean_ms']} ms, p99 {e2e['ttft_p99_ms']} ms")
 
-    attn = "paged_attn_valu_kernel" if wl.dtype == torch.float32 else "paged_attn_mfma_kernel"
-    kernel = attn + " + combine_partials_kernel" + ("" if fused else " + kv_append_kernel")
+    if decode_kernel:
+        kernel = "paged_decode_kernel" + ("" if ops.decode_device(dev).merge_in_kernel else " + decode_combine_kernel")
+    else:
+        attn = "paged_attn_valu_kernel" if wl.dtype == torch.float32 else "paged_attn_mfma_kernel"
+        kernel = attn + " + combine_partials_kernel"
+    kernel += "" if fused else " + kv_append_kernel"
     line = {
         "metric": METRIC,
         "value": round(gbs, 2),
@@ -531,7 +544,8 @@ def main() -> int:
             "batch": wl.batch, "num_heads": wl.num_heads, "num_kv_heads": wl.num_kv_heads,
             "head_dim": wl.head_dim, "block_size": wl.block_size, "num_blocks": wl.num_blocks,
             "mean_context": round(sum(wl.context_lens) / wl.batch, 1), "layers": L,
-            "mode": args.mode, "graph": graph, "partition_tokens": P,
+            "mode": args.mode, "graph": graph, "kernel": "decode" if decode_kernel else "items",
+            "partition_tokens": P,
             "bytes_per_layer_step": bytes_layer["total"],
         },
         "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),

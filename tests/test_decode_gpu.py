@@ -1,0 +1,176 @@
+"""The decode kernel (tb_paged_decode: persistent workgroups over 16-position
+tiles, partials merged inside the launch) against the oracle, through the C ABI.
+
+Bars: appended rows bit-exact; attention rtol = atol = 2e-2 at fp16 / bf16
+against the oracle in the same dtype. Also: the same bits from the in-launch
+merge and the after-launch combine kernel, from repeated calls, and from
+fused RoPE against rotating first; no unit ever merged across XCDs."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import reference_path as ref
+from tinybatch_amd import layer_ops, ops
+from tinybatch_amd.metadata import attach_decode_plan as attach_host, build_step_metadata
+from tinybatch_amd.model import rope_tables
+from tinybatch_amd.workloads import make_decode_workload
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+TOL = dict(atol=2e-2, rtol=2e-2)
+
+
+def _bits(t):
+    return t.contiguous().view(torch.int16)
+
+
+def decode_meta(ctx, tables, NB, BS, Hq, Hkv, D, dtype, merge=None):
+    B = len(ctx)
+    meta = build_step_metadata([c - 1 for c in ctx], [(b, b + 1) for b in range(B)], tables, ctx, block_size=BS,
+                               num_blocks=NB, partition_tokens=ops.partition_tokens(dtype, D))
+    if merge is None:
+        assert ops.attach_decode_plan(meta, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, dtype=dtype, device=DEV)
+    else:   # the device's plan, its partials merged inside the launch or by the combine kernel
+        d = ops.decode_device(DEV)
+        assert attach_host(meta, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, dtype=dtype, workgroups=d.workgroups,
+                           num_xcds=d.num_xcds, merge_in_kernel=merge)
+    return meta.to(DEV)
+
+
+def case(seed, B, Hq, Hkv, D, BS, dtype, ctx=None, nan_stale=True):
+    g = torch.Generator().manual_seed(seed)
+    if ctx is None:
+        ctx = torch.randint(1, 2500, (B,), generator=g).tolist()
+    need = [(c + BS - 1) // BS for c in ctx]
+    NB = sum(need) + 5
+    pool = torch.randn(NB, 2, Hkv, BS, D, generator=g).to(dtype)
+    perm = torch.randperm(NB, generator=g).tolist()
+    tables, at = [], 0
+    for n in need:
+        tables.append(perm[at:at + n])
+        at += n
+    if nan_stale:   # positions past each context, and unused blocks, hold NaN
+        for t, c in zip(tables, ctx):
+            if c % BS:
+                pool[t[-1], :, :, c % BS:] = float("nan")
+        for blk in perm[at:]:
+            pool[blk] = float("nan")
+    q = torch.randn(len(ctx), Hq, D, generator=g).to(dtype)
+    k = torch.randn(len(ctx), Hkv, D, generator=g).to(dtype)
+    v = torch.randn(len(ctx), Hkv, D, generator=g).to(dtype)
+    return dict(pool=pool, tables=tables, ctx=ctx, q=q, k=k, v=v, NB=NB, BS=BS, Hq=Hq, Hkv=Hkv, D=D, dtype=dtype)
+
+
+def oracle(c):
+    pool = c["pool"].clone()
+    out = ref.decode_step(pool, c["q"], c["k"], c["v"], [x - 1 for x in c["ctx"]], c["tables"], c["Hq"], c["Hkv"],
+                          c["BS"])
+    return out, pool
+
+
+def run(c, fused=True, merge=None):
+    meta = decode_meta(c["ctx"], c["tables"], c["NB"], c["BS"], c["Hq"], c["Hkv"], c["D"], c["dtype"], merge)
+    pool = c["pool"].to(DEV)
+    q, k, v = c["q"].to(DEV), c["k"].to(DEV), c["v"].to(DEV)
+    if fused:
+        out = ops.paged_attention(q, pool, meta, num_heads=c["Hq"], k_new=k, v_new=v)
+    else:
+        ops.kv_append(pool, k, v, meta.slot_mapping)
+        out = ops.paged_attention(q, pool, meta, num_heads=c["Hq"])
+    torch.cuda.synchronize()
+    return out.cpu(), pool.cpu(), meta
+
+
+def check(c, fused=True, merge=None):
+    want, want_pool = oracle(c)
+    got, pool, meta = run(c, fused, merge)
+    assert torch.equal(_bits(pool), _bits(want_pool)), "pool differs (append)"
+    torch.testing.assert_close(got.float(), want.float(), **TOL)
+    return got, meta
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("fused", [True, False])
+def test_headline_shape(dtype, fused):
+    wl = make_decode_workload("qwen-fp16-b64")
+    c = dict(pool=wl.pool.to(dtype), tables=wl.block_tables, ctx=wl.context_lens, q=wl.q.to(dtype),
+             k=wl.k_new.to(dtype), v=wl.v_new.to(dtype), NB=wl.num_blocks, BS=16, Hq=14, Hkv=2, D=64, dtype=dtype)
+    _, meta = check(c, fused)
+    assert meta.decode_pieces > 0                  # units cut over workgroups: partials merged
+
+
+def test_llama_geometry_subset():
+    wl = make_decode_workload("llama-bf16-b256", batch=8)
+    c = dict(pool=wl.pool, tables=wl.block_tables, ctx=wl.context_lens, q=wl.q, k=wl.k_new, v=wl.v_new,
+             NB=wl.num_blocks, BS=16, Hq=32, Hkv=8, D=128, dtype=torch.bfloat16)
+    check(c, fused=True)
+
+
+@pytest.mark.parametrize("Hq,Hkv,D", [(14, 2, 64), (8, 8, 64), (16, 2, 64), (4, 2, 128), (32, 8, 128), (7, 7, 128)])
+@pytest.mark.parametrize("BS", [16, 64])
+def test_geometries_and_block_sizes(Hq, Hkv, D, BS):
+    c = case(Hq * 100 + BS, 21, Hq, Hkv, D, BS, torch.bfloat16)
+    check(c, fused=True)
+
+
+def test_short_and_block_multiple_contexts():
+    ctx = [1, 2, 15, 16, 17, 31, 32, 33, 48, 64, 65, 1, 700, 16 * 37]
+    for BS in (16, 32):
+        check(case(7, len(ctx), 14, 2, 64, BS, torch.float16, ctx=ctx), fused=True)
+        check(case(8, len(ctx), 14, 2, 64, BS, torch.float16, ctx=ctx), fused=False)
+
+
+def test_one_long_sequence_over_many_workgroups():
+    c = case(9, 1, 14, 2, 64, 16, torch.bfloat16, ctx=[60000])
+    _, meta = check(c, fused=True)
+    assert meta.decode_pieces > 8
+
+
+def test_in_launch_merge_and_combine_kernel_give_the_same_bits():
+    c = case(10, 40, 14, 2, 64, 16, torch.bfloat16)
+    a, _ = check(c, fused=True, merge=True)
+    b, _ = check(c, fused=True, merge=False)
+    assert torch.equal(_bits(a), _bits(b))
+
+
+def test_repeated_calls_same_bits_and_no_cross_xcd_merges():
+    c = case(11, 64, 14, 2, 64, 16, torch.float16, nan_stale=False)
+    meta = decode_meta(c["ctx"], c["tables"], c["NB"], 16, 14, 2, 64, torch.float16)
+    pool = c["pool"].to(DEV)
+    q = c["q"].to(DEV)
+    outs = [ops.paged_attention(q, pool, meta, num_heads=14).clone() for _ in range(3)]
+    small = case(12, 3, 14, 2, 64, 16, torch.float16)     # a smaller step between: counters reset
+    check(small, fused=False)
+    outs.append(ops.paged_attention(q, pool, meta, num_heads=14))
+    torch.cuda.synchronize()
+    assert all(torch.equal(_bits(o), _bits(outs[0])) for o in outs[1:])
+    assert int(ops.decode_device(DEV).violations.item()) == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fused_rope_equals_rotating_first(dtype):
+    c = case(13, 24, 14, 2, 64, 16, dtype, nan_stale=False)
+    cos, sin = rope_tables(64, 1e6, 8192, DEV)
+    rope = ops.Rope(cos, sin)
+    pos = torch.tensor([x - 1 for x in c["ctx"]], dtype=torch.int64, device=DEV)
+    meta = decode_meta(c["ctx"], c["tables"], c["NB"], 16, 14, 2, 64, dtype)
+    q, k, v = c["q"].to(DEV), c["k"].to(DEV), c["v"].to(DEV)
+    pool_a = c["pool"].to(DEV)
+    out_a = ops.paged_attention(q, pool_a, meta, num_heads=14, k_new=k, v_new=v, rope=rope)
+    # rotate first (the separate RoPE kernel), then the same call without rope
+    qkv = torch.cat([q.reshape(len(c["ctx"]), -1), k.reshape(len(c["ctx"]), -1), v.reshape(len(c["ctx"]), -1)], 1)
+    qr, kr = layer_ops.rope_qk(qkv.contiguous(), pos, cos, sin, 14, 2, 64)
+    pool_b = c["pool"].to(DEV)
+    out_b = ops.paged_attention(qr.contiguous(), pool_b, meta, num_heads=14, k_new=kr.contiguous(), v_new=v)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(pool_a), _bits(pool_b))
+    assert torch.equal(_bits(out_a), _bits(out_b))
+
+
+def test_shared_slot_refused_by_the_fused_append():
+    c = case(14, 3, 14, 2, 64, 16, torch.float16, ctx=[20, 40, 36], nan_stale=False)
+    c["tables"][2][2] = c["tables"][0][1]                     # rows 0 and 2 write one slot
+    meta = decode_meta(c["ctx"], c["tables"], c["NB"], 16, 14, 2, 64, torch.float16)
+    with pytest.raises(ValueError, match="one pool slot"):
+        ops.paged_attention(c["q"].to(DEV), c["pool"].to(DEV), meta, num_heads=14, k_new=c["k"].to(DEV),
+                            v_new=c["v"].to(DEV))

@@ -267,3 +267,131 @@ extern "C" int32_t tb_build_step_metadata(const int32_t* query_start_loc, int32_
   }
   return TB_OK;
 }
+
+// ---------------------------------------------------------------------------
+// Decode plan of tb_paged_decode (decode-only steps: row b = sequence b, one new
+// token each). Units are (sequence, kv head) pairs; a unit's positions are cut
+// into tiles of 16. Units are assigned to XCDs by longest-first bin packing on
+// their tile counts; each XCD's tiles (its units back to back) are split evenly
+// over the workgroups that run on it (workgroup g runs on XCD g % num_xcds), and
+// each workgroup's range is cut at unit boundaries into segments. A unit spread
+// over several workgroups leaves one partial per segment, all on one XCD.
+//
+// Layout (int32): [0] workgroups G, [1] segments S, [2] units U, [3] pieces,
+// [4] num_xcds, [5..7] 0; then wg_first [G + 1] (segment index of each
+// workgroup's first segment), padded to 4; segments [S][4] = (unit, first tile,
+// end tile, piece slot or -1 for a unit held whole by one segment); units [U][2]
+// = (pieces, first slot).
+namespace {
+constexpr int DECODE_TILE = 16;
+
+int64_t plan_ints(int64_t G, int64_t S, int64_t U) {
+  const int64_t wg = (G + 1 + 3) / 4 * 4;
+  return 8 + wg + 4 * S + 2 * U;
+}
+}  // namespace
+
+extern "C" size_t tb_decode_plan_bytes(int32_t num_seqs, int32_t num_kv_heads, int32_t workgroups) {
+  if (num_seqs < 0 || num_kv_heads <= 0 || workgroups <= 0) return 0;
+  const int64_t U = (int64_t)num_seqs * num_kv_heads;
+  return (size_t)plan_ints(workgroups, U + workgroups, U) * sizeof(int32_t);
+}
+
+extern "C" int32_t tb_build_decode_plan(const int32_t* context_lens, int32_t num_seqs, int32_t num_kv_heads,
+                                        int32_t workgroups, int32_t num_xcds, int32_t max_tiles_per_wg,
+                                        int32_t max_segments_per_wg, int32_t* plan, size_t plan_bytes) {
+  if (num_seqs < 0 || num_kv_heads <= 0 || workgroups <= 0 || num_xcds <= 0 || num_xcds > 64 || !plan)
+    return TB_ERR_INVALID_ARG;
+  if (workgroups % num_xcds || max_tiles_per_wg <= 0 || max_segments_per_wg <= 0) return TB_ERR_INVALID_ARG;
+  if (num_seqs > 0 && !context_lens) return TB_ERR_INVALID_ARG;
+  if (plan_bytes < tb_decode_plan_bytes(num_seqs, num_kv_heads, workgroups)) return TB_ERR_INVALID_ARG;
+  if ((int64_t)num_seqs * num_kv_heads >= INDEX_LIMIT) return TB_ERR_INVALID_ARG;
+  const int32_t U = num_seqs * num_kv_heads, G = workgroups, NX = num_xcds, per = G / NX;
+  for (int b = 0; b < num_seqs; ++b)
+    if (context_lens[b] < 1) return TB_ERR_INVALID_ARG;
+  auto tiles = [&](int u) { return (context_lens[u / num_kv_heads] + DECODE_TILE - 1) / DECODE_TILE; };
+  int32_t* const wg_first = plan + 8;
+  int32_t* const segs = wg_first + (G + 1 + 3) / 4 * 4;
+  int32_t* const units = segs + 4 * ((int64_t)U + G);   // each unit's XCD, past every segment the plan can hold
+
+  // 1. XCDs: longest unit first (stable), onto the least loaded XCD (lowest index among equals)
+  int64_t load[64];
+  for (int x = 0; x < NX; ++x) load[x] = 0;
+  int32_t max_t = 0;
+  for (int u = 0; u < U; ++u) max_t = tiles(u) > max_t ? tiles(u) : max_t;
+  for (int t = max_t; t >= 1; --t)
+    for (int u = 0; u < U; ++u) {
+      if (tiles(u) != t) continue;
+      int best = 0;
+      for (int x = 1; x < NX; ++x)
+        if (load[x] < load[best]) best = x;
+      units[2 * u] = best;
+      load[best] += t;
+    }
+
+  // 2. segments in workgroup order: workgroup g = j * NX + x takes the j-th of XCD x's
+  // `per` even ranges of its tiles (its units in unit order, back to back)
+  int32_t cur_u[64], cur_t[64];
+  auto next_unit = [&](int x, int from) {
+    for (int v = from; v < U; ++v)
+      if (units[2 * v] == x) return v;
+    return U;
+  };
+  for (int x = 0; x < NX; ++x) {
+    cur_u[x] = next_unit(x, 0);
+    cur_t[x] = 0;
+  }
+  int64_t S = 0;
+  for (int g = 0; g < G; ++g) {
+    const int x = g % NX, j = g / NX;
+    const int64_t a = load[x] * j / per, b = load[x] * (j + 1) / per;
+    if (b - a > max_tiles_per_wg) return TB_ERR_UNSUPPORTED;
+    wg_first[g] = (int32_t)S;
+    int64_t left = b - a;
+    int nseg = 0;
+    while (left > 0) {
+      const int u = cur_u[x];
+      const int take = (int)(tiles(u) - cur_t[x] < left ? tiles(u) - cur_t[x] : left);
+      int32_t* sg = segs + 4 * S++;
+      sg[0] = u;
+      sg[1] = cur_t[x];
+      sg[2] = cur_t[x] + take;
+      sg[3] = 0;
+      ++nseg;
+      cur_t[x] += take;
+      left -= take;
+      if (cur_t[x] == tiles(u)) {
+        cur_u[x] = next_unit(x, u + 1);
+        cur_t[x] = 0;
+      }
+    }
+    if (nseg > max_segments_per_wg) return TB_ERR_UNSUPPORTED;
+  }
+  wg_first[G] = (int32_t)S;
+  for (int i = G + 1; i < (G + 1 + 3) / 4 * 4; ++i) wg_first[i] = 0;
+
+  // 3. pieces: a unit cut into several segments leaves one partial per segment. The
+  // unit records follow the S segments (the XCD assignment above is no longer needed).
+  int32_t* const rec = segs + 4 * S;
+  for (int u = 0; u < U; ++u) rec[2 * u] = rec[2 * u + 1] = 0;
+  for (int64_t i = 0; i < S; ++i) ++rec[2 * segs[4 * i]];
+  int32_t pieces = 0;
+  for (int u = 0; u < U; ++u) {
+    if (rec[2 * u] > 255) return TB_ERR_UNSUPPORTED;   // arrival counts are 8-bit fields
+    rec[2 * u + 1] = rec[2 * u] > 1 ? pieces : -1;
+    if (rec[2 * u] > 1) pieces += rec[2 * u];
+  }
+  for (int64_t i = 0; i < S; ++i) {
+    const int u = segs[4 * i];
+    segs[4 * i + 3] = rec[2 * u] > 1 ? rec[2 * u + 1]++ : -1;
+  }
+  for (int u = 0; u < U; ++u)
+    if (rec[2 * u] > 1) rec[2 * u + 1] -= rec[2 * u];
+  plan[0] = G;
+  plan[1] = (int32_t)S;
+  plan[2] = U;
+  plan[3] = pieces;
+  plan[4] = NX;
+  plan[5] = plan[6] = plan[7] = 0;
+  return TB_OK;
+}

@@ -76,11 +76,23 @@ class StepMetadata:
     split_rows: torch.Tensor | None = None
     # set for capacity-sized (graph) metadata: {work items, split rows, tiles} on the device
     device_counts: torch.Tensor | None = None
+    # decode plan (tb_paged_decode): set by attach_decode_plan for decode-only steps
+    rows_are_seqs: bool = False  # decode-only with row b = sequence b (the decode kernel's layout)
+    decode_plan_np: np.ndarray | None = None
+    context_lens_np: np.ndarray | None = None
+    decode_workgroups: int = 0
+    decode_pieces: int = 0
+    decode_units: int = 0
+    decode_merge_in_kernel: bool = False
+    decode_plan: torch.Tensor | None = None
+    context_lens: torch.Tensor | None = None
 
     def to(self, device: torch.device) -> "StepMetadata":
         """Upload every array with one host-to-device copy (views into one buffer)."""
         parts = [self.slot_mapping_np, self.block_tables_np.reshape(-1), self.work_np.reshape(-1),
                  self.row_part_off_np, self.prefill_tiles_np.reshape(-1), self.split_rows_np.reshape(-1)]
+        if self.decode_plan_np is not None:
+            parts += [self.context_lens_np, self.decode_plan_np]
         sizes = [pad4(p.size) for p in parts]
         host = np.zeros(sum(sizes), dtype=np.int32)
         offs = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
@@ -97,6 +109,9 @@ class StepMetadata:
         self.row_part_off = buf.narrow(0, int(offs[3]), parts[3].size)
         self.prefill_tiles = buf.narrow(0, int(offs[4]), parts[4].size).view(-1, 4)
         self.split_rows = buf.narrow(0, int(offs[5]), parts[5].size).view(-1, 4)
+        if self.decode_plan_np is not None:
+            self.context_lens = buf.narrow(0, int(offs[6]), parts[6].size)
+            self.decode_plan = buf.narrow(0, int(offs[7]), parts[7].size)
         return self
 
 
@@ -281,6 +296,7 @@ def build_step_metadata(positions, seq_slices, block_tables, context_lens, *, bl
         max_blocks_per_seq=max_nb, num_work_items=W, total_partitions=total_parts,
         max_parts_per_row=int(nparts_by_row.max()) if T else 0,
         decode_only=bool(B) and bool(np.all(qlens == 1)),
+        rows_are_seqs=bool(B) and T == B and bool(np.all(starts == np.arange(B))) and bool(np.all(qlens == 1)),
         rows_per_item=int(rows_per_item),
         num_prefill_tiles=int(tiles_np.shape[0]),
         num_split_rows=int(split_ids.size),
@@ -388,4 +404,71 @@ def pack_decode_step(h: np.ndarray, offs: np.ndarray, Bp: int, max_nb: int, cont
     rec[:, 2] = nparts[split]
     rec[:, 3] = 0
     h[o[5]:o[5] + 4] = (W, S, 0, 0)
+    return True
+
+
+# ---- decode plans (tb_paged_decode) ---------------------------------------------
+def decode_limits(num_heads: int, num_kv_heads: int, head_dim: int):
+    """(max tiles, max segments, waves) per workgroup of the decode kernel for this
+    geometry, or None when the kernel does not serve it."""
+    import ctypes
+
+    from . import _lib
+
+    t, sg, w = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+    st = _lib.lib().tb_decode_limits(num_heads, num_kv_heads, head_dim, ctypes.byref(t), ctypes.byref(sg),
+                                     ctypes.byref(w))
+    return (t.value, sg.value, w.value) if st == 0 else None
+
+
+def build_decode_plan(context_lens, num_heads: int, num_kv_heads: int, head_dim: int, workgroups: int,
+                      num_xcds: int) -> tuple[np.ndarray, int] | None:
+    """tb_build_decode_plan for a decode step (row b = sequence b with context_lens[b]
+    positions): the int32 plan and the workgroup count it needs, starting from
+    ``workgroups`` and doubling while a workgroup's share exceeds its LDS areas. None
+    when the geometry is not served by the decode kernel."""
+    import ctypes
+
+    from . import _lib
+
+    lim = decode_limits(num_heads, num_kv_heads, head_dim)
+    if lim is None:
+        return None
+    tmax, smax, _ = lim
+    ctx = np.ascontiguousarray(np.asarray(context_lens, dtype=np.int32).reshape(-1))
+    B = int(ctx.size)
+    L = _lib.lib()
+    G = int(workgroups)
+    for _ in range(8):
+        nbytes = int(L.tb_decode_plan_bytes(B, num_kv_heads, G))
+        plan = np.zeros(nbytes // 4, dtype=np.int32)
+        st = L.tb_build_decode_plan(ctx.ctypes.data_as(ctypes.c_void_p), B, num_kv_heads, G, num_xcds, tmax, smax,
+                                    plan.ctypes.data_as(ctypes.c_void_p), nbytes)
+        if st == 0:
+            return plan, G
+        if st != _lib.TB_ERR_UNSUPPORTED:
+            _lib.check(st, "tb_build_decode_plan")
+        G *= 2
+    return None
+
+
+def attach_decode_plan(meta: StepMetadata, *, num_heads: int, num_kv_heads: int, head_dim: int,
+                       dtype: torch.dtype, workgroups: int, num_xcds: int, merge_in_kernel: bool) -> bool:
+    """Give a decode-only step (row b = sequence b) the plan of the decode kernel, to be
+    uploaded with the rest of its metadata by ``meta.to``. Returns whether it applies:
+    16-bit rows, head_dim 64 / 128, at most 8 query heads per kv head, blocks of >= 16."""
+    if (not meta.rows_are_seqs or dtype not in (torch.float16, torch.bfloat16) or meta.block_size < 16
+            or meta.device_buffer is not None):
+        return False
+    ctx = meta.row_ctx_np[:meta.num_seqs].astype(np.int32)
+    got = build_decode_plan(ctx, num_heads, num_kv_heads, head_dim, workgroups, num_xcds)
+    if got is None:
+        return False
+    plan, G = got
+    meta.decode_plan_np = plan
+    meta.context_lens_np = ctx
+    meta.decode_workgroups = G
+    meta.decode_units = int(plan[2])
+    meta.decode_pieces = int(plan[3])
+    meta.decode_merge_in_kernel = bool(merge_in_kernel)
     return True

@@ -158,6 +158,147 @@ def workspace_for(meta: StepMetadata, num_heads: int, head_dim: int,
     return ws
 
 
+class DecodeDevice:
+    """Launch facts of the decode kernel on one GPU: one persistent workgroup per CU,
+    and the XCD count under which partials merge inside the launch. The XCD count is
+    the CU count / 32 (the CUs of one XCD) and is used only if a probe launch shows
+    workgroup g running on XCD g mod that count, with distinct XCDs in between;
+    otherwise the plan ignores XCDs and a second kernel merges the partials."""
+
+    def __init__(self, device: torch.device):
+        props = torch.cuda.get_device_properties(device)
+        cus = int(props.multi_processor_count)
+        self.device = device
+        self.workgroups = cus
+        nx = cus // 32 if cus % 32 == 0 and cus >= 32 else 1
+        self.num_xcds, self.merge_in_kernel = self._verify(device, cus, nx)
+        self.violations = torch.zeros(1, dtype=torch.int32, device=device)
+
+    @staticmethod
+    def _verify(device, cus: int, nx: int) -> tuple[int, bool]:
+        g = 8 * cus
+        out = torch.full((g,), -1, dtype=torch.int32, device=device)
+        with torch.cuda.device(device):
+            _lib.check(_lib.lib().tb_decode_xcc_probe(g, out.data_ptr(), _lib.stream_handle(device)),
+                       "tb_decode_xcc_probe")
+        x = out.cpu().numpy()
+        if nx <= 1:
+            return 1, bool(np.all(x == x[0]))
+        ok = len(set(x[:nx].tolist())) == nx and bool(np.all(x == np.tile(x[:nx], g // nx)))
+        return (nx, True) if ok else (1, False)
+
+
+_DECODE_DEVICES: dict[int, DecodeDevice] = {}
+_DECODE_WORKSPACES: dict[tuple[int, int], "DecodeBuffers"] = {}
+
+
+def decode_device(device: torch.device) -> DecodeDevice:
+    """The device's DecodeDevice (built on first use: a probe launch and a synchronisation,
+    so not while a graph is being captured)."""
+    key = device.index if device.index is not None else torch.cuda.current_device()
+    d = _DECODE_DEVICES.get(key)
+    if d is None:
+        d = _DECODE_DEVICES[key] = DecodeDevice(torch.device("cuda", key))
+    return d
+
+
+def attach_decode_plan(meta: StepMetadata, *, num_heads: int, num_kv_heads: int, head_dim: int,
+                       dtype: torch.dtype, device: torch.device) -> bool:
+    """metadata.attach_decode_plan with this device's workgroups and XCDs."""
+    from .metadata import attach_decode_plan as attach
+
+    d = decode_device(device)
+    return attach(meta, num_heads=num_heads, num_kv_heads=num_kv_heads, head_dim=head_dim, dtype=dtype,
+                  workgroups=d.workgroups, num_xcds=d.num_xcds, merge_in_kernel=d.merge_in_kernel)
+
+
+def decode_workspace_bytes(meta: StepMetadata, num_heads: int, num_kv_heads: int, head_dim: int) -> int:
+    return int(_lib.lib().tb_paged_decode_workspace_bytes(meta.decode_pieces, num_heads, num_kv_heads, head_dim))
+
+
+class DecodeBuffers:
+    """The decode kernel's partials workspace and its arrival counters (128 bytes per
+    unit, zero between calls: every call leaves them zero)."""
+
+    def __init__(self, device: torch.device, piece_bytes: int, units: int):
+        self.pieces = torch.empty(max(piece_bytes, 1 << 16), dtype=torch.uint8, device=device)
+        self.units = max(units, 256)
+        self.arrivals = torch.zeros(self.units * 16, dtype=torch.int64, device=device)
+
+
+def decode_buffers(device: torch.device, piece_bytes: int, units: int) -> DecodeBuffers:
+    """Cached per device and stream (calls on one stream are ordered; calls on two
+    streams must not share counters); grown on demand, new counters zeroed."""
+    key = (device.index if device.index is not None else torch.cuda.current_device(),
+           torch.cuda.current_stream(device).cuda_stream)
+    b = _DECODE_WORKSPACES.get(key)
+    if b is None or b.pieces.numel() < piece_bytes or b.units < units:
+        b = DecodeBuffers(device, max(piece_bytes, 0 if b is None else b.pieces.numel()),
+                          max(units, 0 if b is None else b.units))
+        _DECODE_WORKSPACES[key] = b
+    return b
+
+
+def paged_decode(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, num_heads: int,
+                 scale: float | None = None, out: torch.Tensor | None = None,
+                 k_new: torch.Tensor | None = None, v_new: torch.Tensor | None = None,
+                 workspace: "DecodeBuffers | None" = None, rope: Rope | None = None) -> torch.Tensor:
+    """tb_paged_decode: the decode kernel for a step whose metadata carries a decode plan
+    (attach_decode_plan). Arguments and result as paged_attention; ``workspace`` is a
+    DecodeBuffers (by default one cached per device and stream)."""
+    nb, hkv, bs, d = _check_pool(pool)
+    if meta.decode_plan is None:
+        raise ValueError("metadata has no uploaded decode plan (attach_decode_plan, then meta.to(device))")
+    _lib.require_gpu_tensor("q", q)
+    if q.dtype != pool.dtype or q.dtype not in (torch.float16, torch.bfloat16):
+        raise TypeError("the decode kernel takes fp16 / bf16 q in the pool dtype")
+    qs = _rows_view("q", q, num_heads, d)
+    B = meta.num_seqs
+    if q.shape[0] != B:
+        raise ValueError(f"q has {q.shape[0]} rows, the decode step {B}")
+    if out is None:
+        out = torch.empty(B, num_heads * d, device=q.device, dtype=q.dtype)
+    _lib.require_gpu_tensor("out", out)
+    if out.dtype != q.dtype or out.shape[0] != B:
+        raise ValueError("out must match q's dtype and row count")
+    os_ = _rows_view("out", out, num_heads, d)
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    if rope is not None:
+        rope.check(d, q.device)
+    ksp = vsp = None
+    ks = vs = 0
+    if k_new is not None or v_new is not None:
+        if k_new is None or v_new is None:
+            raise ValueError("k_new and v_new go together")
+        sm = meta.slot_mapping_np
+        if sm.size and np.any(sm[:B] < 0):
+            raise ValueError("two decode rows write one pool slot; the fused append cannot serve the "
+                             "step: append with kv_append, then call paged_attention without k_new")
+        for name, t in (("k_new", k_new), ("v_new", v_new)):
+            _lib.require_gpu_tensor(name, t)
+            if t.dtype != pool.dtype or t.shape[0] != B:
+                raise ValueError(f"{name} must be [B, kv_heads, head_dim] in the pool dtype")
+        ks = _rows_view("k_new", k_new, hkv, d)
+        vs = _rows_view("v_new", v_new, hkv, d)
+        ksp, vsp = k_new.data_ptr(), v_new.data_ptr()
+    dev = decode_device(q.device)
+    need = decode_workspace_bytes(meta, num_heads, hkv, d)
+    bufs = workspace if workspace is not None else decode_buffers(q.device, need, meta.decode_units)
+    if bufs.pieces.numel() < need or bufs.units < meta.decode_units:
+        raise ValueError("decode buffers too small for the step")
+    st = _lib.lib().tb_paged_decode(
+        q.data_ptr(), qs, pool.data_ptr(), nb, out.data_ptr(), os_, meta.block_tables.data_ptr(),
+        meta.max_blocks_per_seq, meta.context_lens.data_ptr(), B, meta.decode_plan.data_ptr(),
+        meta.decode_workgroups, meta.decode_units, num_heads, hkv, d, bs, float(scale), _lib.DTYPE_CODE[q.dtype],
+        ksp, ks, vsp, vs, bufs.pieces.data_ptr(), bufs.pieces.numel(), meta.decode_pieces,
+        bufs.arrivals.data_ptr(), bufs.units, int(meta.decode_merge_in_kernel), dev.violations.data_ptr(),
+        None if rope is None else rope.cos.data_ptr(), None if rope is None else rope.sin.data_ptr(),
+        0 if rope is None else rope.max_position, _lib.stream_handle(q.device))
+    _lib.check(st, "tb_paged_decode")
+    return out
+
+
 def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, num_heads: int,
                     scale: float | None = None, out: torch.Tensor | None = None,
                     k_new: torch.Tensor | None = None, v_new: torch.Tensor | None = None,
@@ -175,6 +316,9 @@ def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, 
     given and the split-row partials go to the library's static per-GPU scratch
     (tb_paged_attention_noalloc; calls that overlap in time on one GPU race).
     """
+    if meta.decode_plan is not None and not noalloc and q.dtype in (torch.float16, torch.bfloat16):
+        return paged_decode(q, pool, meta, num_heads=num_heads, scale=scale, out=out, k_new=k_new, v_new=v_new,
+                            rope=rope)
     nb, hkv, bs, d = _check_pool(pool)
     _lib.require_gpu_tensor("q", q)
     if q.dtype != pool.dtype:
