@@ -272,33 +272,30 @@ int32_t tb_paged_attention_noalloc(const void* q, int64_t q_row_stride,
  * fp16 / bf16, head_dim 64 or 128, num_heads / num_kv_heads <= 8, block_size a
  * power of two >= 16 (TB_ERR_UNSUPPORTED otherwise: use tb_paged_attention).
  *
- * The work is a plan (tb_build_decode_plan) of persistent workgroups that each
- * stream an equal share of the 16-position tiles of all (sequence, kv head)
- * units; a unit cut over several workgroups is merged by the one finishing
- * last. plan_workgroups is the grid size the plan was built for.
- *   context_lens: device int32 [num_seqs] (the values the plan was built from)
- *   block_tables: device int32 [num_seqs][max_blocks_per_seq]
+ * The work is a plan (tb_build_decode_plan, which also carries the step's
+ * context lengths and the pool block of every tile) for plan_workgroups
+ * persistent workgroups whose waves each stream an equal share of the
+ * 16-position tiles of all (sequence, kv head) units; a unit cut over several
+ * waves is merged by the one finishing last.
  *   workspace: >= tb_paged_decode_workspace_bytes(max_pieces, ...) bytes of
  *     device memory, 128-byte aligned, for the partials (max_pieces >= the
  *     plan's pieces; max_units >= num_seqs * num_kv_heads).
  *   merge_in_kernel = 1: a unit's partials are merged inside the launch by the
- *     workgroup whose partial arrives last, counted in `arrivals`: device
- *     memory of arrival_units * 128 bytes (arrival_units >= max_units,
- *     128-byte aligned), zero before the first call (allocate it zeroed) and
- *     left zero by every call, so one buffer serves every later call. It
- *     assumes that workgroup g runs on XCD g % num_xcds of the plan (verify
- *     with tb_decode_xcc_probe); `violations` (device uint32) is incremented
- *     for every unit whose pieces ran on more than one XCD (its output may then
- *     be wrong). merge_in_kernel = 0: a second kernel merges the partials
+ *     wave whose partial arrives last, counted in `arrivals`: device memory of
+ *     arrival_units * 128 bytes (arrival_units >= max_units, 128-byte
+ *     aligned), zero before the first call (allocate it zeroed) and left zero
+ *     by every call, so one buffer serves every later call. It assumes that
+ *     workgroup g runs on XCD g % num_xcds of the plan (verify with
+ *     tb_decode_xcc_probe); `violations` (device uint32) is incremented for
+ *     every unit whose pieces ran on more than one XCD (its output may then be
+ *     wrong). merge_in_kernel = 0: a second kernel merges the partials
  *     (arrivals and violations unused). Calls that may overlap in time need
  *     their own workspace and arrival counters.
  * RoPE (rope_cos != NULL) and the fused append: as tb_paged_attention. The
  * newest positions of the rows must map to distinct pool slots.
  */
 int32_t tb_paged_decode(const void* q, int64_t q_row_stride, void* pool, int64_t num_blocks,
-                        void* out, int64_t out_row_stride,
-                        const int32_t* block_tables, int32_t max_blocks_per_seq,
-                        const int32_t* context_lens, int32_t num_seqs,
+                        void* out, int64_t out_row_stride, int32_t num_seqs,
                         const int32_t* plan, int32_t plan_workgroups, int32_t max_units,
                         int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                         float scale, int32_t dtype,
@@ -313,27 +310,42 @@ size_t tb_paged_decode_piece_bytes(int32_t num_heads, int32_t num_kv_heads, int3
 size_t tb_paged_decode_workspace_bytes(int32_t max_pieces, int32_t num_heads, int32_t num_kv_heads,
                                        int32_t head_dim);
 
-/* Per-workgroup limits of tb_paged_decode for a geometry: tiles, segments
- * (both bound the plan) and waves per workgroup. */
+/* Per-worker (wave) limits of tb_paged_decode for a geometry: tiles and
+ * segments (both bound the plan), and waves per workgroup. */
 int32_t tb_decode_limits(int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
-                         int32_t* max_tiles_per_wg, int32_t* max_segments_per_wg, int32_t* waves_per_wg);
+                         int32_t* max_tiles_per_worker, int32_t* max_segments_per_worker,
+                         int32_t* waves_per_wg);
 
 /* Host-side plan of a decode step (no device call, nothing allocated):
  * units (sequence b, kv head h) = b * num_kv_heads + h, each cut into
  * ceil(context_lens[b] / 16) tiles, packed onto num_xcds XCDs by tile count
- * (longest first, least loaded XCD); XCD x's tiles are split evenly over
- * workgroups x, x + num_xcds, ... and cut at unit boundaries into segments.
- * Layout (int32): [0] workgroups, [1] segments S, [2] units U, [3] pieces,
- * [4] num_xcds, [5..7] 0; wg_first [workgroups + 1] padded to a multiple of 4;
- * segments [S][4] = (unit, first tile, end tile, piece slot or -1);
- * units [U][2] = (pieces, first slot or -1).
- * TB_ERR_UNSUPPORTED when a workgroup would exceed max_tiles_per_wg or
- * max_segments_per_wg (more workgroups are then needed) or a unit would have
- * more than 255 pieces. context_lens is host memory here. */
-size_t tb_decode_plan_bytes(int32_t num_seqs, int32_t num_kv_heads, int32_t workgroups);
+ * (longest first, least loaded XCD). The workers are the `waves` waves of each
+ * of `workgroups` workgroups (worker k is wave k % waves of workgroup
+ * k / waves, on XCD (k / waves) % num_xcds); XCD x's tiles are split evenly
+ * over its workers and cut at unit boundaries into segments.
+ * Layout (int32): [0] workers W, [1] segments S, [2] units U, [3] partials,
+ * [4] num_xcds, [5] waves, [6] tiles T, [7] group_pieces; workers [W][4] =
+ * (first segment, segments, first tile, tiles); segments [S][8] = (unit, first
+ * tile, end tile, the group's partial slot or -1, context length, the piece's
+ * LDS index or -1 for a unit the segment holds whole, members | unit partials
+ * << 8 for a group's leader else 0, the unit's first slot or -1); units [U][2]
+ * = (partials, first slot or -1); tiles [T] = pool block of each tile (from
+ * block_tables, host int32 [num_seqs][max_blocks_per_seq]). A unit cut into
+ * several segments leaves a piece per segment; with group_pieces != 0 the
+ * pieces one workgroup holds of a unit form a group merged in LDS (one partial
+ * per workgroup), else every piece is its own group.
+ * TB_ERR_UNSUPPORTED when a worker would exceed max_tiles_per_worker or
+ * max_segments_per_worker (more workgroups are then needed) or a unit would
+ * have more than 255 pieces; TB_ERR_INDEX when a block id used by a tile lies
+ * outside [0, num_blocks). context_lens and block_tables are host memory;
+ * tb_decode_plan_bytes returns 0 for invalid lengths. */
+size_t tb_decode_plan_bytes(const int32_t* context_lens, int32_t num_seqs, int32_t num_kv_heads,
+                            int32_t workgroups, int32_t waves);
 int32_t tb_build_decode_plan(const int32_t* context_lens, int32_t num_seqs, int32_t num_kv_heads,
-                             int32_t workgroups, int32_t num_xcds, int32_t max_tiles_per_wg,
-                             int32_t max_segments_per_wg, int32_t* plan, size_t plan_bytes);
+                             const int32_t* block_tables, int32_t max_blocks_per_seq, int32_t block_size,
+                             int64_t num_blocks, int32_t workgroups, int32_t waves, int32_t num_xcds,
+                             int32_t max_tiles_per_worker, int32_t max_segments_per_worker,
+                             int32_t group_pieces, int32_t* plan, size_t plan_bytes);
 
 /* Records, for each of `workgroups` workgroups of one launch, the XCD it ran on
  * (device int32 [workgroups]): the check behind merge_in_kernel. */

@@ -126,6 +126,26 @@ def test_one_long_sequence_over_many_workgroups():
     assert meta.decode_pieces > 8
 
 
+@pytest.mark.parametrize("group,merge", [(True, True), (True, False), (False, True), (False, False)])
+def test_piece_grouping_and_merge_modes(group, merge):
+    """Pieces grouped per workgroup in LDS or not, merged inside the launch or by the
+    combine kernel: every mode against the oracle."""
+    c = case(15, 48, 14, 2, 64, 16, torch.bfloat16)
+    want, want_pool = oracle(c)
+    meta = build_step_metadata([x - 1 for x in c["ctx"]], [(b, b + 1) for b in range(len(c["ctx"]))], c["tables"],
+                               c["ctx"], block_size=16, num_blocks=c["NB"],
+                               partition_tokens=ops.partition_tokens(torch.bfloat16, 64))
+    assert ops.attach_decode_plan(meta, num_heads=14, num_kv_heads=2, head_dim=64, dtype=torch.bfloat16, device=DEV,
+                                  merge_in_kernel=merge, group_pieces=group)
+    meta.to(DEV)
+    assert meta.decode_pieces > 0
+    pool = c["pool"].to(DEV)
+    out = ops.paged_attention(c["q"].to(DEV), pool, meta, num_heads=14, k_new=c["k"].to(DEV), v_new=c["v"].to(DEV))
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(pool.cpu()), _bits(want_pool))
+    torch.testing.assert_close(out.cpu().float(), want.float(), **TOL)
+
+
 def test_in_launch_merge_and_combine_kernel_give_the_same_bits():
     c = case(10, 40, 14, 2, 64, 16, torch.bfloat16)
     a, _ = check(c, fused=True, merge=True)

@@ -79,20 +79,19 @@ class StepMetadata:
     # decode plan (tb_paged_decode): set by attach_decode_plan for decode-only steps
     rows_are_seqs: bool = False  # decode-only with row b = sequence b (the decode kernel's layout)
     decode_plan_np: np.ndarray | None = None
-    context_lens_np: np.ndarray | None = None
     decode_workgroups: int = 0
     decode_pieces: int = 0
     decode_units: int = 0
     decode_merge_in_kernel: bool = False
     decode_plan: torch.Tensor | None = None
-    context_lens: torch.Tensor | None = None
+    num_blocks: int = 0          # blocks of the pool the step's tables index
 
     def to(self, device: torch.device) -> "StepMetadata":
         """Upload every array with one host-to-device copy (views into one buffer)."""
         parts = [self.slot_mapping_np, self.block_tables_np.reshape(-1), self.work_np.reshape(-1),
                  self.row_part_off_np, self.prefill_tiles_np.reshape(-1), self.split_rows_np.reshape(-1)]
         if self.decode_plan_np is not None:
-            parts += [self.context_lens_np, self.decode_plan_np]
+            parts += [self.decode_plan_np]
         sizes = [pad4(p.size) for p in parts]
         host = np.zeros(sum(sizes), dtype=np.int32)
         offs = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
@@ -110,8 +109,7 @@ class StepMetadata:
         self.prefill_tiles = buf.narrow(0, int(offs[4]), parts[4].size).view(-1, 4)
         self.split_rows = buf.narrow(0, int(offs[5]), parts[5].size).view(-1, 4)
         if self.decode_plan_np is not None:
-            self.context_lens = buf.narrow(0, int(offs[6]), parts[6].size)
-            self.decode_plan = buf.narrow(0, int(offs[7]), parts[7].size)
+            self.decode_plan = buf.narrow(0, int(offs[6]), parts[6].size)
         return self
 
 
@@ -307,6 +305,7 @@ def build_step_metadata(positions, seq_slices, block_tables, context_lens, *, bl
         row_ctx_np=row_ctx_by_row.astype(np.int32),
         prefill_tiles_np=tiles_np.astype(np.int32),
         split_rows_np=split_rows.astype(np.int32),
+        num_blocks=int(num_blocks),
     )
 
 
@@ -409,8 +408,8 @@ def pack_decode_step(h: np.ndarray, offs: np.ndarray, Bp: int, max_nb: int, cont
 
 # ---- decode plans (tb_paged_decode) ---------------------------------------------
 def decode_limits(num_heads: int, num_kv_heads: int, head_dim: int):
-    """(max tiles, max segments, waves) per workgroup of the decode kernel for this
-    geometry, or None when the kernel does not serve it."""
+    """(max tiles, max segments) per worker (wave) and waves per workgroup of the
+    decode kernel for this geometry, or None when the kernel does not serve it."""
     import ctypes
 
     from . import _lib
@@ -421,12 +420,13 @@ def decode_limits(num_heads: int, num_kv_heads: int, head_dim: int):
     return (t.value, sg.value, w.value) if st == 0 else None
 
 
-def build_decode_plan(context_lens, num_heads: int, num_kv_heads: int, head_dim: int, workgroups: int,
-                      num_xcds: int) -> tuple[np.ndarray, int] | None:
+def build_decode_plan(context_lens, block_tables, *, block_size: int, num_blocks: int, num_heads: int,
+                      num_kv_heads: int, head_dim: int, workgroups: int, num_xcds: int,
+                      group_pieces: bool = True) -> tuple[np.ndarray, int] | None:
     """tb_build_decode_plan for a decode step (row b = sequence b with context_lens[b]
-    positions): the int32 plan and the workgroup count it needs, starting from
-    ``workgroups`` and doubling while a workgroup's share exceeds its LDS areas. None
-    when the geometry is not served by the decode kernel."""
+    positions, block_tables[b] its blocks): the int32 plan and the workgroup count it
+    needs, starting from ``workgroups`` and doubling while a worker's share exceeds
+    its LDS areas. None when the geometry is not served by the decode kernel."""
     import ctypes
 
     from . import _lib
@@ -434,16 +434,21 @@ def build_decode_plan(context_lens, num_heads: int, num_kv_heads: int, head_dim:
     lim = decode_limits(num_heads, num_kv_heads, head_dim)
     if lim is None:
         return None
-    tmax, smax, _ = lim
+    tmax, smax, waves = lim
     ctx = np.ascontiguousarray(np.asarray(context_lens, dtype=np.int32).reshape(-1))
     B = int(ctx.size)
+    tables = np.ascontiguousarray(np.asarray(block_tables, dtype=np.int32).reshape(B, -1) if B else
+                                  np.zeros((1, 1), dtype=np.int32))
     L = _lib.lib()
+    vp = lambda a: a.ctypes.data_as(ctypes.c_void_p)
     G = int(workgroups)
     for _ in range(8):
-        nbytes = int(L.tb_decode_plan_bytes(B, num_kv_heads, G))
+        nbytes = int(L.tb_decode_plan_bytes(vp(ctx), B, num_kv_heads, G, waves))
+        if nbytes == 0:
+            raise ValueError("invalid decode step for a plan (every context must hold >= 1 position)")
         plan = np.zeros(nbytes // 4, dtype=np.int32)
-        st = L.tb_build_decode_plan(ctx.ctypes.data_as(ctypes.c_void_p), B, num_kv_heads, G, num_xcds, tmax, smax,
-                                    plan.ctypes.data_as(ctypes.c_void_p), nbytes)
+        st = L.tb_build_decode_plan(vp(ctx), B, num_kv_heads, vp(tables), tables.shape[1], block_size, num_blocks,
+                                    G, waves, num_xcds, tmax, smax, int(group_pieces), vp(plan), nbytes)
         if st == 0:
             return plan, G
         if st != _lib.TB_ERR_UNSUPPORTED:
@@ -453,20 +458,23 @@ def build_decode_plan(context_lens, num_heads: int, num_kv_heads: int, head_dim:
 
 
 def attach_decode_plan(meta: StepMetadata, *, num_heads: int, num_kv_heads: int, head_dim: int,
-                       dtype: torch.dtype, workgroups: int, num_xcds: int, merge_in_kernel: bool) -> bool:
+                       dtype: torch.dtype, workgroups: int, num_xcds: int, merge_in_kernel: bool,
+                       group_pieces: bool = True) -> bool:
     """Give a decode-only step (row b = sequence b) the plan of the decode kernel, to be
     uploaded with the rest of its metadata by ``meta.to``. Returns whether it applies:
     16-bit rows, head_dim 64 / 128, at most 8 query heads per kv head, blocks of >= 16."""
     if (not meta.rows_are_seqs or dtype not in (torch.float16, torch.bfloat16) or meta.block_size < 16
-            or meta.device_buffer is not None):
+            or meta.device_buffer is not None or meta.num_blocks <= 0):
         return False
-    ctx = meta.row_ctx_np[:meta.num_seqs].astype(np.int32)
-    got = build_decode_plan(ctx, num_heads, num_kv_heads, head_dim, workgroups, num_xcds)
+    B = meta.num_seqs
+    ctx = meta.row_ctx_np[:B].astype(np.int32)
+    got = build_decode_plan(ctx, meta.block_tables_np[:B], block_size=meta.block_size, num_blocks=meta.num_blocks,
+                            num_heads=num_heads, num_kv_heads=num_kv_heads, head_dim=head_dim,
+                            workgroups=workgroups, num_xcds=num_xcds, group_pieces=group_pieces)
     if got is None:
         return False
     plan, G = got
     meta.decode_plan_np = plan
-    meta.context_lens_np = ctx
     meta.decode_workgroups = G
     meta.decode_units = int(plan[2])
     meta.decode_pieces = int(plan[3])

@@ -159,8 +159,8 @@ def workspace_for(meta: StepMetadata, num_heads: int, head_dim: int,
 
 
 class DecodeDevice:
-    """Launch facts of the decode kernel on one GPU: one persistent workgroup per CU,
-    and the XCD count under which partials merge inside the launch. The XCD count is
+    """Launch facts of the decode kernel on one GPU: one persistent workgroup (four
+    worker waves) per CU, and the XCD count under which partials merge inside the launch. The XCD count is
     the CU count / 32 (the CUs of one XCD) and is used only if a probe launch shows
     workgroup g running on XCD g mod that count, with distinct XCDs in between;
     otherwise the plan ignores XCDs and a second kernel merges the partials."""
@@ -203,13 +203,17 @@ def decode_device(device: torch.device) -> DecodeDevice:
 
 
 def attach_decode_plan(meta: StepMetadata, *, num_heads: int, num_kv_heads: int, head_dim: int,
-                       dtype: torch.dtype, device: torch.device) -> bool:
-    """metadata.attach_decode_plan with this device's workgroups and XCDs."""
+                       dtype: torch.dtype, device: torch.device, merge_in_kernel: bool | None = None,
+                       group_pieces: bool = True) -> bool:
+    """metadata.attach_decode_plan with this device's workgroups and XCDs (partials merged
+    inside the launch when the device allows it, unless merge_in_kernel is False)."""
     from .metadata import attach_decode_plan as attach
 
     d = decode_device(device)
+    merge = d.merge_in_kernel if merge_in_kernel is None else (bool(merge_in_kernel) and d.merge_in_kernel)
     return attach(meta, num_heads=num_heads, num_kv_heads=num_kv_heads, head_dim=head_dim, dtype=dtype,
-                  workgroups=d.workgroups, num_xcds=d.num_xcds, merge_in_kernel=d.merge_in_kernel)
+                  workgroups=d.workgroups, num_xcds=d.num_xcds if merge else 1, merge_in_kernel=merge,
+                  group_pieces=group_pieces)
 
 
 def decode_workspace_bytes(meta: StepMetadata, num_heads: int, num_kv_heads: int, head_dim: int) -> int:
@@ -249,6 +253,8 @@ def paged_decode(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, num
     nb, hkv, bs, d = _check_pool(pool)
     if meta.decode_plan is None:
         raise ValueError("metadata has no uploaded decode plan (attach_decode_plan, then meta.to(device))")
+    if meta.num_blocks > nb:
+        raise ValueError(f"the decode plan indexes a pool of {meta.num_blocks} blocks; this pool holds {nb}")
     _lib.require_gpu_tensor("q", q)
     if q.dtype != pool.dtype or q.dtype not in (torch.float16, torch.bfloat16):
         raise TypeError("the decode kernel takes fp16 / bf16 q in the pool dtype")
@@ -288,8 +294,7 @@ def paged_decode(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, num
     if bufs.pieces.numel() < need or bufs.units < meta.decode_units:
         raise ValueError("decode buffers too small for the step")
     st = _lib.lib().tb_paged_decode(
-        q.data_ptr(), qs, pool.data_ptr(), nb, out.data_ptr(), os_, meta.block_tables.data_ptr(),
-        meta.max_blocks_per_seq, meta.context_lens.data_ptr(), B, meta.decode_plan.data_ptr(),
+        q.data_ptr(), qs, pool.data_ptr(), nb, out.data_ptr(), os_, B, meta.decode_plan.data_ptr(),
         meta.decode_workgroups, meta.decode_units, num_heads, hkv, d, bs, float(scale), _lib.DTYPE_CODE[q.dtype],
         ksp, ks, vsp, vs, bufs.pieces.data_ptr(), bufs.pieces.numel(), meta.decode_pieces,
         bufs.arrivals.data_ptr(), bufs.units, int(meta.decode_merge_in_kernel), dev.violations.data_ptr(),
