@@ -400,8 +400,9 @@ def main() -> int:
     ap.add_argument("--workload", default="qwen-fp16-b64")
     ap.add_argument("--layers", type=int, default=0, help="layer pools to rotate (0 = auto)")
     ap.add_argument("--mode", choices=["fused", "split"], default="fused")
-    ap.add_argument("--kernel", choices=["decode", "items"], default="items",
-                    help="decode: persistent tile-stream kernel (tb_paged_decode); items: work-item kernel")
+    ap.add_argument("--kernel", choices=["auto", "decode", "items"], default="auto",
+                    help="decode: persistent tile-stream kernel (tb_paged_decode); items: work-item kernel; "
+                         "auto: the decode kernel for steps of >= ops.DECODE_KERNEL_MIN_BYTES of K/V")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--cpu-reps", type=int, default=5)
     ap.add_argument("--cpu-budget", type=float, default=20.0)
@@ -466,7 +467,9 @@ def main() -> int:
     P = args.partition or ops.partition_tokens(wl.dtype, wl.head_dim)
     meta = build_step_metadata(wl.positions, wl.seq_slices, wl.block_tables, wl.context_lens,
                                block_size=wl.block_size, num_blocks=wl.num_blocks, partition_tokens=P)
-    decode_kernel = args.kernel == "decode" and ops.attach_decode_plan(
+    want_decode = args.kernel == "decode" or (args.kernel == "auto" and ops.decode_kernel_preferred(
+        meta, num_kv_heads=wl.num_kv_heads, head_dim=wl.head_dim, dtype=wl.dtype))
+    decode_kernel = want_decode and ops.attach_decode_plan(
         meta, num_heads=wl.num_heads, num_kv_heads=wl.num_kv_heads, head_dim=wl.head_dim, dtype=wl.dtype, device=dev)
     meta.to(dev)
     q = wl.q.to(dev)

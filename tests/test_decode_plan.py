@@ -206,3 +206,31 @@ def test_bad_arguments():
     assert st == _lib.TB_ERR_INVALID_ARG                      # more positions than the table row holds
     st, _ = c_plan([20], 2, 8, 8, tables=np.array([[0, 7]], np.int32), nb=4)
     assert st == _lib.TB_ERR_INDEX                            # a block outside the pool
+
+
+def test_the_decode_kernel_is_chosen_for_large_decode_steps():
+    """ops.decode_kernel_preferred: decode-only fp16 / bf16 steps of at least
+    DECODE_KERNEL_MIN_BYTES of K/V (2 tensors x kv heads x head_dim x 2 bytes per position)."""
+    import torch
+
+    from tinybatch_amd import ops
+    from tinybatch_amd.metadata import build_step_metadata
+
+    def step(ctx, hkv=8, d=128, rows_are_seqs=True):
+        tables, nb = tables_for(ctx, 16)
+        pos = [c - 1 for c in ctx]
+        slices = [(b, b + 1) for b in range(len(ctx))]
+        if not rows_are_seqs:                   # one sequence with two rows: not a decode-only step
+            pos = [ctx[0] - 2, ctx[0] - 1] + pos[1:]
+            slices = [(0, 2)] + [(b + 1, b + 2) for b in range(1, len(ctx))]
+        return build_step_metadata(pos, slices, tables, ctx, block_size=16, num_blocks=nb, partition_tokens=256)
+
+    per_pos = 2 * 8 * 128 * 2
+    at = ops.DECODE_KERNEL_MIN_BYTES // per_pos
+    big = step([at // 4 + 1] * 4)
+    small = step([at // 4 - 1] * 4)
+    kw = dict(num_kv_heads=8, head_dim=128)
+    assert ops.decode_kernel_preferred(big, dtype=torch.bfloat16, **kw)
+    assert not ops.decode_kernel_preferred(small, dtype=torch.bfloat16, **kw)
+    assert not ops.decode_kernel_preferred(big, dtype=torch.float32, **kw)
+    assert not ops.decode_kernel_preferred(step([at // 4 + 1] * 4, rows_are_seqs=False), dtype=torch.float16, **kw)

@@ -18,7 +18,7 @@ import torch
 from . import _lib
 from .metadata import StepMetadata
 
-_WORKSPACES: dict[int, torch.Tensor] = {}
+_WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -145,12 +145,14 @@ def partition_tokens(dtype: torch.dtype, head_dim: int) -> int:
 
 def workspace_for(meta: StepMetadata, num_heads: int, head_dim: int,
                   device: torch.device) -> torch.Tensor | None:
-    """Split-row partials buffer, grown on demand and cached per device (calls on
-    one stream are ordered, so consecutive calls can share it)."""
+    """Split-row partials buffer, grown on demand and cached per device and stream:
+    calls on one stream are ordered, so consecutive calls can share it; calls on two
+    streams may overlap in time, so each stream has its own."""
     if meta.max_parts_per_row <= 1:
         return None
     need = int(_lib.lib().tb_paged_attention_workspace_bytes(meta.total_partitions, num_heads, head_dim))
-    key = device.index if device.index is not None else torch.cuda.current_device()
+    key = (device.index if device.index is not None else torch.cuda.current_device(),
+           torch.cuda.current_stream(device).cuda_stream)
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < need:
         ws = torch.empty(max(need, 1 << 20), dtype=torch.uint8, device=device)
@@ -200,6 +202,25 @@ def decode_device(device: torch.device) -> DecodeDevice:
     if d is None:
         d = _DECODE_DEVICES[key] = DecodeDevice(torch.device("cuda", key))
     return d
+
+
+# Decode-only steps with at least this many K/V bytes per call go to the persistent
+# decode kernel (tb_paged_decode). On MI355X it streams about 6.6 TB/s against about
+# 5.0 TB/s for the work-item kernel, but its fixed cost per call (the plan and first
+# tiles at the start, the piece merges at the end) is about 12 us against about 6 us;
+# the two meet near 134 MB (a 72 MB step: 23 us against 20 us; an 8.9 GB step:
+# 1.35 ms against 1.79 ms).
+DECODE_KERNEL_MIN_BYTES = 128 << 20
+
+
+def decode_kernel_preferred(meta: StepMetadata, *, num_kv_heads: int, head_dim: int, dtype: torch.dtype) -> bool:
+    """Whether a step is served faster by the persistent decode kernel: a decode-only
+    step (row b = sequence b) in fp16 / bf16 reading at least DECODE_KERNEL_MIN_BYTES
+    of K/V. The plan must then be attached (attach_decode_plan) before meta.to()."""
+    if not meta.rows_are_seqs or dtype not in (torch.float16, torch.bfloat16):
+        return False
+    kv_bytes = int(meta.row_ctx_np[:meta.num_seqs].astype(np.int64).sum()) * num_kv_heads * head_dim * 2 * 2
+    return kv_bytes >= DECODE_KERNEL_MIN_BYTES
 
 
 def attach_decode_plan(meta: StepMetadata, *, num_heads: int, num_kv_heads: int, head_dim: int,
