@@ -403,6 +403,8 @@ def main() -> int:
     ap.add_argument("--kernel", choices=["auto", "decode", "items"], default="auto",
                     help="decode: persistent tile-stream kernel (tb_paged_decode); items: work-item kernel; "
                          "auto: the decode kernel for steps of >= ops.DECODE_KERNEL_MIN_BYTES of K/V")
+    ap.add_argument("--combine", action="store_true",
+                    help="work-item kernel: merge split rows with the separate combine kernel, not inside the launch")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--cpu-reps", type=int, default=5)
     ap.add_argument("--cpu-budget", type=float, default=20.0)
@@ -471,6 +473,9 @@ def main() -> int:
         meta, num_kv_heads=wl.num_kv_heads, head_dim=wl.head_dim, dtype=wl.dtype))
     decode_kernel = want_decode and ops.attach_decode_plan(
         meta, num_heads=wl.num_heads, num_kv_heads=wl.num_kv_heads, head_dim=wl.head_dim, dtype=wl.dtype, device=dev)
+    # work items: split rows merged inside the launch where the device allows it
+    merged = (not decode_kernel and not args.combine and ops.attach_xcd_slot_map(
+        meta, num_heads=wl.num_heads, num_kv_heads=wl.num_kv_heads, dtype=wl.dtype, device=dev))
     meta.to(dev)
     q = wl.q.to(dev)
     k = wl.k_new.to(dev)
@@ -498,7 +503,7 @@ def main() -> int:
     per_launch_ms = ms / L
     achieved = bytes_layer["total"] / (per_launch_ms * 1e-3) / 1e9
     traffic = load_traffic(wl.name, args.mode)
-    if decode_kernel:
+    if decode_kernel or merged:
         viol = int(ops.decode_device(dev).violations.item())
         if viol:
             raise RuntimeError(f"{viol} units merged across XCDs: the workgroup placement assumption failed")
@@ -527,7 +532,7 @@ def main() -> int:
         kernel = "paged_decode_kernel" + ("" if ops.decode_device(dev).merge_in_kernel else " + decode_combine_kernel")
     else:
         attn = "paged_attn_valu_kernel" if wl.dtype == torch.float32 else "paged_attn_mfma_kernel"
-        kernel = attn + " + combine_partials_kernel"
+        kernel = attn if merged else attn + " + combine_partials_kernel"
     kernel += "" if fused else " + kv_append_kernel"
     line = {
         "metric": METRIC,
@@ -547,7 +552,8 @@ def main() -> int:
             "batch": wl.batch, "num_heads": wl.num_heads, "num_kv_heads": wl.num_kv_heads,
             "head_dim": wl.head_dim, "block_size": wl.block_size, "num_blocks": wl.num_blocks,
             "mean_context": round(sum(wl.context_lens) / wl.batch, 1), "layers": L,
-            "mode": args.mode, "graph": graph, "kernel": "decode" if decode_kernel else "items",
+            "mode": args.mode, "graph": graph,
+            "kernel": "decode" if decode_kernel else ("items, split rows merged in the launch" if merged else "items"),
             "partition_tokens": P,
             "bytes_per_layer_step": bytes_layer["total"],
         },

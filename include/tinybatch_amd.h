@@ -264,6 +264,51 @@ int32_t tb_paged_attention_noalloc(const void* q, int64_t q_row_stride,
                                    const float* rope_cos, const float* rope_sin, int32_t rope_max_position,
                                    hipStream_t stream);
 
+/* K2 with the split rows merged inside the launch (no combine kernel), for a
+ * 16-bit step of work items only (no prefill tiles; num_heads / num_kv_heads
+ * <= 16; TB_ERR_UNSUPPORTED otherwise). Arguments as tb_paged_attention, plus:
+ *   slot_map: device int32 [slot_count], the grid: slot s runs item
+ *     slot_map[s] / num_kv_heads for kv head slot_map[s] % num_kv_heads, or
+ *     nothing for -1. Every item of a row group (the partitions of split rows)
+ *     and kv head must sit in slots s with one s % num_xcds, the XCD that slot
+ *     runs on (slot s on XCD s % num_xcds: verify with tb_decode_xcc_probe);
+ *     tb_build_xcd_slot_map builds such a map.
+ *   arrivals: device memory of arrival_units * 128 bytes (arrival_units >=
+ *     num_rows * num_kv_heads, 128-byte aligned), zero before the first call
+ *     and left zero by every call; `violations` (device uint32) is incremented
+ *     for every row group whose partitions ran on more than one XCD (its
+ *     output may then be wrong). Calls that may overlap in time need their own
+ *     workspace and arrival counters.
+ * The workspace holds the split rows' partials as for tb_paged_attention
+ * (< 2 GiB). The outputs equal tb_paged_attention's bit for bit.
+ */
+int32_t tb_paged_attention_merged(const void* q, int64_t q_row_stride, void* pool, int64_t num_blocks,
+                                  void* out, int64_t out_row_stride,
+                                  const int32_t* block_tables, int32_t max_blocks_per_seq,
+                                  const int32_t* work_items, int32_t num_work_items,
+                                  const int32_t* row_part_offsets, int32_t num_rows,
+                                  int32_t max_parts_per_row, int32_t partition_tokens, int32_t total_partitions,
+                                  int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                  float scale, int32_t dtype,
+                                  const void* k_new, int64_t k_row_stride, const void* v_new, int64_t v_row_stride,
+                                  void* workspace, size_t workspace_bytes,
+                                  const int32_t* slot_map, int32_t slot_count,
+                                  unsigned long long* arrivals, int32_t arrival_units, uint32_t* violations,
+                                  const float* rope_cos, const float* rope_sin, int32_t rope_max_position,
+                                  hipStream_t stream);
+
+/* Host-side slot map of tb_paged_attention_merged (nothing allocated): the
+ * row groups (work items sharing their first row, all of one row's
+ * partitions) of each kv head are packed onto num_xcds XCDs by item count
+ * (longest first, least loaded XCD), and XCD x's items, in item order, fill
+ * slots x, x + num_xcds, ...; the map is padded with -1 to
+ * tb_xcd_slot_map_slots(...) slots (a multiple of num_xcds). work_items is
+ * the host copy of the step's work items (int32 [num_work_items][4]). */
+int32_t tb_xcd_slot_map_slots(const int32_t* work_items, int32_t num_work_items, int32_t num_kv_heads,
+                              int32_t num_xcds);
+int32_t tb_build_xcd_slot_map(const int32_t* work_items, int32_t num_work_items, int32_t num_kv_heads,
+                              int32_t num_xcds, int32_t* slot_map, int32_t slots);
+
 /* ---------------------------------------------------------------------------
  * K2 for decode steps: row b of q / out / k_new / v_new is sequence b's one new
  * token, at position context_lens[b] - 1, attending to positions

@@ -91,6 +91,18 @@ SIGNATURES = {
         c_vp,                   # device_counts (no workspace arguments)
         c_vp, c_vp, c_i32, c_vp,
     ]),
+    "tb_paged_attention_merged": (c_i32, [
+        c_vp, c_i64, c_vp, c_i64, c_vp, c_i64,   # q, stride, pool, num_blocks, out, stride
+        c_vp, c_i32, c_vp, c_i32, c_vp, c_i32,   # block_tables, max_nb, work_items, n, row_part_offsets, rows
+        c_i32, c_i32, c_i32,                     # max_parts_per_row, partition_tokens, total_partitions
+        c_i32, c_i32, c_i32, c_i32, c_f32, c_i32,   # heads, kv heads, head_dim, block_size, scale, dtype
+        c_vp, c_i64, c_vp, c_i64,                # k_new, stride, v_new, stride
+        c_vp, c_sz,                              # workspace, bytes
+        c_vp, c_i32, c_vp, c_i32, c_vp,          # slot_map, slot_count, arrivals, arrival_units, violations
+        c_vp, c_vp, c_i32, c_vp,                 # rope cos, sin, max position, stream
+    ]),
+    "tb_xcd_slot_map_slots": (c_i32, [c_vp, c_i32, c_i32, c_i32]),
+    "tb_build_xcd_slot_map": (c_i32, [c_vp, c_i32, c_i32, c_i32, c_vp, c_i32]),
     "tb_block_copy": (c_i32, [c_vp, c_i32, c_i64, c_vp, c_vp, c_i32, c_i64, c_vp]),
     "tb_block_gather": (c_i32, [c_vp, c_i64, c_vp, c_i32, c_vp, c_i64, c_vp]),
     "tb_block_scatter": (c_i32, [c_vp, c_vp, c_i64, c_vp, c_i32, c_i64, c_vp]),

@@ -94,6 +94,12 @@ struct attn_args {
   const char* v_new;
   int64_t v_new_row_bytes;
   rope_tables rope;       // rope.cos != null: q (and a fused append's K) rotated at position row_ctx - 1
+  // split rows merged inside the launch (tb_paged_attention_merged; null otherwise):
+  const int32_t* slot_map;          // grid slot -> item * num_kv_heads + kv head, or -1
+  unsigned long long* arrivals;     // per (first row of an item, kv head), 128 bytes apart, zero between launches
+  uint32_t* violations;             // incremented when a row group's partials ran on more than one XCD
+  uint32_t ws_bytes;                // the workspace bytes addressable through a buffer resource
+  int32_t num_work;                 // work items (bounds the slot map's values)
 };
 
 
@@ -344,6 +350,85 @@ struct mfma_shape {
 // block, so the block id and the tile base are wave-uniform (a scalar table
 // read and scalar address arithmetic per tile); otherwise each lane looks its
 // block up in a per-lane copy of the partition's table entries.
+// Split rows merged inside the launch (tb_paged_attention_merged). All partitions
+// of a row group and kv head ran on one XCD (the slot map places them so), whose
+// L2 every CU of the XCD shares: once a workgroup's partials are acknowledged by
+// the L2 it counts itself in the group's arrival word (8-bit fields per XCD, so a
+// partition that ran elsewhere is detected and reported), and the workgroup whose
+// partition arrives last merges the nparts partials of every (row, head) of the
+// item with L1-bypassing loads, as combine_partials_kernel does, and writes the
+// output. It leaves the arrival word zero for the next launch.
+template <typename Tag, int D>
+__device__ __forceinline__ void merge_in_launch(const attn_args& a, int row0, int kvh, int head0, int R, int ncols,
+                                                int pbeg0, int nparts) {
+  typedef typename math<Tag>::scalar_t scalar_t;
+  constexpr int NT = 64 * mfma_shape<D>::NW;
+  constexpr int BATCH = 8;                       // as combine_partials_kernel: the same bits
+  __shared__ int last;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this thread's partial stores are in the L2
+  __syncthreads();
+  unsigned long long* const word = a.arrivals + 16 * ((int64_t)row0 * a.num_kv_heads + kvh);
+  if (threadIdx.x == 0) {
+    unsigned xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    xcc &= 7;
+    const unsigned long long mine = 1ull << (8 * xcc);
+    const unsigned long long now = __hip_atomic_fetch_add(word, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + mine;
+    int arrived = 0;
+#pragma unroll
+    for (int x = 0; x < 8; ++x) arrived += (int)((now >> (8 * x)) & 0xFF);
+    const bool is_last = arrived == nparts;
+    if (is_last && now != ((unsigned long long)nparts << (8 * xcc)))
+      __hip_atomic_fetch_add(a.violations, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = is_last;
+  }
+  __syncthreads();
+  if (!last) return;
+  const auto rs = __builtin_amdgcn_make_buffer_rsrc(a.ws_acc, 0, a.ws_bytes, 0x00020000);
+  const uint32_t ml_base = (uint32_t)((const char*)a.ws_ml - (const char*)a.ws_acc);
+  for (int idx = threadIdx.x; idx < ncols * (D / 4); idx += NT) {
+    const int h = idx / (D / 4), d4 = idx - h * (D / 4);
+    const int row = row0 + h / R, head = head0 + h - (h / R) * R;
+    const int pfirst = pbeg0 + (h / R) * nparts;
+    float M = -INFINITY, L = 0.f;
+    float4_t o = float4_t{0.f, 0.f, 0.f, 0.f};
+    for (int p0 = 0; p0 < nparts; p0 += BATCH) {
+      float2 ml[BATCH];
+      float4_t av[BATCH];
+#pragma unroll
+      for (int k = 0; k < BATCH; ++k) {
+        ml[k] = make_float2(-INFINITY, 0.f);
+        av[k] = float4_t{0.f, 0.f, 0.f, 0.f};
+        if (p0 + k < nparts) {
+          const uint32_t slot = (uint32_t)(pfirst + p0 + k) * a.num_heads + head;
+          ml[k] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rs, ml_base + 8u * slot, 0, 1));
+          av[k] = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, 4u * (slot * D + 4 * d4), 0, 1));
+        }
+      }
+      float mb = M;
+#pragma unroll
+      for (int k = 0; k < BATCH; ++k) mb = fmaxf(mb, ml[k].x);
+      const float keep = fast_exp2(M - mb);   // 0 while M = -inf
+      L *= keep;
+      o *= keep;
+#pragma unroll
+      for (int k = 0; k < BATCH; ++k) {
+        const float w = ml[k].y > 0.f ? fast_exp2(ml[k].x - mb) : 0.f;
+        L = fmaf(ml[k].y, w, L);
+        o += av[k] * w;
+      }
+      M = mb;
+    }
+    const float inv = 1.f / L;
+    typedef scalar_t s4_t __attribute__((ext_vector_type(4)));
+    s4_t r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r[j] = (scalar_t)(o[j] * inv);
+    *reinterpret_cast<s4_t*>(a.out + row * a.out_row_bytes + ((int64_t)head * D + 4 * d4) * 2) = r;
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(word, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <typename Tag, int D, bool UT>
 __device__ __forceinline__ void decode_items_body(const attn_args& a, char* const lds, const int bx, const int bz) {
   using S = mfma_shape<D>;
@@ -364,8 +449,12 @@ __device__ __forceinline__ void decode_items_body(const attn_args& a, char* cons
   // The kv head varies fastest across the grid: the workgroups reading the K
   // and V tiles of the same blocks for the two (or more) kv heads run side by
   // side, so each block's bytes are fetched close together in time.
-  const int item = bx / a.num_kv_heads;
-  const int kvh = bx - item * a.num_kv_heads;
+  // the grid slot's item and kv head (a slot map places every partition of a split row
+  // group on one XCD, for the merge inside the launch; slots past the work hold -1)
+  const int slot_v = a.slot_map ? a.slot_map[bx] : bx;
+  if (slot_v < 0 || (a.slot_map && slot_v >= a.num_work * a.num_kv_heads)) return;   // whole workgroup
+  const int item = slot_v / a.num_kv_heads;
+  const int kvh = slot_v - item * a.num_kv_heads;
   const int4 wi = a.work[item];                  // the array holds the grid's capacity
   if (a.counts && item >= a.counts[0]) return;   // whole workgroup: beyond this step's items
   const int row0 = wi.x, seq = wi.y, part = wi.z & 0xFFFFFF, nrows = (wi.z >> 24) + 1, ctx0 = wi.w;
@@ -644,6 +733,7 @@ __device__ __forceinline__ void decode_items_body(const attn_args& a, char* cons
       if (d == 0) *reinterpret_cast<float2*>(a.ws_ml + (pidx * a.num_heads + head) * 2) = make_float2(Mh, L);
     }
   }
+  if (nparts > 1 && a.arrivals) merge_in_launch<Tag, D>(a, row0, kvh, head0, R, ncols, pbeg0, nparts);
 }
 
 template <typename Tag, int D, bool UT>
@@ -957,7 +1047,7 @@ template <typename Tag, int D>
 __global__ __launch_bounds__(COMBINE_THREADS) void combine_partials_kernel(const attn_args a) {
   constexpr int EB = elem<Tag>::bytes;
   constexpr int QPH = D / 4;                       // float4 columns per head
-  constexpr int BATCH = 16;
+  constexpr int BATCH = 8;                       // as merge_in_launch: the same bits
   const int col = threadIdx.x + COMBINE_THREADS * blockIdx.y;
   if (col >= a.num_heads * QPH) return;
   const int4 rec = a.split_rows[blockIdx.x];       // the array holds the grid's capacity
@@ -1033,6 +1123,14 @@ static int dispatch_valu_rep(const attn_args& a, int num_work, hipStream_t s) {
 template <typename Tag, int D>
 static void launch_mfma(const attn_args& a, int num_work, hipStream_t stream) {
   const dim3 grid(num_work * a.num_kv_heads, 1, a.rep / a.group), block(64 * mfma_shape<D>::NW);
+  if (a.log2_bs >= 4)   // 16-position tiles never cross a block
+    hipLaunchKernelGGL((paged_attn_mfma_kernel<Tag, D, true>), grid, block, 0, stream, a);
+  else
+    hipLaunchKernelGGL((paged_attn_mfma_kernel<Tag, D, false>), grid, block, 0, stream, a);
+}
+
+template <typename Tag, int D>
+static void launch_mfma_grid(const attn_args& a, dim3 grid, dim3 block, hipStream_t stream) {
   if (a.log2_bs >= 4)   // 16-position tiles never cross a block
     hipLaunchKernelGGL((paged_attn_mfma_kernel<Tag, D, true>), grid, block, 0, stream, a);
   else
@@ -1130,7 +1228,9 @@ static int32_t paged_attention_impl(const void* q, int64_t q_row_stride, void* p
                                     void* workspace, size_t workspace_bytes,
                                     const int32_t* device_counts, const float* rope_cos,
                                     const float* rope_sin, int32_t rope_max_position,
-                                    hipStream_t stream) {
+                                    hipStream_t stream, const int32_t* slot_map = nullptr,
+                                    int32_t slot_count = 0, unsigned long long* arrivals = nullptr,
+                                    int32_t arrival_units = 0, uint32_t* violations = nullptr) {
   const int eb = elem_bytes(dtype);
   TB_CHECK_ARG(eb > 0);
   TB_CHECK_ARG(num_heads > 0 && num_kv_heads > 0 && num_heads % num_kv_heads == 0);
@@ -1172,6 +1272,14 @@ static int32_t paged_attention_impl(const void* q, int64_t q_row_stride, void* p
   const int rep = num_heads / num_kv_heads;
   // heads per wave: the MFMA operand holds 16; the fp32 kernel keeps 8 in registers
   const int group = largest_divisor_upto(rep, eb == 2 ? 16 : 8);
+  const bool merged = slot_map != nullptr;
+  if (merged) {   // split rows merged inside the launch of the 16-bit work-item kernel
+    if (eb != 2 || num_prefill_tiles > 0 || group != rep || device_counts) return TB_ERR_UNSUPPORTED;
+    TB_CHECK_ARG(slot_count >= num_work_items * num_kv_heads && arrivals && violations);
+    TB_CHECK_ARG(((uintptr_t)arrivals & 127u) == 0 && (int64_t)arrival_units >= (int64_t)num_rows * num_kv_heads);
+    TB_CHECK_ARG(max_parts_per_row <= 1 ||
+                 tb_paged_attention_workspace_bytes(total_partitions, num_heads, head_dim) < ((size_t)1 << 31));
+  }
   TB_CHECK_ARG(num_kv_heads <= 65535 && rep / group <= 65535);
   TB_CHECK_ARG((int64_t)num_work_items * num_kv_heads < ((int64_t)1 << 31));
 
@@ -1204,8 +1312,26 @@ static int32_t paged_attention_impl(const void* q, int64_t q_row_stride, void* p
   a.k_new_row_bytes = k_row_stride * eb;
   a.v_new = (const char*)v_new;
   a.v_new_row_bytes = v_row_stride * eb;
+  a.slot_map = slot_map;
+  a.num_work = num_work_items;
+  a.arrivals = merged ? arrivals : nullptr;
+  a.violations = violations;
+  a.ws_bytes = workspace ? (uint32_t)tb_paged_attention_workspace_bytes(total_partitions, num_heads, head_dim) : 0u;
 
   const bool d64 = head_dim == 64;
+  if (merged) {
+    if (num_work_items > 0) {
+      const dim3 grid(slot_count), block(64 * (d64 ? mfma_shape<64>::NW : mfma_shape<128>::NW));
+      if (dtype == TB_DTYPE_F16) {
+        if (d64) launch_mfma_grid<f16_t, 64>(a, grid, block, stream);
+        else launch_mfma_grid<f16_t, 128>(a, grid, block, stream);
+      } else {
+        if (d64) launch_mfma_grid<bf16_t, 64>(a, grid, block, stream);
+        else launch_mfma_grid<bf16_t, 128>(a, grid, block, stream);
+      }
+    }
+    TB_RETURN_LAUNCH_STATUS();
+  }
   int st = TB_OK;
   switch (dtype) {
     case TB_DTYPE_F32:
@@ -1315,4 +1441,30 @@ extern "C" int32_t tb_paged_attention_noalloc(const void* q, int64_t q_row_strid
                                   num_kv_heads, head_dim, block_size, scale, dtype, k_new, k_row_stride, v_new,
                                   v_row_stride, ws, ws_bytes, device_counts, rope_cos, rope_sin,
                                   rope_max_position, stream);
+}
+
+extern "C" int32_t tb_paged_attention_merged(const void* q, int64_t q_row_stride, void* pool,
+                                             int64_t num_blocks, void* out, int64_t out_row_stride,
+                                             const int32_t* block_tables, int32_t max_blocks_per_seq,
+                                             const int32_t* work_items, int32_t num_work_items,
+                                             const int32_t* row_part_offsets, int32_t num_rows,
+                                             int32_t max_parts_per_row, int32_t partition_tokens,
+                                             int32_t total_partitions, int32_t num_heads,
+                                             int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                             float scale, int32_t dtype, const void* k_new,
+                                             int64_t k_row_stride, const void* v_new, int64_t v_row_stride,
+                                             void* workspace, size_t workspace_bytes,
+                                             const int32_t* slot_map, int32_t slot_count,
+                                             unsigned long long* arrivals, int32_t arrival_units,
+                                             uint32_t* violations, const float* rope_cos,
+                                             const float* rope_sin, int32_t rope_max_position,
+                                             hipStream_t stream) {
+  if (!slot_map || slot_count <= 0) return TB_ERR_INVALID_ARG;
+  return tb::paged_attention_impl(q, q_row_stride, pool, num_blocks, out, out_row_stride, block_tables,
+                                  max_blocks_per_seq, work_items, num_work_items, nullptr, 0, row_part_offsets,
+                                  num_rows, nullptr, 0, max_parts_per_row, partition_tokens, total_partitions,
+                                  num_heads, num_kv_heads, head_dim, block_size, scale, dtype, k_new, k_row_stride,
+                                  v_new, v_row_stride, workspace, workspace_bytes, nullptr, rope_cos, rope_sin,
+                                  rope_max_position, stream, slot_map, slot_count, arrivals, arrival_units,
+                                  violations);
 }

@@ -14,6 +14,7 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <algorithm>
 #include <vector>
 
 #include "../../include/tinybatch_amd.h"
@@ -494,5 +495,80 @@ extern "C" int32_t tb_build_decode_plan(const int32_t* context_lens, int32_t num
   plan[5] = waves;
   plan[6] = (int32_t)T;
   plan[7] = group_pieces ? 1 : 0;
+  return TB_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Slot map of tb_paged_attention_merged: a unit is (row group, kv head), a row
+// group being the work items that share their first row (the partitions of
+// that row, or of a run of decode rows of one sequence). Units are packed onto
+// the XCDs by item count, longest first onto the least loaded XCD (lowest index
+// among equals); XCD x's slot values (item * num_kv_heads + kv head, ascending)
+// fill slots x, x + num_xcds, ...; the rest hold -1.
+namespace {
+int32_t xcd_slot_lists(const int32_t* work_items, int32_t num_work_items, int32_t num_kv_heads, int32_t num_xcds,
+                       std::vector<std::vector<int32_t>>& lists) {
+  if (num_work_items < 0 || num_kv_heads <= 0 || num_xcds <= 0 || num_xcds > 64) return TB_ERR_INVALID_ARG;
+  if (num_work_items > 0 && !work_items) return TB_ERR_INVALID_ARG;
+  if ((int64_t)num_work_items * num_kv_heads >= ((int64_t)1 << 31)) return TB_ERR_INVALID_ARG;
+  // row groups in order of first appearance
+  std::vector<std::pair<int32_t, int32_t>> by_row(num_work_items);   // (first row, item)
+  for (int i = 0; i < num_work_items; ++i) by_row[i] = {work_items[4 * (int64_t)i], i};
+  std::stable_sort(by_row.begin(), by_row.end(),
+                   [](const std::pair<int32_t, int32_t>& x, const std::pair<int32_t, int32_t>& y) {
+                     return x.first < y.first;
+                   });
+  std::vector<std::pair<int32_t, int32_t>> groups;   // (first index in by_row, items)
+  for (int i = 0; i < num_work_items;) {
+    int j = i;
+    while (j < num_work_items && by_row[j].first == by_row[i].first) ++j;
+    groups.push_back({i, j - i});
+    i = j;
+  }
+  // units (group, kv head), longest first (stable: group order, then kv head)
+  std::vector<int64_t> units(groups.size() * (size_t)num_kv_heads);
+  for (size_t u = 0; u < units.size(); ++u) units[u] = (int64_t)u;
+  std::stable_sort(units.begin(), units.end(), [&](int64_t x, int64_t y) {
+    return groups[x / num_kv_heads].second > groups[y / num_kv_heads].second;
+  });
+  std::vector<int64_t> load(num_xcds, 0);
+  lists.assign(num_xcds, {});
+  for (const int64_t u : units) {
+    int best = 0;
+    for (int x = 1; x < num_xcds; ++x)
+      if (load[x] < load[best]) best = x;
+    const auto& g = groups[u / num_kv_heads];
+    const int32_t kvh = (int32_t)(u % num_kv_heads);
+    for (int k = 0; k < g.second; ++k) lists[best].push_back(by_row[g.first + k].second * num_kv_heads + kvh);
+    load[best] += g.second;
+  }
+  for (auto& l : lists) std::sort(l.begin(), l.end());
+  return TB_OK;
+}
+}  // namespace
+
+extern "C" int32_t tb_xcd_slot_map_slots(const int32_t* work_items, int32_t num_work_items, int32_t num_kv_heads,
+                                         int32_t num_xcds) {
+  std::vector<std::vector<int32_t>> lists;
+  const int32_t st = xcd_slot_lists(work_items, num_work_items, num_kv_heads, num_xcds, lists);
+  if (st != TB_OK) return st;
+  size_t most = 0;
+  for (const auto& l : lists) most = l.size() > most ? l.size() : most;
+  if (most * (size_t)num_xcds >= ((size_t)1 << 31)) return TB_ERR_INVALID_ARG;
+  return (int32_t)(most * num_xcds);
+}
+
+extern "C" int32_t tb_build_xcd_slot_map(const int32_t* work_items, int32_t num_work_items, int32_t num_kv_heads,
+                                         int32_t num_xcds, int32_t* slot_map, int32_t slots) {
+  if (!slot_map || slots < 0) return TB_ERR_INVALID_ARG;
+  std::vector<std::vector<int32_t>> lists;
+  const int32_t st = xcd_slot_lists(work_items, num_work_items, num_kv_heads, num_xcds, lists);
+  if (st != TB_OK) return st;
+  size_t most = 0;
+  for (const auto& l : lists) most = l.size() > most ? l.size() : most;
+  if ((int64_t)slots < (int64_t)(most * num_xcds)) return TB_ERR_INVALID_ARG;
+  for (int32_t s = 0; s < slots; ++s) slot_map[s] = -1;
+  for (int x = 0; x < num_xcds; ++x)
+    for (size_t j = 0; j < lists[x].size(); ++j) slot_map[j * num_xcds + x] = lists[x][j];
   return TB_OK;
 }

@@ -85,13 +85,17 @@ class StepMetadata:
     decode_merge_in_kernel: bool = False
     decode_plan: torch.Tensor | None = None
     num_blocks: int = 0          # blocks of the pool the step's tables index
+    # slot map of the work-item kernel with split rows merged inside the launch
+    # (tb_paged_attention_merged): set by attach_xcd_slot_map
+    slot_map_np: np.ndarray | None = None
+    slot_map: torch.Tensor | None = None
 
     def to(self, device: torch.device) -> "StepMetadata":
         """Upload every array with one host-to-device copy (views into one buffer)."""
         parts = [self.slot_mapping_np, self.block_tables_np.reshape(-1), self.work_np.reshape(-1),
                  self.row_part_off_np, self.prefill_tiles_np.reshape(-1), self.split_rows_np.reshape(-1)]
-        if self.decode_plan_np is not None:
-            parts += [self.decode_plan_np]
+        extra = [x for x in (self.decode_plan_np, self.slot_map_np) if x is not None]
+        parts += extra
         sizes = [pad4(p.size) for p in parts]
         host = np.zeros(sum(sizes), dtype=np.int32)
         offs = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int64)
@@ -108,8 +112,12 @@ class StepMetadata:
         self.row_part_off = buf.narrow(0, int(offs[3]), parts[3].size)
         self.prefill_tiles = buf.narrow(0, int(offs[4]), parts[4].size).view(-1, 4)
         self.split_rows = buf.narrow(0, int(offs[5]), parts[5].size).view(-1, 4)
+        k = 6
         if self.decode_plan_np is not None:
-            self.decode_plan = buf.narrow(0, int(offs[6]), parts[6].size)
+            self.decode_plan = buf.narrow(0, int(offs[k]), parts[k].size)
+            k += 1
+        if self.slot_map_np is not None:
+            self.slot_map = buf.narrow(0, int(offs[k]), parts[k].size)
         return self
 
 
@@ -480,3 +488,34 @@ def attach_decode_plan(meta: StepMetadata, *, num_heads: int, num_kv_heads: int,
     meta.decode_pieces = int(plan[3])
     meta.decode_merge_in_kernel = bool(merge_in_kernel)
     return True
+
+
+def build_xcd_slot_map(work, num_work_items: int, num_kv_heads: int, num_xcds: int) -> np.ndarray:
+    """tb_build_xcd_slot_map: the grid of tb_paged_attention_merged for these work items
+    (int32 [num_work_items, 4]): every row group's items of one kv head on one XCD."""
+    import ctypes
+
+    from . import _lib
+
+    w = np.ascontiguousarray(np.asarray(work, dtype=np.int32).reshape(-1, 4)[:num_work_items])
+    L = _lib.lib()
+    vp = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    n = int(L.tb_xcd_slot_map_slots(vp(w), num_work_items, num_kv_heads, num_xcds))
+    if n < 0:
+        _lib.check(n, "tb_xcd_slot_map_slots")
+    out = np.full(max(n, 1), -1, dtype=np.int32)
+    _lib.check(L.tb_build_xcd_slot_map(vp(w), num_work_items, num_kv_heads, num_xcds, vp(out), n),
+               "tb_build_xcd_slot_map")
+    return out[:n]
+
+
+def attach_xcd_slot_map(meta: StepMetadata, *, num_heads: int, num_kv_heads: int, dtype: torch.dtype,
+                        num_xcds: int) -> bool:
+    """Give a step of work items with split rows the slot map of the merged launch, to be
+    uploaded by ``meta.to``. Applies to 16-bit steps without prefill tiles, with at most
+    16 query heads per kv head and no capacity counts; returns whether it does."""
+    if (dtype not in (torch.float16, torch.bfloat16) or meta.num_prefill_tiles > 0 or meta.num_split_rows == 0
+            or num_heads // num_kv_heads > 16 or meta.device_buffer is not None or meta.num_work_items == 0):
+        return False
+    meta.slot_map_np = build_xcd_slot_map(meta.work_np, meta.num_work_items, num_kv_heads, num_xcds)
+    return meta.slot_map_np.size > 0

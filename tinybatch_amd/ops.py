@@ -237,6 +237,19 @@ def attach_decode_plan(meta: StepMetadata, *, num_heads: int, num_kv_heads: int,
                   group_pieces=group_pieces)
 
 
+def attach_xcd_slot_map(meta: StepMetadata, *, num_heads: int, num_kv_heads: int, dtype: torch.dtype,
+                        device: torch.device) -> bool:
+    """metadata.attach_xcd_slot_map with this device's XCDs, when the device runs workgroup
+    g on XCD g mod the XCD count (DecodeDevice); before meta.to(). Returns whether the
+    step's split rows will be merged inside the launch."""
+    from .metadata import attach_xcd_slot_map as attach
+
+    d = decode_device(device)
+    if not d.merge_in_kernel or d.num_xcds <= 1:
+        return False
+    return attach(meta, num_heads=num_heads, num_kv_heads=num_kv_heads, dtype=dtype, num_xcds=d.num_xcds)
+
+
 def decode_workspace_bytes(meta: StepMetadata, num_heads: int, num_kv_heads: int, head_dim: int) -> int:
     return int(_lib.lib().tb_paged_decode_workspace_bytes(meta.decode_pieces, num_heads, num_kv_heads, head_dim))
 
@@ -417,6 +430,17 @@ def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, 
         workspace = workspace_for(meta, num_heads, d, q.device)
     ws = workspace
     ws_bytes = 0 if ws is None else ws.numel() * ws.element_size()
+    if meta.slot_map is not None:   # split rows merged inside the launch (attach_xcd_slot_map)
+        dev = decode_device(q.device)
+        bufs = decode_buffers(q.device, 0, T * hkv)
+        _lib.check(_lib.lib().tb_paged_attention_merged(
+            q.data_ptr(), qs, pool.data_ptr(), nb, out.data_ptr(), os_,
+            meta.block_tables.data_ptr(), meta.max_blocks_per_seq, meta.work.data_ptr(), meta.num_work_items,
+            meta.row_part_off.data_ptr(), T, max(meta.max_parts_per_row, 1), meta.partition_tokens,
+            meta.total_partitions, num_heads, hkv, d, bs, float(scale), _lib.DTYPE_CODE[q.dtype], ksp, ks, vsp, vs,
+            _ptr(ws), ws_bytes, meta.slot_map.data_ptr(), int(meta.slot_map.numel()), bufs.arrivals.data_ptr(),
+            bufs.units, dev.violations.data_ptr(), *tail[1:]), "tb_paged_attention_merged")
+        return out
     _lib.check(_lib.lib().tb_paged_attention(*head, _ptr(ws), ws_bytes, *tail), "tb_paged_attention")
     return out
 
