@@ -780,7 +780,8 @@ struct prefill_shape {
   static constexpr int NCH = PART_TILE / CK;   // chunks per partition
   static constexpr int VCOLS = RB / 16;        // 16-byte pieces of a row
   static constexpr int LPT = CK * VCOLS / 256; // 16-byte loads per thread per chunk, of K and of V each
-  static constexpr int LDS = CK * RS + CK * RSV;
+  static constexpr int BLKS = PART_TILE / 4;   // block ids of a partition (block size >= 4)
+  static constexpr int LDS = CK * RS + CK * RSV + BLKS * 4;
   static constexpr int PF = LPT <= 2 ? 2 : 1;  // chunks loaded ahead (register sets; D = 128 has room for one)
   static_assert(LPT >= 1 && (CK * VCOLS) % 256 == 0 && PART_TILE % CK == 0, "chunk split");
 };
@@ -795,6 +796,7 @@ __device__ __forceinline__ void prefill_tiles_body(const attn_args& a, char* con
   constexpr int VCOLS = S::VCOLS, LPT = S::LPT, RSV = S::RSV, EB = 2;
   char* const k_lds = lds;
   char* const v_lds = lds + CK * RS;
+  int32_t* const blk_lds = reinterpret_cast<int32_t*>(lds + CK * RS + CK * RSV);
 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, lc = lane & 15, lg = lane >> 4;
   const int item = bx / a.num_heads;
@@ -826,17 +828,24 @@ __device__ __forceinline__ void prefill_tiles_body(const attn_args& a, char* con
     nparts = a.row_part_off[row0 + my_row + 1] - pbeg;
   }
 
+  // The block ids of the partition's positions, read once into LDS: a table read
+  // inside the chunk loop would be a load whose result the next chunk's addresses
+  // wait for, and since loads complete in issue order that wait would also take
+  // every K/V load issued before it, leaving one chunk in flight instead of PF.
+  const int blk0 = (c0 * CK) >> a.log2_bs;                    // first block of the partition
+  const int nblk = c_end > c0 ? (((c_end * CK < limit ? c_end * CK : limit) - 1) >> a.log2_bs) - blk0 + 1 : 0;
+  for (int i = threadIdx.x; i < nblk; i += 256) {           // nblk <= PART_TILE / block_size <= BLKS
+    int b = table[blk0 + i];
+    if (b < 0 || b >= a.num_blocks) b = 0;   // host validates; stay inside the pool
+    blk_lds[i] = b;
+  }
+  __syncthreads();
   // Thread t, load i: row (t + 256 i) / VCOLS of the chunk, 16-byte piece (t + 256 i) % VCOLS.
   auto load_ids = [&](int c, int (&ids)[LPT]) {
 #pragma unroll
     for (int i = 0; i < LPT; ++i) {
       const int p = c * CK + (threadIdx.x + 256 * i) / VCOLS;
-      int b = -1;
-      if (c < c_end && p < limit) {
-        b = table[p >> a.log2_bs];
-        if (b < 0 || b >= a.num_blocks) b = 0;   // host validates; stay inside the pool
-      }
-      ids[i] = b;
+      ids[i] = (c < c_end && p < limit) ? blk_lds[(p >> a.log2_bs) - blk0] : -1;
     }
   };
   auto load_kv = [&](int c, const int (&ids)[LPT], vec16 (&kr)[LPT], vec16 (&vr)[LPT]) {
