@@ -401,8 +401,8 @@ __device__ __forceinline__ void merge_in_launch(const attn_args& a, int row0, in
         av[k] = float4_t{0.f, 0.f, 0.f, 0.f};
         if (p0 + k < nparts) {
           const uint32_t slot = (uint32_t)(pfirst + p0 + k) * a.num_heads + head;
-          ml[k] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rs, ml_base + 8u * slot, 0, 1));
-          av[k] = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, 4u * (slot * D + 4 * d4), 0, 1));
+          ml[k] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rs, ml_base + 8u * slot, 0, LOAD_DEVICE_SCOPE));
+          av[k] = __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(rs, 4u * (slot * D + 4 * d4), 0, LOAD_DEVICE_SCOPE));
         }
       }
       float mb = M;

@@ -39,6 +39,12 @@ __device__ __forceinline__ vec16 ld16_stream(const void* p) {
   return r;
 }
 
+// Cache policy of a buffer load that must see stores other CUs of this XCD (or this
+// wave, just before) made to the L2: SC1 set, device scope, so the load misses in
+// the CU's vector L1 and is served by the L2. SC0 alone (workgroup scope) may still
+// hit a stale L1 line.
+constexpr int LOAD_DEVICE_SCOPE = 16;
+
 __device__ __forceinline__ void st16(void* p, const vec16& r) {
   uint4 v;
   v.x = r.w[0]; v.y = r.w[1]; v.z = r.w[2]; v.w = r.w[3];
@@ -147,18 +153,15 @@ __device__ __forceinline__ uint2 lds_read_tr16(const void* p) {
   return __builtin_bit_cast(uint2, r);
 }
 
-// Maxima of softmax scores (MFMA results or -inf, never NaN) as single
-// instructions: in IEEE mode the compiler quiets every input of fmaxf with an
-// extra v_max first, which doubled the max reductions of the attention loops.
-__device__ __forceinline__ float max_f32(float a, float b) {
-  float r;
-  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-  return r;
-}
+// Maxima of softmax scores (MFMA results or -inf, never NaN): IEEE-754 maximum
+// needs no quieting of its inputs, so a pair or triple is one v_maximum3_f32 (a
+// plain fmaxf in IEEE mode first quiets every input with an extra v_max). Written
+// with builtins, never inline asm: the compiler inserts the wait states between an
+// MFMA and a VALU read of its result only for reads it can see, and an asm max
+// placed right after an MFMA reads the accumulator's previous contents.
+__device__ __forceinline__ float max_f32(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 __device__ __forceinline__ float max3_f32(float a, float b, float c) {
-  float r;
-  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-  return r;
+  return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
 }
 
 // Reductions across the 16-lane rows of a wave on the VALU (gfx950 permlane
@@ -180,12 +183,17 @@ __device__ __forceinline__ float sum_xor32(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// A product rounded on its own: one v_mul_f32 that the compiler cannot fuse
+// A product rounded on its own to fp32: a multiply the compiler may not contract
 // into a following add (HIP's __fmul_rn is a plain multiply, and whether it is
-// contracted into an FMA depends on where it is inlined).
+// fused into an FMA depends on where it is inlined), nor fold with a following
+// conversion to fp16 into one v_fma_mixlo (a single rounding). The multiply is an
+// ordinary instruction, so the compiler sees its operand reads (the wait states
+// after v_rsq and the like); the empty asm only hides the product's origin from
+// the folds and executes nothing.
 __device__ __forceinline__ float mul_rn(float a, float b) {
-  float p;
-  asm("v_mul_f32 %0, %1, %2" : "=v"(p) : "v"(a), "v"(b));
+#pragma clang fp contract(off)
+  float p = a * b;
+  asm("" : "+v"(p));
   return p;
 }
 
