@@ -401,8 +401,12 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=0, help="layer pools to rotate (0 = auto)")
     ap.add_argument("--mode", choices=["fused", "split"], default="fused")
     ap.add_argument("--kernel", choices=["auto", "decode", "items"], default="auto",
-                    help="decode: persistent tile-stream kernel (tb_paged_decode); items: work-item kernel; "
+                    help="decode: streaming decode kernel (tb_paged_decode); items: work-item kernel; "
                          "auto: the decode kernel for steps of >= ops.DECODE_KERNEL_MIN_BYTES of K/V")
+    ap.add_argument("--decode-waves", type=int, default=0,
+                    help="decode kernel: waves per workgroup (a compiled variant; 0 = the library's default)")
+    ap.add_argument("--unit-cost", type=int, default=-1,
+                    help="decode kernel: tile-equivalents a unit adds to its worker's share (-1 = default)")
     ap.add_argument("--combine", action="store_true",
                     help="work-item kernel: merge split rows with the separate combine kernel, not inside the launch")
     ap.add_argument("--no-graph", action="store_true")
@@ -472,7 +476,8 @@ def main() -> int:
     want_decode = args.kernel == "decode" or (args.kernel == "auto" and ops.decode_kernel_preferred(
         meta, num_kv_heads=wl.num_kv_heads, head_dim=wl.head_dim, dtype=wl.dtype))
     decode_kernel = want_decode and ops.attach_decode_plan(
-        meta, num_heads=wl.num_heads, num_kv_heads=wl.num_kv_heads, head_dim=wl.head_dim, dtype=wl.dtype, device=dev)
+        meta, num_heads=wl.num_heads, num_kv_heads=wl.num_kv_heads, head_dim=wl.head_dim, dtype=wl.dtype, device=dev,
+        waves=args.decode_waves or None, unit_cost=args.unit_cost if args.unit_cost >= 0 else None)
     # work items: split rows merged inside the launch where the device allows it
     merged = (not decode_kernel and not args.combine and ops.attach_xcd_slot_map(
         meta, num_heads=wl.num_heads, num_kv_heads=wl.num_kv_heads, dtype=wl.dtype, device=dev))
@@ -529,7 +534,7 @@ def main() -> int:
         _log(f"e2e: {e2e['tok_s']} tok/s, TTFT mean {e2e['ttft_mean_ms']} ms, p99 {e2e['ttft_p99_ms']} ms")
 
     if decode_kernel:
-        kernel = "paged_decode_kernel" + ("" if ops.decode_device(dev).merge_in_kernel else " + decode_combine_kernel")
+        kernel = "paged_stream_kernel"
     else:
         attn = "paged_attn_valu_kernel" if wl.dtype == torch.float32 else "paged_attn_mfma_kernel"
         kernel = attn if merged else attn + " + combine_partials_kernel"
@@ -553,7 +558,8 @@ def main() -> int:
             "head_dim": wl.head_dim, "block_size": wl.block_size, "num_blocks": wl.num_blocks,
             "mean_context": round(sum(wl.context_lens) / wl.batch, 1), "layers": L,
             "mode": args.mode, "graph": graph,
-            "kernel": "decode" if decode_kernel else ("items, split rows merged in the launch" if merged else "items"),
+            "kernel": (f"decode ({meta.decode_waves} waves per workgroup)" if decode_kernel else
+                       ("items, split rows merged in the launch" if merged else "items")),
             "partition_tokens": P,
             "bytes_per_layer_step": bytes_layer["total"],
         },

@@ -314,86 +314,80 @@ int32_t tb_build_xcd_slot_map(const int32_t* work_items, int32_t num_work_items,
  * token, at position context_lens[b] - 1, attending to positions
  * 0 .. context_lens[b] - 1 (reference src/tinybatch/model.py:130-147 for
  * decode rows, with the append of kv_cache.py:25-38 fused when k_new != NULL).
- * fp16 / bf16, head_dim 64 or 128, num_heads / num_kv_heads <= 8, block_size a
- * power of two >= 16 (TB_ERR_UNSUPPORTED otherwise: use tb_paged_attention).
+ * fp16 / bf16, head_dim 64 or 128, num_heads / num_kv_heads <= 8,
+ * num_kv_heads <= 16, block_size a power of two >= 16 (TB_ERR_UNSUPPORTED
+ * otherwise: use tb_paged_attention).
  *
- * The work is a plan (tb_build_decode_plan, which also carries the step's
- * context lengths and the pool block of every tile) for plan_workgroups
- * persistent workgroups whose waves each stream an equal share of the
- * 16-position tiles of all (sequence, kv head) units; a unit cut over several
- * waves is merged by the one finishing last.
+ * The work is a plan (tb_build_decode_plan) for plan_workgroups workgroups of
+ * plan_waves waves, one workgroup per CU: every wave streams its own share of
+ * the step's 16-position tiles (sequence, kv head, 16 positions) through a ring
+ * in LDS; a (sequence, kv head) unit cut over several waves is merged by the
+ * workgroup whose partial arrives last.
  *   workspace: >= tb_paged_decode_workspace_bytes(max_pieces, ...) bytes of
  *     device memory, 128-byte aligned, for the partials (max_pieces >= the
- *     plan's pieces; max_units >= num_seqs * num_kv_heads).
- *   merge_in_kernel = 1: a unit's partials are merged inside the launch by the
- *     wave whose partial arrives last, counted in `arrivals`: device memory of
- *     arrival_units * 128 bytes (arrival_units >= max_units, 128-byte
- *     aligned), zero before the first call (allocate it zeroed) and left zero
- *     by every call, so one buffer serves every later call. It assumes that
- *     workgroup g runs on XCD g % num_xcds of the plan (verify with
- *     tb_decode_xcc_probe); `violations` (device uint32) is incremented for
- *     every unit whose pieces ran on more than one XCD (its output may then be
- *     wrong). merge_in_kernel = 0: a second kernel merges the partials
- *     (arrivals and violations unused). Calls that may overlap in time need
- *     their own workspace and arrival counters.
+ *     plan's pieces).
+ *   arrivals: arrival_units * 128 bytes of device memory (arrival_units >=
+ *     num_seqs * num_kv_heads, 128-byte aligned), zero before the first call
+ *     (allocate it zeroed) and left zero by every call, so one buffer serves
+ *     every later call. The partials of a unit are written and merged inside one
+ *     XCD: the plan assumes that workgroup g runs on XCD g % num_xcds (verify
+ *     with tb_decode_xcc_probe); `violations` (device uint32) is incremented
+ *     for every unit whose partials ran on more than one XCD (its output may
+ *     then be wrong). Calls that may overlap in time need their own workspace
+ *     and arrival counters.
  * RoPE (rope_cos != NULL) and the fused append: as tb_paged_attention. The
  * newest positions of the rows must map to distinct pool slots.
  */
 int32_t tb_paged_decode(const void* q, int64_t q_row_stride, void* pool, int64_t num_blocks,
                         void* out, int64_t out_row_stride, int32_t num_seqs,
-                        const int32_t* plan, int32_t plan_workgroups, int32_t max_units,
+                        const int32_t* plan, int32_t plan_workgroups, int32_t plan_waves, int32_t plan_stride,
                         int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
-                        float scale, int32_t dtype,
-                        const void* k_new, int64_t k_row_stride, const void* v_new, int64_t v_row_stride,
-                        void* workspace, size_t workspace_bytes, int32_t max_pieces,
-                        unsigned long long* arrivals, int32_t arrival_units,
-                        int32_t merge_in_kernel, uint32_t* violations,
-                        const float* rope_cos, const float* rope_sin, int32_t rope_max_position,
-                        hipStream_t stream);
-
+                        float scale, int32_t dtype, const void* k_new, int64_t k_row_stride,
+                        const void* v_new, int64_t v_row_stride, void* workspace, size_t workspace_bytes,
+                        int32_t max_pieces, unsigned long long* arrivals, int32_t arrival_units,
+                        uint32_t* violations, const float* rope_cos, const float* rope_sin,
+                        int32_t rope_max_position, hipStream_t stream);
 size_t tb_paged_decode_piece_bytes(int32_t num_heads, int32_t num_kv_heads, int32_t head_dim);
 size_t tb_paged_decode_workspace_bytes(int32_t max_pieces, int32_t num_heads, int32_t num_kv_heads,
                                        int32_t head_dim);
 
-/* Per-worker (wave) limits of tb_paged_decode for a geometry: tiles and
- * segments (both bound the plan), and waves per workgroup. */
-int32_t tb_decode_limits(int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
-                         int32_t* max_tiles_per_worker, int32_t* max_segments_per_worker,
-                         int32_t* waves_per_wg);
+/* The default waves per workgroup and per-unit cost (below) of tb_paged_decode
+ * for a head dim (TB_ERR_UNSUPPORTED for head dims it does not serve), and
+ * whether a (head dim, waves) pair is compiled. */
+int32_t tb_decode_defaults(int32_t head_dim, int32_t* waves, int32_t* unit_cost);
+int32_t tb_decode_variant_supported(int32_t head_dim, int32_t waves);
 
-/* Host-side plan of a decode step (no device call, nothing allocated):
- * units (sequence b, kv head h) = b * num_kv_heads + h, each cut into
- * ceil(context_lens[b] / 16) tiles, packed onto num_xcds XCDs by tile count
- * (longest first, least loaded XCD). The workers are the `waves` waves of each
- * of `workgroups` workgroups (worker k is wave k % waves of workgroup
- * k / waves, on XCD (k / waves) % num_xcds); XCD x's tiles are split evenly
- * over its workers and cut at unit boundaries into segments.
- * Layout (int32): [0] workers W, [1] segments S, [2] units U, [3] partials,
- * [4] num_xcds, [5] waves, [6] tiles T, [7] group_pieces; workers [W][4] =
- * (first segment, segments, first tile, tiles); segments [S][8] = (unit, first
- * tile, end tile, the group's partial slot or -1, context length, the piece's
- * LDS index or -1 for a unit the segment holds whole, members | unit partials
- * << 8 for a group's leader else 0, the unit's first slot or -1); units [U][2]
- * = (partials, first slot or -1); tiles [T] = pool block of each tile (from
- * block_tables, host int32 [num_seqs][max_blocks_per_seq]). A unit cut into
- * several segments leaves a piece per segment; with group_pieces != 0 the
- * pieces one workgroup holds of a unit form a group merged in LDS (one partial
- * per workgroup), else every piece is its own group.
- * TB_ERR_UNSUPPORTED when a worker would exceed max_tiles_per_worker or
- * max_segments_per_worker (more workgroups are then needed) or a unit would
- * have more than 255 pieces; TB_ERR_INDEX when a block id used by a tile lies
- * outside [0, num_blocks). context_lens and block_tables are host memory;
- * tb_decode_plan_bytes returns 0 for invalid lengths. */
-size_t tb_decode_plan_bytes(const int32_t* context_lens, int32_t num_seqs, int32_t num_kv_heads,
-                            int32_t workgroups, int32_t waves);
+/* Host-side plan of a decode step (no device call, nothing allocated): units
+ * (sequence b, kv head h), each cut into ceil(context_lens[b] / 16) tiles, are
+ * packed onto num_xcds XCDs (longest first, least loaded XCD; a unit weighs
+ * its tiles + unit_cost). XCD x's list is split evenly on that weight over
+ * its workers (worker kk = wave kk % waves of workgroup
+ * (kk / waves) * num_xcds + x); each unit segment of a worker is padded to an
+ * even number of tiles. Layout (int32): counts [workers] (padded to a multiple
+ * of 4), then entries [workers][stride] + 64 of padding, each int32 x4 =
+ *   (byte offset of the tile's K rows in the pool >> 8,
+ *    b | h << 20 | (valid rows - 1) << 24 | unit's last tile << 28 | pad << 29,
+ *    context_lens[b] | piece index << 24,
+ *    -1 for a unit one worker holds whole, else first partial slot |
+ *      (pieces - 1) << 20 | (wave of piece 0) << 28).
+ * tb_decode_plan_shape gives the entries of the busiest worker (stride must be
+ * at least that, and even) and the partial slots (max_pieces); both return
+ * TB_ERR_UNSUPPORTED when a unit would be cut over more than 255 workers (use
+ * fewer waves or tb_paged_attention), TB_ERR_INDEX when a block id lies
+ * outside [0, num_blocks) or a table is too short. context_lens and
+ * block_tables (int32 [num_seqs][max_blocks_per_seq]) are host memory. */
+int32_t tb_decode_plan_shape(const int32_t* context_lens, int32_t num_seqs, int32_t num_kv_heads,
+                             int32_t head_dim, int32_t workgroups, int32_t waves, int32_t num_xcds,
+                             int32_t unit_cost, int32_t* max_entries, int32_t* pieces);
+size_t tb_decode_plan_words(int32_t workers, int32_t stride);
 int32_t tb_build_decode_plan(const int32_t* context_lens, int32_t num_seqs, int32_t num_kv_heads,
-                             const int32_t* block_tables, int32_t max_blocks_per_seq, int32_t block_size,
-                             int64_t num_blocks, int32_t workgroups, int32_t waves, int32_t num_xcds,
-                             int32_t max_tiles_per_worker, int32_t max_segments_per_worker,
-                             int32_t group_pieces, int32_t* plan, size_t plan_bytes);
+                             int32_t head_dim, const int32_t* block_tables, int32_t max_blocks_per_seq,
+                             int32_t block_size, int64_t num_blocks, int32_t workgroups, int32_t waves,
+                             int32_t num_xcds, int32_t unit_cost, int32_t stride, int32_t* plan,
+                             size_t plan_words);
 
 /* Records, for each of `workgroups` workgroups of one launch, the XCD it ran on
- * (device int32 [workgroups]): the check behind merge_in_kernel. */
+ * (device int32 [workgroups]): the check behind the in-launch merges. */
 int32_t tb_decode_xcc_probe(int32_t workgroups, int32_t* out, hipStream_t stream);
 
 /* ---------------------------------------------------------------------------

@@ -1,17 +1,19 @@
-"""The decode kernel (tb_paged_decode: persistent workgroups over 16-position
-tiles, partials merged inside the launch) against the oracle, through the C ABI.
+"""The decode kernel (tb_paged_decode: one workgroup per CU, every wave streaming
+its share of the step's 16-position tiles, partials merged inside the launch)
+against the oracle, through the C ABI.
 
 Bars: appended rows bit-exact; attention rtol = atol = 2e-2 at fp16 / bf16
-against the oracle in the same dtype. Also: the same bits from the in-launch
-merge and the after-launch combine kernel, from repeated calls, and from
-fused RoPE against rotating first; no unit ever merged across XCDs."""
+against the oracle in the same dtype. Also: every compiled variant (waves per
+workgroup), steps with fewer tiles than workers, the same bits from repeated
+calls and from fused RoPE against rotating first; no unit ever merged across
+XCDs."""
 import numpy as np
 import pytest
 import torch
 
 from oracle import reference_path as ref
 from tinybatch_amd import layer_ops, ops
-from tinybatch_amd.metadata import attach_decode_plan as attach_host, build_step_metadata
+from tinybatch_amd.metadata import build_step_metadata
 from tinybatch_amd.model import rope_tables
 from tinybatch_amd.workloads import make_decode_workload
 
@@ -24,16 +26,12 @@ def _bits(t):
     return t.contiguous().view(torch.int16)
 
 
-def decode_meta(ctx, tables, NB, BS, Hq, Hkv, D, dtype, merge=None):
+def decode_meta(ctx, tables, NB, BS, Hq, Hkv, D, dtype, waves=None):
     B = len(ctx)
     meta = build_step_metadata([c - 1 for c in ctx], [(b, b + 1) for b in range(B)], tables, ctx, block_size=BS,
                                num_blocks=NB, partition_tokens=ops.partition_tokens(dtype, D))
-    if merge is None:
-        assert ops.attach_decode_plan(meta, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, dtype=dtype, device=DEV)
-    else:   # the device's plan, its partials merged inside the launch or by the combine kernel
-        d = ops.decode_device(DEV)
-        assert attach_host(meta, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, dtype=dtype, workgroups=d.workgroups,
-                           num_xcds=d.num_xcds, merge_in_kernel=merge)
+    assert ops.attach_decode_plan(meta, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, dtype=dtype, device=DEV,
+                                  waves=waves)
     return meta.to(DEV)
 
 
@@ -68,8 +66,8 @@ def oracle(c):
     return out, pool
 
 
-def run(c, fused=True, merge=None):
-    meta = decode_meta(c["ctx"], c["tables"], c["NB"], c["BS"], c["Hq"], c["Hkv"], c["D"], c["dtype"], merge)
+def run(c, fused=True, waves=None):
+    meta = decode_meta(c["ctx"], c["tables"], c["NB"], c["BS"], c["Hq"], c["Hkv"], c["D"], c["dtype"], waves)
     pool = c["pool"].to(DEV)
     q, k, v = c["q"].to(DEV), c["k"].to(DEV), c["v"].to(DEV)
     if fused:
@@ -81,9 +79,9 @@ def run(c, fused=True, merge=None):
     return out.cpu(), pool.cpu(), meta
 
 
-def check(c, fused=True, merge=None):
+def check(c, fused=True, waves=None):
     want, want_pool = oracle(c)
-    got, pool, meta = run(c, fused, merge)
+    got, pool, meta = run(c, fused, waves)
     assert torch.equal(_bits(pool), _bits(want_pool)), "pool differs (append)"
     torch.testing.assert_close(got.float(), want.float(), **TOL)
     return got, meta
@@ -120,37 +118,25 @@ def test_short_and_block_multiple_contexts():
         check(case(8, len(ctx), 14, 2, 64, BS, torch.float16, ctx=ctx), fused=False)
 
 
-def test_one_long_sequence_over_many_workgroups():
-    c = case(9, 1, 14, 2, 64, 16, torch.bfloat16, ctx=[60000])
-    _, meta = check(c, fused=True)
-    assert meta.decode_pieces > 8
+def test_long_sequences_over_many_workgroups():
+    """Units cut over up to 128 workers (4 waves per workgroup)."""
+    c = case(9, 4, 14, 2, 64, 16, torch.bfloat16, ctx=[60000, 31000, 900, 5])
+    _, meta = check(c, fused=True, waves=4)
+    assert meta.decode_pieces > 100
 
 
-@pytest.mark.parametrize("group,merge", [(True, True), (True, False), (False, True), (False, False)])
-def test_piece_grouping_and_merge_modes(group, merge):
-    """Pieces grouped per workgroup in LDS or not, merged inside the launch or by the
-    combine kernel: every mode against the oracle."""
-    c = case(15, 48, 14, 2, 64, 16, torch.bfloat16)
-    want, want_pool = oracle(c)
-    meta = build_step_metadata([x - 1 for x in c["ctx"]], [(b, b + 1) for b in range(len(c["ctx"]))], c["tables"],
-                               c["ctx"], block_size=16, num_blocks=c["NB"],
-                               partition_tokens=ops.partition_tokens(torch.bfloat16, 64))
-    assert ops.attach_decode_plan(meta, num_heads=14, num_kv_heads=2, head_dim=64, dtype=torch.bfloat16, device=DEV,
-                                  merge_in_kernel=merge, group_pieces=group)
-    meta.to(DEV)
-    assert meta.decode_pieces > 0
-    pool = c["pool"].to(DEV)
-    out = ops.paged_attention(c["q"].to(DEV), pool, meta, num_heads=14, k_new=c["k"].to(DEV), v_new=c["v"].to(DEV))
-    torch.cuda.synchronize()
-    assert torch.equal(_bits(pool.cpu()), _bits(want_pool))
-    torch.testing.assert_close(out.cpu().float(), want.float(), **TOL)
+@pytest.mark.parametrize("D,waves", [(64, 8), (64, 6), (64, 4), (128, 4), (128, 3)])
+def test_every_variant(D, waves):
+    Hq, Hkv = (14, 2) if D == 64 else (32, 8)
+    c = case(15 + waves, 48, Hq, Hkv, D, 16, torch.bfloat16)
+    _, meta = check(c, fused=True, waves=waves)
+    assert meta.decode_waves == waves and meta.decode_pieces > 0
 
 
-def test_in_launch_merge_and_combine_kernel_give_the_same_bits():
-    c = case(10, 40, 14, 2, 64, 16, torch.bfloat16)
-    a, _ = check(c, fused=True, merge=True)
-    b, _ = check(c, fused=True, merge=False)
-    assert torch.equal(_bits(a), _bits(b))
+def test_fewer_tiles_than_workers():
+    """A step far smaller than the grid: most workers idle, units over consecutive workers."""
+    for seed, ctx in ((16, [40, 33, 17, 1, 64]), (17, [300] * 12), (18, [2000, 20])):
+        check(case(seed, len(ctx), 14, 2, 64, 16, torch.float16, ctx=ctx), fused=True)
 
 
 def test_repeated_calls_same_bits_and_no_cross_xcd_merges():
@@ -165,6 +151,25 @@ def test_repeated_calls_same_bits_and_no_cross_xcd_merges():
     torch.cuda.synchronize()
     assert all(torch.equal(_bits(o), _bits(outs[0])) for o in outs[1:])
     assert int(ops.decode_device(DEV).violations.item()) == 0
+
+
+def test_workspace_contents_before_the_call_never_reach_the_output():
+    # every partial slot holds a NaN bit pattern before each call: the merges must
+    # read only what this launch wrote (the last arriving group's own partial too)
+    c = case(13, 64, 14, 2, 64, 16, torch.float16, nan_stale=False)
+    want, want_pool = oracle(c)
+    meta = decode_meta(c["ctx"], c["tables"], c["NB"], 16, 14, 2, 64, torch.float16)
+    bufs = ops.DecodeBuffers(DEV, ops.decode_workspace_bytes(meta, 14, 2, 64), meta.decode_units)
+    q, k, v = c["q"].to(DEV), c["k"].to(DEV), c["v"].to(DEV)
+    outs = []
+    for _ in range(3):
+        pool = c["pool"].to(DEV)
+        bufs.pieces.fill_(0xFF)
+        outs.append(ops.paged_decode(q, pool, meta, num_heads=14, k_new=k, v_new=v, workspace=bufs).cpu())
+        assert torch.equal(_bits(pool.cpu()), _bits(want_pool))
+    for o in outs:
+        torch.testing.assert_close(o.float(), want.float(), **TOL)
+        assert torch.equal(_bits(o), _bits(outs[0]))
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])

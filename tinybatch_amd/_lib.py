@@ -71,18 +71,20 @@ SIGNATURES = {
     ]),
     "tb_paged_decode": (c_i32, [
         c_vp, c_i64, c_vp, c_i64, c_vp, c_i64,   # q, q stride, pool, num_blocks, out, out stride
-        c_i32, c_vp, c_i32, c_i32,               # num_seqs, plan, plan_workgroups, max_units
+        c_i32, c_vp, c_i32, c_i32, c_i32,        # num_seqs, plan, plan_workgroups, plan_waves, plan_stride
         c_i32, c_i32, c_i32, c_i32, c_f32, c_i32,   # heads, kv heads, head_dim, block_size, scale, dtype
         c_vp, c_i64, c_vp, c_i64,                # k_new, k stride, v_new, v stride
         c_vp, c_sz, c_i32,                       # workspace, bytes, max_pieces
-        c_vp, c_i32, c_i32, c_vp,                # arrivals, arrival_units, merge_in_kernel, violations
+        c_vp, c_i32, c_vp,                       # arrivals, arrival_units, violations
         c_vp, c_vp, c_i32, c_vp,                 # rope cos, sin, max position, stream
     ]),
     "tb_paged_decode_piece_bytes": (c_sz, [c_i32, c_i32, c_i32]),
     "tb_paged_decode_workspace_bytes": (c_sz, [c_i32, c_i32, c_i32, c_i32]),
-    "tb_decode_limits": (c_i32, [c_i32, c_i32, c_i32, c_vp, c_vp, c_vp]),
-    "tb_decode_plan_bytes": (c_sz, [c_vp, c_i32, c_i32, c_i32, c_i32]),
-    "tb_build_decode_plan": (c_i32, [c_vp, c_i32, c_i32, c_vp, c_i32, c_i32, c_i64, c_i32, c_i32, c_i32, c_i32,
+    "tb_decode_defaults": (c_i32, [c_i32, c_vp, c_vp]),
+    "tb_decode_variant_supported": (c_i32, [c_i32, c_i32]),
+    "tb_decode_plan_shape": (c_i32, [c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp]),
+    "tb_decode_plan_words": (c_sz, [c_i32, c_i32]),
+    "tb_build_decode_plan": (c_i32, [c_vp, c_i32, c_i32, c_i32, c_vp, c_i32, c_i32, c_i64, c_i32, c_i32, c_i32,
                                      c_i32, c_i32, c_vp, c_sz]),
     "tb_decode_xcc_probe": (c_i32, [c_i32, c_vp, c_vp]),
     "tb_paged_attention_noalloc": (c_i32, [

@@ -272,233 +272,6 @@ extern "C" int32_t tb_build_step_metadata(const int32_t* query_start_loc, int32_
 }
 
 // ---------------------------------------------------------------------------
-// Decode plan of tb_paged_decode (decode-only steps: row b = sequence b, one new
-// token each). Units are (sequence, kv head) pairs; a unit's positions are cut
-// into tiles of 16. Units are assigned to XCDs by longest-first bin packing on
-// their tile counts. The workers are the waves of the persistent workgroups
-// (worker k = wave k % waves of workgroup k / waves, which runs on XCD
-// (k / waves) % num_xcds); each XCD's tiles (its units back to back) are split
-// evenly over its workers, and each worker's range is cut at unit boundaries
-// into segments. A unit spread over several workers leaves one partial per
-// segment, all on one XCD. The plan carries everything a worker needs before
-// its first load: its segments with their context lengths, and the pool block
-// of every tile it streams (block_tables gathered on the host).
-//
-// Layout (int32):
-//   [0] workers W, [1] segments S, [2] units U, [3] partials, [4] num_xcds,
-//   [5] waves per workgroup, [6] tiles T, [7] pieces grouped per workgroup (0 / 1)
-//   workers [W][4]  = (first segment, segments, first tile, tiles)
-//   segments [S][8] = (unit, first tile, end tile, the group's partial slot or -1,
-//                      context length, the piece's LDS index or -1 for a unit held
-//                      whole by the segment, members | unit partials << 8 for a
-//                      group's leader else 0, the unit's first slot or -1)
-//   units [U][2]    = (partials: 0 for a unit held by one segment, 1 for one held
-//                      by one group, else one per group; first slot or -1)
-//   tiles [T]       = pool block of each tile, in worker order
-namespace {
-constexpr int DECODE_TILE = 16;
-
-int64_t decode_tiles(const int32_t* context_lens, int32_t num_seqs, int32_t num_kv_heads) {
-  int64_t t = 0;
-  for (int b = 0; b < num_seqs; ++b) t += (context_lens[b] + DECODE_TILE - 1) / DECODE_TILE;
-  return t * num_kv_heads;
-}
-
-int64_t plan_ints(int64_t W, int64_t S, int64_t U, int64_t T) { return 8 + 4 * W + 8 * S + 2 * U + T; }
-}  // namespace
-
-extern "C" size_t tb_decode_plan_bytes(const int32_t* context_lens, int32_t num_seqs, int32_t num_kv_heads,
-                                       int32_t workgroups, int32_t waves) {
-  if (num_seqs < 0 || num_kv_heads <= 0 || workgroups <= 0 || waves <= 0) return 0;
-  if (num_seqs > 0 && !context_lens) return 0;
-  for (int b = 0; b < num_seqs; ++b)
-    if (context_lens[b] < 1) return 0;
-  const int64_t U = (int64_t)num_seqs * num_kv_heads, W = (int64_t)workgroups * waves;
-  return (size_t)plan_ints(W, W + U, U, decode_tiles(context_lens, num_seqs, num_kv_heads)) * sizeof(int32_t);
-}
-
-extern "C" int32_t tb_build_decode_plan(const int32_t* context_lens, int32_t num_seqs, int32_t num_kv_heads,
-                                        const int32_t* block_tables, int32_t max_blocks_per_seq,
-                                        int32_t block_size, int64_t num_blocks, int32_t workgroups,
-                                        int32_t waves, int32_t num_xcds, int32_t max_tiles_per_worker,
-                                        int32_t max_segments_per_worker, int32_t group_pieces, int32_t* plan,
-                                        size_t plan_bytes) {
-  if (num_seqs < 0 || num_kv_heads <= 0 || workgroups <= 0 || waves <= 0 || num_xcds <= 0 || num_xcds > 64 || !plan)
-    return TB_ERR_INVALID_ARG;
-  if (workgroups % num_xcds || max_tiles_per_worker <= 0 || max_segments_per_worker <= 0) return TB_ERR_INVALID_ARG;
-  if (num_seqs > 0 && (!context_lens || !block_tables || max_blocks_per_seq <= 0)) return TB_ERR_INVALID_ARG;
-  if (block_size < DECODE_TILE || (block_size & (block_size - 1)) || num_blocks <= 0) return TB_ERR_INVALID_ARG;
-  for (int b = 0; b < num_seqs; ++b)
-    if (context_lens[b] < 1 || (int64_t)context_lens[b] > (int64_t)max_blocks_per_seq * block_size)
-      return TB_ERR_INVALID_ARG;
-  const size_t need = tb_decode_plan_bytes(context_lens, num_seqs, num_kv_heads, workgroups, waves);
-  if (need == 0 || plan_bytes < need) return TB_ERR_INVALID_ARG;
-  if ((int64_t)num_seqs * num_kv_heads >= INDEX_LIMIT || (int64_t)workgroups * waves >= INDEX_LIMIT)
-    return TB_ERR_INVALID_ARG;
-  const int64_t T = decode_tiles(context_lens, num_seqs, num_kv_heads);
-  if (T >= ((int64_t)1 << 31)) return TB_ERR_INVALID_ARG;
-  const int32_t U = num_seqs * num_kv_heads, NX = num_xcds, W = workgroups * waves;
-  const int32_t per = W / NX;                          // workers per XCD
-  auto tiles = [&](int u) { return (context_lens[u / num_kv_heads] + DECODE_TILE - 1) / DECODE_TILE; };
-  int32_t* const workers = plan + 8;
-  int32_t* const segs = workers + 4 * (int64_t)W;
-  // scratch inside the plan until the final layout is known: each unit's XCD sits
-  // where the unit records would go if every worker held one extra segment
-  int32_t* const scratch_xcd = segs + 8 * ((int64_t)W + U);
-
-  // 1. XCDs: longest unit first (stable), onto the least loaded XCD (lowest index among equals)
-  int64_t load[64];
-  for (int x = 0; x < NX; ++x) load[x] = 0;
-  int32_t max_t = 0;
-  for (int u = 0; u < U; ++u) max_t = tiles(u) > max_t ? tiles(u) : max_t;
-  for (int t = max_t; t >= 1; --t)
-    for (int u = 0; u < U; ++u) {
-      if (tiles(u) != t) continue;
-      int best = 0;
-      for (int x = 1; x < NX; ++x)
-        if (load[x] < load[best]) best = x;
-      scratch_xcd[2 * u] = best;
-      load[best] += t;
-    }
-
-  // 2. segments in worker order: worker k (workgroup g = k / waves, XCD x = g % NX)
-  // takes the j-th of XCD x's `per` even ranges of its tiles, j = (g / NX) * waves + k % waves
-  int32_t cur_u[64], cur_t[64];
-  auto next_unit = [&](int x, int from) {
-    for (int v = from; v < U; ++v)
-      if (scratch_xcd[2 * v] == x) return v;
-    return U;
-  };
-  for (int x = 0; x < NX; ++x) {
-    cur_u[x] = next_unit(x, 0);
-    cur_t[x] = 0;
-  }
-  int64_t S = 0, tile_at = 0;
-  for (int k = 0; k < W; ++k) {
-    const int g = k / waves, x = g % NX, j = (g / NX) * waves + k % waves;
-    const int64_t lo = load[x] * j / per, hi = load[x] * (j + 1) / per;
-    if (hi - lo > max_tiles_per_worker) return TB_ERR_UNSUPPORTED;
-    int32_t* const wr = workers + 4 * (int64_t)k;
-    wr[0] = (int32_t)S;
-    wr[2] = (int32_t)tile_at;
-    wr[3] = (int32_t)(hi - lo);
-    tile_at += hi - lo;
-    int64_t left = hi - lo;
-    int nseg = 0;
-    while (left > 0) {
-      const int u = cur_u[x];
-      const int take = (int)(tiles(u) - cur_t[x] < left ? tiles(u) - cur_t[x] : left);
-      int32_t* sg = segs + 8 * S++;
-      sg[0] = u;
-      sg[1] = cur_t[x];
-      sg[2] = cur_t[x] + take;
-      sg[3] = 0;
-      sg[4] = context_lens[u / num_kv_heads];
-      sg[5] = sg[6] = sg[7] = 0;
-      ++nseg;
-      cur_t[x] += take;
-      left -= take;
-      if (cur_t[x] == tiles(u)) {
-        cur_u[x] = next_unit(x, u + 1);
-        cur_t[x] = 0;
-      }
-    }
-    if (nseg > max_segments_per_worker) return TB_ERR_UNSUPPORTED;
-    wr[1] = nseg;
-  }
-
-  // 3. pieces. A unit cut into several segments leaves one partial per segment; only a
-  // worker's first and last segments can be such pieces. With group_pieces, the pieces
-  // of one workgroup (its waves' first and last segments, in wave order) that belong to
-  // one unit are consecutive: they form a group, merged in LDS by its first member (the
-  // leader); without, every piece is a group of its own.
-  // A group that holds the whole unit writes the output; otherwise it leaves one
-  // partial in the workspace (a slot), and the unit's partials (one per group) are
-  // merged by the group whose partial arrives last. The unit records follow the S
-  // segments (the XCD assignment is no longer needed).
-  int32_t* const rec = segs + 8 * S;
-  int32_t* const tile_blk = rec + 2 * (int64_t)U;
-  std::vector<int32_t> nseg_u(U, 0), ngrp_u(U, 0);
-  for (int64_t i = 0; i < S; ++i) ++nseg_u[segs[8 * i]];
-  // the workgroup's pieces in order: (segment, LDS index)
-  auto wg_pieces = [&](int g, int32_t* out) {
-    int n = 0;
-    for (int w = 0; w < waves; ++w) {
-      const int32_t* wr = workers + 4 * ((int64_t)g * waves + w);
-      const int s0 = wr[0], ns = wr[1];
-      for (int e = 0; e < 2 && ns > 0; ++e) {
-        if (e == 1 && ns < 2) break;
-        const int sg = e == 0 ? s0 : s0 + ns - 1;
-        if (nseg_u[segs[8 * (int64_t)sg]] > 1) out[n++] = sg;
-      }
-    }
-    return n;
-  };
-  std::vector<int32_t> wp(2 * (size_t)waves);
-  for (int g = 0; g < workgroups; ++g) {
-    const int n = wg_pieces(g, wp.data());
-    for (int k = 0; k < n; ++k)
-      if (!group_pieces || k == 0 || segs[8 * (int64_t)wp[k]] != segs[8 * (int64_t)wp[k - 1]])
-        ++ngrp_u[segs[8 * (int64_t)wp[k]]];
-  }
-  int32_t pieces = 0;
-  for (int u = 0; u < U; ++u) {
-    if (ngrp_u[u] > 255) return TB_ERR_UNSUPPORTED;   // arrival counts are 8-bit fields
-    rec[2 * u] = nseg_u[u] > 1 ? ngrp_u[u] : 0;
-    rec[2 * u + 1] = ngrp_u[u] > 1 ? pieces : -1;
-    if (ngrp_u[u] > 1) pieces += ngrp_u[u];
-  }
-  for (int64_t i = 0; i < S; ++i) {               // segments held whole by one worker
-    segs[8 * i + 3] = -1;
-    segs[8 * i + 5] = -1;
-    segs[8 * i + 6] = 0;
-    segs[8 * i + 7] = -1;
-  }
-  std::vector<int32_t> next_slot(U);
-  for (int u = 0; u < U; ++u) next_slot[u] = rec[2 * u + 1];
-  for (int g = 0; g < workgroups; ++g) {
-    const int n = wg_pieces(g, wp.data());
-    for (int k = 0; k < n;) {
-      const int u = segs[8 * (int64_t)wp[k]];
-      int m = 1;
-      while (group_pieces && k + m < n && segs[8 * (int64_t)wp[k + m]] == u) ++m;
-      const int32_t slot = ngrp_u[u] > 1 ? next_slot[u]++ : -1;
-      for (int j = 0; j < m; ++j) {
-        int32_t* sg = segs + 8 * (int64_t)wp[k + j];
-        sg[3] = slot;                            // the group's partial, or -1: the group writes the output
-        sg[5] = k + j;                           // LDS index of the piece's state
-        sg[6] = j == 0 ? (m | (ngrp_u[u] << 8)) : 0;   // leader: members, and the unit's partials
-        sg[7] = rec[2 * u + 1];                  // the unit's first slot
-      }
-      k += m;
-    }
-  }
-
-  // 4. the pool block of every tile, in worker order (a tile of 16 lies in one block)
-  int log2_bs = 0;
-  while ((1 << log2_bs) < block_size) ++log2_bs;
-  int64_t at = 0;
-  for (int64_t i = 0; i < S; ++i) {
-    const int32_t* sg = segs + 8 * i;
-    const int b = sg[0] / num_kv_heads;
-    for (int t = sg[1]; t < sg[2]; ++t) {
-      const int32_t blk = block_tables[(int64_t)b * max_blocks_per_seq + (((int64_t)DECODE_TILE * t) >> log2_bs)];
-      if (blk < 0 || blk >= num_blocks) return TB_ERR_INDEX;
-      tile_blk[at++] = blk;
-    }
-  }
-  plan[0] = W;
-  plan[1] = (int32_t)S;
-  plan[2] = U;
-  plan[3] = pieces;
-  plan[4] = NX;
-  plan[5] = waves;
-  plan[6] = (int32_t)T;
-  plan[7] = group_pieces ? 1 : 0;
-  return TB_OK;
-}
-
-// ---------------------------------------------------------------------------
 // Slot map of tb_paged_attention_merged: a unit is (row group, kv head), a row
 // group being the work items that share their first row (the partitions of
 // that row, or of a run of decode rows of one sequence). Units are packed onto

@@ -80,9 +80,10 @@ class StepMetadata:
     rows_are_seqs: bool = False  # decode-only with row b = sequence b (the decode kernel's layout)
     decode_plan_np: np.ndarray | None = None
     decode_workgroups: int = 0
+    decode_waves: int = 0
+    decode_stride: int = 0
     decode_pieces: int = 0
     decode_units: int = 0
-    decode_merge_in_kernel: bool = False
     decode_plan: torch.Tensor | None = None
     num_blocks: int = 0          # blocks of the pool the step's tables index
     # slot map of the work-item kernel with split rows merged inside the launch
@@ -415,78 +416,86 @@ def pack_decode_step(h: np.ndarray, offs: np.ndarray, Bp: int, max_nb: int, cont
 
 
 # ---- decode plans (tb_paged_decode) ---------------------------------------------
-def decode_limits(num_heads: int, num_kv_heads: int, head_dim: int):
-    """(max tiles, max segments) per worker (wave) and waves per workgroup of the
-    decode kernel for this geometry, or None when the kernel does not serve it."""
+def decode_defaults(head_dim: int):
+    """(waves per workgroup, per-unit cost) the decode kernel uses for this head dim by
+    default, or None when it does not serve the head dim."""
     import ctypes
 
     from . import _lib
 
-    t, sg, w = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
-    st = _lib.lib().tb_decode_limits(num_heads, num_kv_heads, head_dim, ctypes.byref(t), ctypes.byref(sg),
-                                     ctypes.byref(w))
-    return (t.value, sg.value, w.value) if st == 0 else None
+    w, uc = ctypes.c_int32(), ctypes.c_int32()
+    st = _lib.lib().tb_decode_defaults(head_dim, ctypes.byref(w), ctypes.byref(uc))
+    return (w.value, uc.value) if st == 0 else None
 
 
-def build_decode_plan(context_lens, block_tables, *, block_size: int, num_blocks: int, num_heads: int,
-                      num_kv_heads: int, head_dim: int, workgroups: int, num_xcds: int,
-                      group_pieces: bool = True) -> tuple[np.ndarray, int] | None:
+def build_decode_plan(context_lens, block_tables, *, block_size: int, num_blocks: int, num_kv_heads: int,
+                      head_dim: int, workgroups: int, num_xcds: int, waves: int | None = None,
+                      unit_cost: int | None = None) -> tuple[np.ndarray, int, int, int] | None:
     """tb_build_decode_plan for a decode step (row b = sequence b with context_lens[b]
-    positions, block_tables[b] its blocks): the int32 plan and the workgroup count it
-    needs, starting from ``workgroups`` and doubling while a worker's share exceeds
-    its LDS areas. None when the geometry is not served by the decode kernel."""
+    positions, block_tables[b] its blocks): (int32 plan, waves, stride, partial slots),
+    or None when the kernel does not serve the step (head dim, or a unit cut over more
+    than 255 workers)."""
     import ctypes
 
     from . import _lib
 
-    lim = decode_limits(num_heads, num_kv_heads, head_dim)
-    if lim is None:
+    dflt = decode_defaults(head_dim)
+    if dflt is None:
         return None
-    tmax, smax, waves = lim
+    waves = dflt[0] if waves is None else int(waves)
+    unit_cost = dflt[1] if unit_cost is None else int(unit_cost)
+    L = _lib.lib()
+    if not L.tb_decode_variant_supported(head_dim, waves):
+        raise ValueError(f"the decode kernel has no {waves}-wave variant for head_dim {head_dim}")
     ctx = np.ascontiguousarray(np.asarray(context_lens, dtype=np.int32).reshape(-1))
     B = int(ctx.size)
-    tables = np.ascontiguousarray(np.asarray(block_tables, dtype=np.int32).reshape(B, -1) if B else
-                                  np.zeros((1, 1), dtype=np.int32))
-    L = _lib.lib()
+    if B == 0 or np.any(ctx <= 0):
+        raise ValueError("a decode plan needs >= 1 sequence, each with >= 1 position")
+    tables = np.ascontiguousarray(np.asarray(block_tables, dtype=np.int32).reshape(B, -1))
     vp = lambda a: a.ctypes.data_as(ctypes.c_void_p)
-    G = int(workgroups)
-    for _ in range(8):
-        nbytes = int(L.tb_decode_plan_bytes(vp(ctx), B, num_kv_heads, G, waves))
-        if nbytes == 0:
-            raise ValueError("invalid decode step for a plan (every context must hold >= 1 position)")
-        plan = np.zeros(nbytes // 4, dtype=np.int32)
-        st = L.tb_build_decode_plan(vp(ctx), B, num_kv_heads, vp(tables), tables.shape[1], block_size, num_blocks,
-                                    G, waves, num_xcds, tmax, smax, int(group_pieces), vp(plan), nbytes)
-        if st == 0:
-            return plan, G
-        if st != _lib.TB_ERR_UNSUPPORTED:
-            _lib.check(st, "tb_build_decode_plan")
-        G *= 2
-    return None
+    me, pieces = ctypes.c_int32(), ctypes.c_int32()
+    st = L.tb_decode_plan_shape(vp(ctx), B, num_kv_heads, head_dim, workgroups, waves, num_xcds, unit_cost,
+                                ctypes.byref(me), ctypes.byref(pieces))
+    if st == _lib.TB_ERR_UNSUPPORTED:
+        return None
+    _lib.check(st, "tb_decode_plan_shape")
+    stride = max(2, (me.value + 1) // 2 * 2)
+    words = int(L.tb_decode_plan_words(workgroups * waves, stride))
+    plan = np.zeros(words, dtype=np.int32)
+    st = L.tb_build_decode_plan(vp(ctx), B, num_kv_heads, head_dim, vp(tables), tables.shape[1], block_size,
+                                num_blocks, workgroups, waves, num_xcds, unit_cost, stride, vp(plan), words)
+    if st == _lib.TB_ERR_UNSUPPORTED:
+        return None
+    if st == _lib.TB_ERR_INDEX:
+        raise IndexError("a block table is too short for its context, or holds a block outside the pool")
+    _lib.check(st, "tb_build_decode_plan")
+    return plan, waves, stride, pieces.value
 
 
 def attach_decode_plan(meta: StepMetadata, *, num_heads: int, num_kv_heads: int, head_dim: int,
-                       dtype: torch.dtype, workgroups: int, num_xcds: int, merge_in_kernel: bool,
-                       group_pieces: bool = True) -> bool:
+                       dtype: torch.dtype, workgroups: int, num_xcds: int, waves: int | None = None,
+                       unit_cost: int | None = None) -> bool:
     """Give a decode-only step (row b = sequence b) the plan of the decode kernel, to be
     uploaded with the rest of its metadata by ``meta.to``. Returns whether it applies:
-    16-bit rows, head_dim 64 / 128, at most 8 query heads per kv head, blocks of >= 16."""
+    16-bit rows, head_dim 64 / 128, at most 8 query heads per kv head, at most 16 kv
+    heads, blocks of >= 16 positions."""
     if (not meta.rows_are_seqs or dtype not in (torch.float16, torch.bfloat16) or meta.block_size < 16
-            or meta.device_buffer is not None or meta.num_blocks <= 0):
+            or meta.device_buffer is not None or meta.num_blocks <= 0 or num_heads % num_kv_heads
+            or num_heads // num_kv_heads > 8 or num_kv_heads > 16):
         return False
     B = meta.num_seqs
-    ctx = meta.row_ctx_np[:B].astype(np.int32)
-    got = build_decode_plan(ctx, meta.block_tables_np[:B], block_size=meta.block_size, num_blocks=meta.num_blocks,
-                            num_heads=num_heads, num_kv_heads=num_kv_heads, head_dim=head_dim,
-                            workgroups=workgroups, num_xcds=num_xcds, group_pieces=group_pieces)
+    got = build_decode_plan(meta.row_ctx_np[:B], meta.block_tables_np[:B], block_size=meta.block_size,
+                            num_blocks=meta.num_blocks, num_kv_heads=num_kv_heads, head_dim=head_dim,
+                            workgroups=workgroups, num_xcds=num_xcds, waves=waves, unit_cost=unit_cost)
     if got is None:
         return False
-    plan, G = got
+    plan, w, stride, pieces = got
     meta.decode_plan_np = plan
-    meta.decode_workgroups = G
-    meta.decode_units = int(plan[2])
-    meta.decode_pieces = int(plan[3])
-    meta.decode_merge_in_kernel = bool(merge_in_kernel)
+    meta.decode_workgroups = workgroups
+    meta.decode_waves = w
+    meta.decode_stride = stride
+    meta.decode_units = B * num_kv_heads
+    meta.decode_pieces = pieces
     return True
 
 

@@ -161,11 +161,11 @@ def workspace_for(meta: StepMetadata, num_heads: int, head_dim: int,
 
 
 class DecodeDevice:
-    """Launch facts of the decode kernel on one GPU: one persistent workgroup (four
-    worker waves) per CU, and the XCD count under which partials merge inside the launch. The XCD count is
-    the CU count / 32 (the CUs of one XCD) and is used only if a probe launch shows
-    workgroup g running on XCD g mod that count, with distinct XCDs in between;
-    otherwise the plan ignores XCDs and a second kernel merges the partials."""
+    """Launch facts of the decode kernel on one GPU: one workgroup per CU, and the XCD
+    count under which a unit's partials are written and merged inside one XCD. The XCD
+    count is the CU count / 32 (the CUs of one XCD); the decode kernel is used only if
+    a probe launch shows workgroup g running on XCD g mod that count, with distinct
+    XCDs in between (merge_in_kernel), and steps go to the work-item kernel otherwise."""
 
     def __init__(self, device: torch.device):
         props = torch.cuda.get_device_properties(device)
@@ -204,37 +204,39 @@ def decode_device(device: torch.device) -> DecodeDevice:
     return d
 
 
-# Decode-only steps with at least this many K/V bytes per call go to the persistent
-# decode kernel (tb_paged_decode). On MI355X it streams about 6.6 TB/s against about
-# 5.0 TB/s for the work-item kernel, but its fixed cost per call (the plan and first
-# tiles at the start, the piece merges at the end) is about 12 us against about 6 us;
-# the two meet near 134 MB (a 72 MB step: 23 us against 20 us; an 8.9 GB step:
-# 1.35 ms against 1.79 ms).
-DECODE_KERNEL_MIN_BYTES = 128 << 20
+# Decode-only steps with at least this many K/V bytes per call go to the streaming
+# decode kernel (tb_paged_decode); smaller steps to the work-item kernel, whose
+# fixed cost per call is lower.
+DECODE_KERNEL_MIN_BYTES = 32 << 20
 
 
 def decode_kernel_preferred(meta: StepMetadata, *, num_kv_heads: int, head_dim: int, dtype: torch.dtype) -> bool:
-    """Whether a step is served faster by the persistent decode kernel: a decode-only
+    """Whether a step is served faster by the streaming decode kernel: a decode-only
     step (row b = sequence b) in fp16 / bf16 reading at least DECODE_KERNEL_MIN_BYTES
-    of K/V. The plan must then be attached (attach_decode_plan) before meta.to()."""
+    of K/V, with at least 32 (sequence, kv head) units (a unit stays on one XCD, so
+    fewer units leave XCDs idle). The plan must then be attached (attach_decode_plan)
+    before meta.to()."""
     if not meta.rows_are_seqs or dtype not in (torch.float16, torch.bfloat16):
+        return False
+    if meta.num_seqs * num_kv_heads < 32:
         return False
     kv_bytes = int(meta.row_ctx_np[:meta.num_seqs].astype(np.int64).sum()) * num_kv_heads * head_dim * 2 * 2
     return kv_bytes >= DECODE_KERNEL_MIN_BYTES
 
 
 def attach_decode_plan(meta: StepMetadata, *, num_heads: int, num_kv_heads: int, head_dim: int,
-                       dtype: torch.dtype, device: torch.device, merge_in_kernel: bool | None = None,
-                       group_pieces: bool = True) -> bool:
-    """metadata.attach_decode_plan with this device's workgroups and XCDs (partials merged
-    inside the launch when the device allows it, unless merge_in_kernel is False)."""
+                       dtype: torch.dtype, device: torch.device, waves: int | None = None,
+                       unit_cost: int | None = None) -> bool:
+    """metadata.attach_decode_plan with this device's workgroups and XCDs; False (the
+    step stays with the work-item kernel) when the device's workgroup placement is not
+    the one the kernel's in-XCD merges assume."""
     from .metadata import attach_decode_plan as attach
 
     d = decode_device(device)
-    merge = d.merge_in_kernel if merge_in_kernel is None else (bool(merge_in_kernel) and d.merge_in_kernel)
+    if not d.merge_in_kernel or d.num_xcds <= 1:
+        return False
     return attach(meta, num_heads=num_heads, num_kv_heads=num_kv_heads, head_dim=head_dim, dtype=dtype,
-                  workgroups=d.workgroups, num_xcds=d.num_xcds if merge else 1, merge_in_kernel=merge,
-                  group_pieces=group_pieces)
+                  workgroups=d.workgroups, num_xcds=d.num_xcds, waves=waves, unit_cost=unit_cost)
 
 
 def attach_xcd_slot_map(meta: StepMetadata, *, num_heads: int, num_kv_heads: int, dtype: torch.dtype,
@@ -329,9 +331,9 @@ def paged_decode(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, num
         raise ValueError("decode buffers too small for the step")
     st = _lib.lib().tb_paged_decode(
         q.data_ptr(), qs, pool.data_ptr(), nb, out.data_ptr(), os_, B, meta.decode_plan.data_ptr(),
-        meta.decode_workgroups, meta.decode_units, num_heads, hkv, d, bs, float(scale), _lib.DTYPE_CODE[q.dtype],
-        ksp, ks, vsp, vs, bufs.pieces.data_ptr(), bufs.pieces.numel(), meta.decode_pieces,
-        bufs.arrivals.data_ptr(), bufs.units, int(meta.decode_merge_in_kernel), dev.violations.data_ptr(),
+        meta.decode_workgroups, meta.decode_waves, meta.decode_stride, num_heads, hkv, d, bs, float(scale),
+        _lib.DTYPE_CODE[q.dtype], ksp, ks, vsp, vs, bufs.pieces.data_ptr(), bufs.pieces.numel(), meta.decode_pieces,
+        bufs.arrivals.data_ptr(), bufs.units, dev.violations.data_ptr(),
         None if rope is None else rope.cos.data_ptr(), None if rope is None else rope.sin.data_ptr(),
         0 if rope is None else rope.max_position, _lib.stream_handle(q.device))
     _lib.check(st, "tb_paged_decode")
