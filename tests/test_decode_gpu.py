@@ -172,6 +172,35 @@ def test_workspace_contents_before_the_call_never_reach_the_output():
         assert torch.equal(_bits(o), _bits(outs[0]))
 
 
+def test_drop_in_cache_runs_the_decode_kernel_on_large_steps():
+    # the reference's call sequence (write, then attention) and the fused
+    # decode_step both attach the streaming kernel's plan on the headline step
+    from tinybatch_amd.kv_cache import PagedKVCache
+
+    wl = make_decode_workload("qwen-fp16-b64")
+    c = dict(pool=wl.pool, tables=wl.block_tables, ctx=wl.context_lens, q=wl.q, k=wl.k_new, v=wl.v_new,
+             NB=wl.num_blocks, BS=16, Hq=14, Hkv=2, D=64, dtype=torch.float16)
+    want, want_pool = oracle(c)
+    B = len(c["ctx"])
+    pos = torch.tensor([x - 1 for x in c["ctx"]], dtype=torch.int64, device=DEV)
+    slices = [(b, b + 1) for b in range(B)]
+    q, k, v = c["q"].to(DEV), c["k"].to(DEV), c["v"].to(DEV)
+    for fused in (False, True):
+        cache = PagedKVCache(1, c["NB"], 16, 2, 64, DEV, torch.float16)
+        cache.pools[0].copy_(c["pool"].to(DEV))
+        if fused:
+            meta = cache.step_metadata(pos, slices, c["tables"], c["ctx"], num_heads=14)
+            out = cache.decode_step(0, q, k, v, meta)
+        else:
+            cache.write(0, k, v, pos, slices, c["tables"])
+            out = cache.attention(0, q, pos, slices, c["tables"], c["ctx"])
+            meta = cache.step_metadata(pos, slices, c["tables"], c["ctx"], cache.rows_per_item(14))
+        torch.cuda.synchronize()
+        assert meta.decode_plan is not None, f"fused={fused}: the step did not take the decode kernel"
+        assert torch.equal(_bits(cache.pools[0].cpu()), _bits(want_pool)), f"fused={fused}"
+        torch.testing.assert_close(out.cpu().float(), want.float(), **TOL)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_fused_rope_equals_rotating_first(dtype):
     c = case(13, 24, 14, 2, 64, 16, dtype, nan_stale=False)

@@ -54,7 +54,7 @@ class PagedKVCache:
 
     # ---- per-step metadata -------------------------------------------------
     def step_metadata(self, positions, seq_slices, block_tables, context_lens=None,
-                      rows_per_item: int = 1, host_positions=None) -> StepMetadata:
+                      rows_per_item: int = 1, host_positions=None, num_heads: int | None = None) -> StepMetadata:
         """Build (or reuse) the step's device metadata.
 
         Every layer of a forward pass passes the same argument objects, so the
@@ -64,7 +64,10 @@ class PagedKVCache:
         and context lengths compare equal. write() (no context lengths) may
         reuse an entry built for attention(). ``host_positions`` (the same
         positions as a host list) spares the device-to-host copy of a device
-        ``positions`` tensor; the entry is still keyed on ``positions``.
+        ``positions`` tensor; the entry is still keyed on ``positions``. With
+        ``num_heads`` (query heads), a decode-only step that the streaming decode
+        kernel serves faster (ops.decode_kernel_preferred) also gets its plan, and
+        attention() / decode_step() with this metadata then run that kernel.
         """
         pos_key = (positions, positions._version) if isinstance(positions, torch.Tensor) else list(positions)
         for e in self._meta_cache:
@@ -79,6 +82,11 @@ class PagedKVCache:
                                    block_size=self.block_size, num_blocks=self.num_blocks,
                                    partition_tokens=self.partition_tokens, rows_per_item=rows_per_item,
                                    tile_prefill=tile)
+        if (num_heads is not None and context_lens is not None and self.device.type == "cuda"
+                and ops.decode_kernel_preferred(meta, num_kv_heads=self.n_kv_heads, head_dim=self.head_dim,
+                                                dtype=self.dtype)):
+            ops.attach_decode_plan(meta, num_heads=num_heads, num_kv_heads=self.n_kv_heads,
+                                   head_dim=self.head_dim, dtype=self.dtype, device=self.device)
         meta.to(self.device)
         entry = {"pos": pos_key, "slices": [tuple(x) for x in seq_slices],
                  "tables": [list(t) for t in block_tables],
@@ -121,7 +129,7 @@ class PagedKVCache:
         ``rope``, q is the projection before rotation (rotated inside the kernels)."""
         hq = num_heads if num_heads is not None else q.shape[1]
         rows = self.rows_per_item(hq)
-        meta = self._lookup_or_build(positions, seq_slices, block_tables, context_lens, q.shape[0], rows)
+        meta = self._lookup_or_build(positions, seq_slices, block_tables, context_lens, q.shape[0], rows, hq)
         return ops.paged_attention(q, self.pools[layer], meta, num_heads=hq, scale=scale, out=out, rope=rope)
 
     def decode_step(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, meta: StepMetadata,
@@ -146,8 +154,9 @@ class PagedKVCache:
             ops.block_scatter(st, pool, blocks)
 
     def _lookup_or_build(self, positions, seq_slices, block_tables, context_lens, num_tokens,
-                         rows_per_item: int = 1) -> StepMetadata:
-        meta = self.step_metadata(positions, seq_slices, block_tables, context_lens, rows_per_item)
+                         rows_per_item: int = 1, num_heads: int | None = None) -> StepMetadata:
+        meta = self.step_metadata(positions, seq_slices, block_tables, context_lens, rows_per_item,
+                                  num_heads=num_heads)
         if meta.num_tokens != num_tokens:
             raise ValueError(f"{num_tokens} tokens given, positions describe {meta.num_tokens}")
         return meta
