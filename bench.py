@@ -226,9 +226,18 @@ def bench_mixed(args, dev) -> int:
     Hq = wl.num_heads
     results = {}
     for which, w in (("step", wl), ("prefill", wl.part("prefill")), ("decode", wl.part("decode"))):
+        # whole prefill sequences go to tb_paged_prefill in a prefill-only step; a
+        # step with decode rows keeps the one launch of tiles and decode items
+        route = None if (which != "prefill" or args.no_tiles or args.no_stream_prefill) else ops.prefill_route(
+            wl.dtype, wl.num_heads, wl.num_kv_heads, wl.head_dim, dev)
         meta = build_step_metadata(w.positions, w.seq_slices, w.block_tables, w.context_lens,
                                    block_size=w.block_size, num_blocks=w.num_blocks, partition_tokens=P,
-                                   rows_per_item=rows, tile_prefill=not args.no_tiles).to(dev)
+                                   rows_per_item=rows, tile_prefill=not args.no_tiles, prefill_route=route)
+        if which == "decode" and args.decode_stream and ops.decode_kernel_preferred(
+                meta, num_kv_heads=wl.num_kv_heads, head_dim=wl.head_dim, dtype=wl.dtype, min_bytes=0):
+            ops.attach_decode_plan(meta, num_heads=Hq, num_kv_heads=wl.num_kv_heads, head_dim=wl.head_dim,
+                                   dtype=wl.dtype, device=dev)
+        meta = meta.to(dev)
         q, k, v = w.q.to(dev), w.k_new.to(dev), w.v_new.to(dev)
         out = torch.empty(w.num_tokens, Hq * w.head_dim, dtype=w.dtype, device=dev)
         ws = ops.workspace_for(meta, Hq, w.head_dim, dev)
@@ -291,7 +300,8 @@ def bench_mixed(args, dev) -> int:
         "roofline": {"bound": "mfma", "achieved": round(pre_tflops, 2), "peak": MFMA_PEAK_TFLOPS_16,
                      "unit": "TFLOP/s", "frac": round(pre_tflops / MFMA_PEAK_TFLOPS_16, 4), "traffic": None,
                      "kernel": ("paged_attn_mfma_kernel + combine_partials_kernel" if args.no_tiles
-                                else "paged_prefill_mfma_kernel") + " (prefill rows)"},
+                                else "paged_prefill_mfma_kernel" if args.no_stream_prefill
+                                else "paged_prefill_stream_kernel") + " (prefill rows)"},
         "decode_roofline": {"bound": "hbm", "achieved": round(dec_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                             "frac": round(dec_gbs / HBM_PEAK_GBS, 4)},
         "copy_roofline": {"bound": "hbm", "achieved": round(copy_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -410,6 +420,10 @@ def main() -> int:
     ap.add_argument("--combine", action="store_true",
                     help="work-item kernel: merge split rows with the separate combine kernel, not inside the launch")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--decode-stream", action="store_true",
+                    help="mixed workload: the decode rows through the streaming decode kernel")
+    ap.add_argument("--no-stream-prefill", action="store_true",
+                    help="mixed workload: prefill sequences through the tile kernel, not tb_paged_prefill")
     ap.add_argument("--cpu-reps", type=int, default=5)
     ap.add_argument("--cpu-budget", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (profiling runs)")

@@ -208,6 +208,47 @@ int32_t tb_build_step_metadata(const int32_t* query_start_loc, int32_t num_seqs,
 #define TB_PREFILL_TILE_ROWS 64
 #define TB_PREFILL_TILE_PARTITION 1024
 
+/* K2 for whole prefill sequences whose context fits in one workgroup's LDS
+ * (reference src/tinybatch/model.py:130-147 for the rows of those sequences:
+ * gather, repeat_interleave, the causal mask of model.py:139-146 and SDPA).
+ * fp16 / bf16, head_dim 64 or 128, num_heads / num_kv_heads <=
+ * tb_prefill_stream_max_group (8 at head dim 64, 4 at 128), block_size a
+ * power of two >= 16, context (pos0 + new rows) <= tb_prefill_stream_max_context
+ * (TB_ERR_UNSUPPORTED otherwise: use tb_paged_attention's tiles). Each sequence's
+ * K/V range moves into LDS once per (kv head, pair of 16-row blocks p and
+ * nb-1-p) and the kv head's query heads share it; every row's output is written
+ * whole (no workspace). The rows it serves must not also be given to
+ * tb_paged_attention. The K/V of the step's new rows must already be in the pool
+ * (append first).
+ *   work: tb_build_prefill_work's list (device memory), num_work entries;
+ *     max_tiles: the value the builder returned.
+ * q, out, strides, scale, dtype, rope: as tb_paged_attention. */
+#define TB_PREFILL_STREAM_LDS (144 * 1024)
+int32_t tb_paged_prefill(const void* q, int64_t q_row_stride, const void* pool, int64_t num_blocks,
+                         void* out, int64_t out_row_stride, const int32_t* block_tables,
+                         int32_t max_blocks_per_seq, const int32_t* work, int32_t num_work,
+                         int32_t max_tiles, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                         int32_t block_size, float scale, int32_t dtype, const float* rope_cos,
+                         const float* rope_sin, int32_t rope_max_position, hipStream_t stream);
+/* The longest context (positions) and the most query heads per kv head
+ * tb_paged_prefill serves at a head dim (0: none). */
+int32_t tb_prefill_stream_max_context(int32_t head_dim);
+int32_t tb_prefill_stream_max_group(int32_t head_dim);
+/* Work entries for num_seqs prefill sequences (host arrays: first row of the
+ * sequence in q / out, its index into block_tables, position of its first new
+ * row, new rows >= 1): sum over sequences of ceil(ceil(new_rows / 16) / 2) *
+ * num_kv_heads, or -1 for bad arguments. */
+int32_t tb_prefill_work_count(const int32_t* new_rows, int32_t num_seqs, int32_t num_kv_heads);
+/* The work list (host memory, int32 x4 per entry: first row, sequence, pos0,
+ * new rows | pair << 16 | kv head << 24) and the most 16-position tiles one
+ * entry holds (*max_tiles). The entries of one (sequence, kv head), which read
+ * the same K/V, are placed where entry g runs on XCD g % num_xcds (1: no
+ * placement), longest contexts first. Nothing is allocated. */
+int32_t tb_build_prefill_work(const int32_t* first_row, const int32_t* seq_index, const int32_t* pos0,
+                              const int32_t* new_rows, int32_t num_seqs, int32_t num_kv_heads,
+                              int32_t head_dim, int32_t num_xcds, int32_t* work, int32_t capacity,
+                              int32_t* max_tiles);
+
 size_t tb_paged_attention_workspace_bytes(int32_t total_partitions, int32_t num_heads,
                                           int32_t head_dim);
 

@@ -1,0 +1,133 @@
+"""tb_paged_prefill (whole prefill sequences; a workgroup per sequence, kv head and
+pair of 16-row blocks holds the K/V range in LDS, shared by the kv head's query
+heads) against the oracle through the C ABI. Bar: attention within 2e-2 at fp16 /
+bf16 against the oracle in the same dtype.
+
+Cases: 1, 2, 4, 7 and 8 query heads per kv head at head dim 64, 1, 2 and 4 at 128;
+block sizes 16 to 64; new-row counts that are not multiples of 16 (a lone middle
+block, a last block of one row); cached prefixes (pos0 > 0); contexts at the
+longest the kernel serves; stale NaN slots past every context; a step mixing these
+sequences with decode rows and with sequences past the kernel's limit (which keep
+the tiles); the config-4 mixed step; fused RoPE equal to rotating q first."""
+import pytest
+import torch
+
+from oracle import reference_path as ref
+from tinybatch_amd import layer_ops, ops
+from tinybatch_amd.metadata import build_step_metadata
+from tinybatch_amd.model import rope_tables
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda", 0)
+TOL = dict(atol=2e-2, rtol=2e-2)
+
+
+def _bits(t):
+    return t.contiguous().view(torch.int16)
+
+
+def case(seed, Hq, Hkv, D, BS, dtype, qlens, cached, nan_tail=True):
+    g = torch.Generator().manual_seed(seed)
+    need = [(c + n + BS - 1) // BS for c, n in zip(cached, qlens)]
+    NB = sum(need) + 3
+    pool = torch.randn(NB, 2, Hkv, BS, D, generator=g).to(dtype)
+    perm = torch.randperm(NB, generator=g).tolist()
+    tables, slices, ctx, pos, at, t = [], [], [], [], 0, 0
+    for c, n, nb in zip(cached, qlens, need):
+        tables.append(perm[at:at + nb])
+        at += nb
+        slices.append((t, t + n))
+        t += n
+        ctx.append(c + n)
+        pos.extend(range(c, c + n))
+    if nan_tail:   # stale slots past every context, and unused blocks, hold NaN
+        for table, c in zip(tables, ctx):
+            if c % BS:
+                pool[table[-1], :, :, c % BS:] = float("nan")
+        for b in perm[at:]:
+            pool[b] = float("nan")
+    q = torch.randn(t, Hq, D, generator=g).to(dtype)
+    return dict(pool=pool, tables=tables, slices=slices, ctx=ctx, pos=pos, q=q, NB=NB, Hq=Hq, Hkv=Hkv, D=D, BS=BS,
+                dtype=dtype)
+
+
+def metadata(c, route=True):
+    dt, Hq, Hkv, D = c["dtype"], c["Hq"], c["Hkv"], c["D"]
+    r = ops.prefill_route(dt, Hq, Hkv, D) if route else None
+    assert not route or r is not None
+    return build_step_metadata(c["pos"], c["slices"], c["tables"], c["ctx"], block_size=c["BS"], num_blocks=c["NB"],
+                               partition_tokens=ops.partition_tokens(dt, D),
+                               rows_per_item=ops.rows_per_item(dt, Hq, Hkv), tile_prefill=True,
+                               prefill_route=r).to(DEV)
+
+
+def check(c, min_work=1):
+    want = ref.attention(c["q"], c["pool"], c["slices"], c["tables"], c["ctx"], c["Hq"], c["Hkv"])
+    meta = metadata(c)
+    assert meta.num_prefill_work >= min_work
+    out = ops.paged_attention(c["q"].to(DEV), c["pool"].to(DEV), meta, num_heads=c["Hq"])
+    torch.cuda.synchronize()
+    got = out.cpu()
+    assert torch.isfinite(got).all()
+    torch.testing.assert_close(got.float(), want.float(), **TOL)
+    return meta
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("Hq,Hkv,D", [(14, 2, 64), (8, 8, 64), (16, 2, 64), (8, 2, 64), (16, 8, 64),
+                                      (32, 8, 128), (4, 2, 128), (8, 8, 128)])
+@pytest.mark.parametrize("BS", [16, 64])
+def test_geometries_rows_and_prefixes(Hq, Hkv, D, BS, dtype):
+    # new rows 16 .. 100 (lone middle blocks, a last block of one row), cached
+    # prefixes, and two decode rows in the same step (work items)
+    lim = ops.prefill_route(dtype, Hq, Hkv, D).max_context
+    qlens = [16, 17, 33, 100, 1, 49, 1]
+    cached = [0, 5, 64, lim - 100 - 13, 300, 160, 40]
+    c = case(Hq * 10 + D + BS, Hq, Hkv, D, BS, dtype, qlens, cached)
+    meta = check(c)
+    assert meta.num_work_items > 0                     # the decode rows
+    assert meta.num_prefill_tiles == 0                 # every long run of rows went to the new kernel
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_contexts_at_the_limit_and_past_it(D):
+    lim = ops.prefill_route(torch.bfloat16, 14 if D == 64 else 32, 2 if D == 64 else 8, D).max_context
+    # one context at the limit from position 0, one at the limit after a prefix,
+    # one past it (tiles), one short
+    c = case(D, 14 if D == 64 else 32, 2 if D == 64 else 8, D, 32, torch.bfloat16,
+             qlens=[lim, lim - 48, lim + 40, 16], cached=[0, 48, 0, 7])
+    meta = check(c)
+    assert meta.num_prefill_tiles > 0                  # the sequence past the limit keeps the tiles
+
+
+def test_block_size_32_and_a_lone_sequence():
+    c = case(3, 14, 2, 64, 32, torch.float16, qlens=[65], cached=[130])
+    check(c)
+
+
+def test_config4_mixed_step():
+    from tinybatch_amd.workloads import make_mixed_workload
+
+    wl = make_mixed_workload()
+    c = dict(pool=wl.pool, tables=wl.block_tables, slices=wl.seq_slices, ctx=wl.context_lens,
+             pos=list(wl.positions),
+             q=wl.q, NB=wl.num_blocks, Hq=14, Hkv=2, D=64, BS=16, dtype=torch.bfloat16)
+    meta = check(c)
+    assert meta.num_prefill_work == 8 * 16 * 2          # 8 sequences x 16 block pairs x 2 kv heads
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fused_rope_equals_rotating_first(dtype):
+    c = case(21, 14, 2, 64, 16, dtype, qlens=[40, 96, 1], cached=[3, 100, 50], nan_tail=False)
+    cos, sin = rope_tables(64, 1e6, 8192, DEV)
+    meta = metadata(c)
+    q = c["q"].to(DEV)
+    pool = c["pool"].to(DEV)
+    out_a = ops.paged_attention(q, pool, meta, num_heads=14, rope=ops.Rope(cos, sin))
+    T = q.shape[0]
+    pos = torch.tensor(c["pos"], dtype=torch.int64, device=DEV)
+    zeros = torch.zeros(T, 2 * 2 * 64, dtype=dtype, device=DEV)
+    qr, _ = layer_ops.rope_qk(torch.cat([q.reshape(T, -1), zeros], 1).contiguous(), pos, cos, sin, 14, 2, 64)
+    out_b = ops.paged_attention(qr.contiguous(), pool, meta, num_heads=14)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(out_a), _bits(out_b))

@@ -87,6 +87,15 @@ SIGNATURES = {
     "tb_build_decode_plan": (c_i32, [c_vp, c_i32, c_i32, c_i32, c_vp, c_i32, c_i32, c_i64, c_i32, c_i32, c_i32,
                                      c_i32, c_i32, c_vp, c_sz]),
     "tb_decode_xcc_probe": (c_i32, [c_i32, c_vp, c_vp]),
+    "tb_paged_prefill": (c_i32, [
+        c_vp, c_i64, c_vp, c_i64, c_vp, c_i64,   # q, q stride, pool, num_blocks, out, out stride
+        c_vp, c_i32, c_vp, c_i32, c_i32,         # block tables, max_nb, work, num_work, max_tiles
+        c_i32, c_i32, c_i32, c_i32, c_f32, c_i32,   # heads, kv heads, head_dim, block_size, scale, dtype
+        c_vp, c_vp, c_i32, c_vp]),               # rope cos, sin, max position, stream
+    "tb_prefill_stream_max_context": (c_i32, [c_i32]),
+    "tb_prefill_stream_max_group": (c_i32, [c_i32]),
+    "tb_prefill_work_count": (c_i32, [c_vp, c_i32, c_i32]),
+    "tb_build_prefill_work": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_i32, c_i32, c_i32, c_i32, c_vp, c_i32, c_vp]),
     "tb_paged_attention_noalloc": (c_i32, [
         c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_vp, c_i32, c_vp, c_i32, c_vp, c_i32, c_vp, c_i32, c_vp, c_i32,
         c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_f32, c_i32, c_vp, c_i64, c_vp, c_i64,

@@ -14,7 +14,8 @@ REPO_DIR = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_NAME = "libtinybatch_amd.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ["tb_append.hip", "tb_attention.hip", "tb_copy.hip", "tb_fused.hip", "tb_linear.hip", "tb_decode.hip", "tb_metadata.cpp"]
+SOURCES = ["tb_append.hip", "tb_attention.hip", "tb_copy.hip", "tb_fused.hip", "tb_linear.hip", "tb_decode.hip",
+           "tb_prefill.hip", "tb_metadata.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

@@ -48,73 +48,9 @@
 // counted) and L1-bypassing loads suffice. The arrival word keeps a count per
 // XCD (8-bit fields), so a partial that ran on another XCD is detected and
 // counted in `violations`.
-#include "tb_common.h"
+#include "tb_stream.h"
 
 namespace tb {
-
-typedef _Float16 shalf8_t __attribute__((ext_vector_type(8)));
-typedef __bf16 sbf168_t __attribute__((ext_vector_type(8)));
-typedef _Float16 shalf4_t __attribute__((ext_vector_type(4)));
-typedef short sshort4_t __attribute__((ext_vector_type(4)));
-typedef unsigned int su32x2_t __attribute__((ext_vector_type(2)));
-typedef unsigned int su32x4_t __attribute__((ext_vector_type(4)));
-
-template <typename Tag>
-struct smath;
-template <>
-struct smath<f16_t> {
-  typedef _Float16 scalar_t;
-  static __device__ __forceinline__ float4_t mfma32(su32x4_t a, su32x4_t b, float4_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(shalf8_t, a), __builtin_bit_cast(shalf8_t, b), c,
-                                                   0, 0, 0);
-  }
-  // 4 probabilities as the B operand of the 16x16x16 product
-  static __device__ __forceinline__ su32x2_t pack4(float4_t p) {
-    shalf4_t h;
-    h[0] = (_Float16)p[0];
-    h[1] = (_Float16)p[1];
-    h[2] = (_Float16)p[2];
-    h[3] = (_Float16)p[3];
-    return __builtin_bit_cast(su32x2_t, h);
-  }
-  // 8 probabilities as the B operand of the 16x16x32 product
-  static __device__ __forceinline__ su32x4_t pack8(const float (&p)[8]) {
-    shalf8_t h;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) h[i] = (_Float16)p[i];
-    return __builtin_bit_cast(su32x4_t, h);
-  }
-  static __device__ __forceinline__ float4_t mfma16(su32x2_t a, su32x2_t b, float4_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(shalf4_t, a), __builtin_bit_cast(shalf4_t, b), c, 0,
-                                                  0, 0);
-  }
-};
-template <>
-struct smath<bf16_t> {
-  typedef __bf16 scalar_t;
-  static __device__ __forceinline__ float4_t mfma32(su32x4_t a, su32x4_t b, float4_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(sbf168_t, a), __builtin_bit_cast(sbf168_t, b),
-                                                    c, 0, 0, 0);
-  }
-  static __device__ __forceinline__ su32x2_t pack4(float4_t p) {
-    __bf16 h[4];
-    h[0] = (__bf16)p[0];
-    h[1] = (__bf16)p[1];
-    h[2] = (__bf16)p[2];
-    h[3] = (__bf16)p[3];
-    return __builtin_bit_cast(su32x2_t, h);
-  }
-  static __device__ __forceinline__ su32x4_t pack8(const float (&p)[8]) {
-    sbf168_t h;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) h[i] = (__bf16)p[i];
-    return __builtin_bit_cast(su32x4_t, h);
-  }
-  static __device__ __forceinline__ float4_t mfma16(su32x2_t a, su32x2_t b, float4_t c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(sshort4_t, a),
-                                                     __builtin_bit_cast(sshort4_t, b), c, 0, 0, 0);
-  }
-};
 
 struct stream_args {
   const char* q;            // [B][Hq][D]
@@ -166,135 +102,9 @@ struct sshape {
   static_assert(LDS <= 160 * 1024, "LDS budget of a workgroup");
   static_assert(2 * TLD * R + QLD * R + 2 <= 63, "vmcnt range");
   static_assert(STATE <= R * 2 * TB, "a partial's state fits in the ring");
-  // K row r keeps its 16-byte chunk c in slot c ^ (r & 7): the A-operand reads
-  // (16 rows x 16 bytes per 16 lanes) cover every bank. V row r keeps c in slot
-  // c ^ 2 (r & 3): so do the transpose reads (4 rows x 32 bytes per 16 lanes).
-  static __device__ __forceinline__ int kswz(int r) { return r & 7; }
-  static __device__ __forceinline__ int vswz(int r) { return 2 * (r & 3); }
-};
-
-__device__ __forceinline__ uint32_t s_lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
-
-// One direct global->LDS load of a wave: lane l's 16 bytes at src go to
-// lds_dst + 16 l (lds_dst wave-uniform, in M0). Issued as asm, so the compiler,
-// which cannot tell which LDS a direct load writes, sees none and never makes an
-// LDS access wait for one; every wait for these loads is explicit (s_vm_wait_le).
-// The s_nop is the wait state an M0 write needs before a direct load.
-__device__ __forceinline__ void s_dma16(const void* src, const void* lds_dst) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src), "{m0}"(s_lds_addr(lds_dst)) : "memory");
-}
-
-// The same with a wave-uniform base (SGPRs) and a per-lane 32-bit byte offset.
-__device__ __forceinline__ void s_dma16_s(uint32_t off, const void* base, const void* lds_dst) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(off), "s"(base), "{m0}"(s_lds_addr(lds_dst))
-               : "memory");
-}
-
-// Wait until at most n vector memory instructions of this wave are outstanding
-// (they complete in issue order); n is wave-uniform.
-template <int LO, int HI>
-__device__ __forceinline__ void s_vm_wait_range(int n) {
-  if constexpr (LO == HI) {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LO) : "memory");
-  } else {
-    constexpr int MID = (LO + HI) / 2;
-    if (n <= MID)
-      s_vm_wait_range<LO, MID>(n);
-    else
-      s_vm_wait_range<MID + 1, HI>(n);
-  }
-}
-__device__ __forceinline__ void s_vm_wait_le(int n) { s_vm_wait_range<0, 63>(n < 0 ? 0 : (n > 63 ? 63 : n)); }
-
-// The reads of one ring slot, one asm block that ends complete (lgkmcnt(0)):
-// the A-operand reads of the K rows (every k-slice) and the transpose reads of
-// V (every 16-dim slice). Compiler-visible, each would wait for every direct
-// load of the wave in flight; the slot's own wait already covers them. Once the
-// block ends the slot can be refilled.
-template <int KS, int NSL>
-struct slot_reads;
-template <>
-struct slot_reads<2, 4> {
-  static __device__ __forceinline__ void run(const uint32_t (&ka)[2], const uint32_t (&va)[4], su32x4_t (&k)[2],
-                                             su32x2_t (&v)[4]) {
-    asm volatile(
-        "ds_read_b128 %0, %6\n\tds_read_b128 %1, %7\n\t"
-        "ds_read_b64_tr_b16 %2, %8\n\tds_read_b64_tr_b16 %3, %9\n\t"
-        "ds_read_b64_tr_b16 %4, %10\n\tds_read_b64_tr_b16 %5, %11\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(k[0]), "=&v"(k[1]), "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3])
-        : "v"(ka[0]), "v"(ka[1]), "v"(va[0]), "v"(va[1]), "v"(va[2]), "v"(va[3])
-        : "memory");
-  }
-};
-template <>
-struct slot_reads<4, 8> {
-  static __device__ __forceinline__ void run(const uint32_t (&ka)[4], const uint32_t (&va)[8], su32x4_t (&k)[4],
-                                             su32x2_t (&v)[8]) {
-    asm volatile(
-        "ds_read_b128 %0, %12\n\tds_read_b128 %1, %13\n\tds_read_b128 %2, %14\n\tds_read_b128 %3, %15\n\t"
-        "ds_read_b64_tr_b16 %4, %16\n\tds_read_b64_tr_b16 %5, %17\n\t"
-        "ds_read_b64_tr_b16 %6, %18\n\tds_read_b64_tr_b16 %7, %19\n\t"
-        "ds_read_b64_tr_b16 %8, %20\n\tds_read_b64_tr_b16 %9, %21\n\t"
-        "ds_read_b64_tr_b16 %10, %22\n\tds_read_b64_tr_b16 %11, %23\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(k[0]), "=&v"(k[1]), "=&v"(k[2]), "=&v"(k[3]), "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]),
-          "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]), "=&v"(v[7])
-        : "v"(ka[0]), "v"(ka[1]), "v"(ka[2]), "v"(ka[3]), "v"(va[0]), "v"(va[1]), "v"(va[2]), "v"(va[3]),
-          "v"(va[4]), "v"(va[5]), "v"(va[6]), "v"(va[7])
-        : "memory");
-  }
-};
-
-// The reads of a step's two ring slots (A and B; the same slot twice for a one-tile
-// step) in one asm block that ends complete: K rows of both (A operand) and the
-// transposed V rows of both (the lo and hi halves of the P.V operand).
-template <int KS, int NSL>
-struct step_reads2;
-template <>
-struct step_reads2<2, 4> {
-  static __device__ __forceinline__ void run(const uint32_t (&ka)[4], const uint32_t (&va)[4], const uint32_t (&vb)[4],
-                                             su32x4_t (&k)[4], su32x2_t (&lo)[4], su32x2_t (&hi)[4]) {
-    asm volatile(
-        "ds_read_b128 %0, %12\n\tds_read_b128 %1, %13\n\tds_read_b128 %2, %14\n\tds_read_b128 %3, %15\n\t"
-        "ds_read_b64_tr_b16 %4, %16\n\tds_read_b64_tr_b16 %5, %17\n\t"
-        "ds_read_b64_tr_b16 %6, %18\n\tds_read_b64_tr_b16 %7, %19\n\t"
-        "ds_read_b64_tr_b16 %8, %20\n\tds_read_b64_tr_b16 %9, %21\n\t"
-        "ds_read_b64_tr_b16 %10, %22\n\tds_read_b64_tr_b16 %11, %23\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(k[0]), "=&v"(k[1]), "=&v"(k[2]), "=&v"(k[3]), "=&v"(lo[0]), "=&v"(lo[1]), "=&v"(lo[2]), "=&v"(lo[3]),
-          "=&v"(hi[0]), "=&v"(hi[1]), "=&v"(hi[2]), "=&v"(hi[3])
-        : "v"(ka[0]), "v"(ka[1]), "v"(ka[2]), "v"(ka[3]), "v"(va[0]), "v"(va[1]), "v"(va[2]), "v"(va[3]),
-          "v"(vb[0]), "v"(vb[1]), "v"(vb[2]), "v"(vb[3])
-        : "memory");
-  }
-};
-template <>
-struct step_reads2<4, 8> {
-  static __device__ __forceinline__ void run(const uint32_t (&ka)[8], const uint32_t (&va)[8], const uint32_t (&vb)[8],
-                                             su32x4_t (&k)[8], su32x2_t (&lo)[8], su32x2_t (&hi)[8]) {
-    asm volatile(
-        "ds_read_b128 %0, %24\n\tds_read_b128 %1, %25\n\tds_read_b128 %2, %26\n\tds_read_b128 %3, %27\n\t"
-        "ds_read_b128 %4, %28\n\tds_read_b128 %5, %29\n\tds_read_b128 %6, %30\n\tds_read_b128 %7, %31\n\t"
-        "ds_read_b64_tr_b16 %8, %32\n\tds_read_b64_tr_b16 %9, %33\n\t"
-        "ds_read_b64_tr_b16 %10, %34\n\tds_read_b64_tr_b16 %11, %35\n\t"
-        "ds_read_b64_tr_b16 %12, %36\n\tds_read_b64_tr_b16 %13, %37\n\t"
-        "ds_read_b64_tr_b16 %14, %38\n\tds_read_b64_tr_b16 %15, %39\n\t"
-        "ds_read_b64_tr_b16 %16, %40\n\tds_read_b64_tr_b16 %17, %41\n\t"
-        "ds_read_b64_tr_b16 %18, %42\n\tds_read_b64_tr_b16 %19, %43\n\t"
-        "ds_read_b64_tr_b16 %20, %44\n\tds_read_b64_tr_b16 %21, %45\n\t"
-        "ds_read_b64_tr_b16 %22, %46\n\tds_read_b64_tr_b16 %23, %47\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=&v"(k[0]), "=&v"(k[1]), "=&v"(k[2]), "=&v"(k[3]), "=&v"(k[4]), "=&v"(k[5]), "=&v"(k[6]), "=&v"(k[7]),
-          "=&v"(lo[0]), "=&v"(lo[1]), "=&v"(lo[2]), "=&v"(lo[3]), "=&v"(lo[4]), "=&v"(lo[5]), "=&v"(lo[6]), "=&v"(lo[7]),
-          "=&v"(hi[0]), "=&v"(hi[1]), "=&v"(hi[2]), "=&v"(hi[3]), "=&v"(hi[4]), "=&v"(hi[5]), "=&v"(hi[6]), "=&v"(hi[7])
-        : "v"(ka[0]), "v"(ka[1]), "v"(ka[2]), "v"(ka[3]), "v"(ka[4]), "v"(ka[5]), "v"(ka[6]), "v"(ka[7]),
-          "v"(va[0]), "v"(va[1]), "v"(va[2]), "v"(va[3]), "v"(va[4]), "v"(va[5]), "v"(va[6]), "v"(va[7]),
-          "v"(vb[0]), "v"(vb[1]), "v"(vb[2]), "v"(vb[3]), "v"(vb[4]), "v"(vb[5]), "v"(vb[6]), "v"(vb[7])
-        : "memory");
-  }
+  // the swizzled tile layout of tb_stream.h
+  static __device__ __forceinline__ int kswz(int r) { return stream_kswz(r); }
+  static __device__ __forceinline__ int vswz(int r) { return stream_vswz(r); }
 };
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t s_rsrc(const void* base, uint32_t bytes) {

@@ -67,7 +67,8 @@ class PagedKVCache:
         ``positions`` tensor; the entry is still keyed on ``positions``. With
         ``num_heads`` (query heads), a decode-only step that the streaming decode
         kernel serves faster (ops.decode_kernel_preferred) also gets its plan, and
-        attention() / decode_step() with this metadata then run that kernel.
+        attention() / decode_step() with this metadata then run that kernel; a
+        prefill-only step goes to tb_paged_prefill.
         """
         pos_key = (positions, positions._version) if isinstance(positions, torch.Tensor) else list(positions)
         for e in self._meta_cache:
@@ -75,13 +76,23 @@ class PagedKVCache:
                     and e["tables"] == block_tables
                     and (context_lens is None or (e["ctx"] == context_lens and e["rows"] == rows_per_item))):
                 return e["meta"]
-        # 16-bit pools serve long runs of new rows (prefills) with the tile kernel
+        # 16-bit pools serve long runs of new rows (prefills) with the tile kernel; a
+        # step of prefills only (every sequence >= 16 new rows, its context within
+        # the kernel's limit) goes to tb_paged_prefill instead: a step that also has
+        # decode rows keeps them in the one launch with the tiles
         tile = self.pools[0].dtype in (torch.float16, torch.bfloat16)
+        route = None
+        if num_heads is not None and context_lens is not None and self.device.type == "cuda" and tile:
+            r = ops.prefill_route(self.dtype, num_heads, self.n_kv_heads, self.head_dim, self.device)
+            qlens = [e - b for b, e in seq_slices]
+            if r is not None and any(qlens) and all(
+                    n == 0 or (n >= 16 and c <= r.max_context) for n, c in zip(qlens, context_lens)):
+                route = r
         meta = build_step_metadata(positions if host_positions is None else host_positions,
                                    seq_slices, block_tables, context_lens,
                                    block_size=self.block_size, num_blocks=self.num_blocks,
                                    partition_tokens=self.partition_tokens, rows_per_item=rows_per_item,
-                                   tile_prefill=tile)
+                                   tile_prefill=tile, prefill_route=route)
         if (num_heads is not None and context_lens is not None and self.device.type == "cuda"
                 and ops.decode_kernel_preferred(meta, num_kv_heads=self.n_kv_heads, head_dim=self.head_dim,
                                                 dtype=self.dtype)):

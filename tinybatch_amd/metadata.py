@@ -40,6 +40,8 @@ from __future__ import annotations
 import itertools
 from dataclasses import dataclass
 
+from typing import NamedTuple
+
 import numpy as np
 import torch
 
@@ -90,12 +92,18 @@ class StepMetadata:
     # (tb_paged_attention_merged): set by attach_xcd_slot_map
     slot_map_np: np.ndarray | None = None
     slot_map: torch.Tensor | None = None
+    # whole prefill sequences served by tb_paged_prefill (build_step_metadata's
+    # prefill_route): its work list and the most tiles one entry holds
+    prefill_work_np: np.ndarray | None = None
+    num_prefill_work: int = 0
+    prefill_max_tiles: int = 0
+    prefill_work: torch.Tensor | None = None
 
     def to(self, device: torch.device) -> "StepMetadata":
         """Upload every array with one host-to-device copy (views into one buffer)."""
         parts = [self.slot_mapping_np, self.block_tables_np.reshape(-1), self.work_np.reshape(-1),
                  self.row_part_off_np, self.prefill_tiles_np.reshape(-1), self.split_rows_np.reshape(-1)]
-        extra = [x for x in (self.decode_plan_np, self.slot_map_np) if x is not None]
+        extra = [x for x in (self.decode_plan_np, self.slot_map_np, self.prefill_work_np) if x is not None]
         parts += extra
         sizes = [pad4(p.size) for p in parts]
         host = np.zeros(sum(sizes), dtype=np.int32)
@@ -119,6 +127,9 @@ class StepMetadata:
             k += 1
         if self.slot_map_np is not None:
             self.slot_map = buf.narrow(0, int(offs[k]), parts[k].size)
+            k += 1
+        if self.prefill_work_np is not None:
+            self.prefill_work = buf.narrow(0, int(offs[k]), parts[k].size)
         return self
 
 
@@ -126,6 +137,39 @@ class StepMetadata:
 # in include/tinybatch_amd.h): query rows per tile, positions per tile partition.
 TILE_ROWS = 64
 TILE_PARTITION = 1024
+
+
+class PrefillRoute(NamedTuple):
+    """Where whole prefill sequences go to tb_paged_prefill: the step's kv heads and
+    head dim, and the longest context that kernel serves (ops.prefill_route)."""
+    num_kv_heads: int
+    head_dim: int
+    max_context: int
+    num_xcds: int = 1
+
+
+def build_prefill_work(first_rows, seqs, pos0s, new_rows, *, num_kv_heads: int, head_dim: int,
+                       num_xcds: int = 1) -> tuple[np.ndarray, int]:
+    """tb_build_prefill_work: one entry (first row, sequence, pos0, new rows | pair <<
+    16 | kv head << 24) per (sequence, kv head, pair of 16-row blocks), the entries of
+    one (sequence, kv head) on one XCD, and the most 16-position tiles one entry holds."""
+    import ctypes
+
+    from . import _lib
+
+    cols = [np.ascontiguousarray(np.asarray(x, dtype=np.int32).reshape(-1)) for x in (first_rows, seqs, pos0s, new_rows)]
+    n = cols[0].size
+    lib = _lib.lib()
+    ptrs = [c.ctypes.data_as(ctypes.c_void_p) for c in cols]
+    count = lib.tb_prefill_work_count(ptrs[3], n, num_kv_heads)
+    if count < 0:
+        raise ValueError("bad prefill sequences (new rows must be >= 1)")
+    work = np.zeros((max(count, 1), 4), dtype=np.int32)
+    tiles = ctypes.c_int32()
+    st = lib.tb_build_prefill_work(*ptrs, n, num_kv_heads, head_dim, num_xcds, work.ctypes.data_as(ctypes.c_void_p),
+                                   count, ctypes.byref(tiles))
+    _lib.check(st, "tb_build_prefill_work")
+    return work[:count], int(tiles.value)
 
 
 def tiles_sequence(q_len: int, ctx: int, min_rows: int = 16, max_ctx: int = 4096) -> bool:
@@ -149,8 +193,11 @@ def _host_positions(positions) -> np.ndarray:
 def build_step_metadata(positions, seq_slices, block_tables, context_lens, *, block_size: int,
                         num_blocks: int, partition_tokens: int, num_tokens: int | None = None,
                         validate_attention: bool = True, rows_per_item: int = 1,
-                        tile_prefill: bool = False) -> StepMetadata:
-    """Build the per-step arrays (host side). See the module docstring."""
+                        tile_prefill: bool = False, prefill_route: PrefillRoute | None = None) -> StepMetadata:
+    """Build the per-step arrays (host side). See the module docstring. With
+    ``prefill_route``, sequences of >= 16 new rows whose context is at most its
+    max_context go to tb_paged_prefill whole (prefill_work_np); their rows get no
+    work items, tiles or partition slots."""
     if block_size <= 0 or block_size & (block_size - 1):
         raise ValueError(f"block_size must be a power of two, got {block_size}")
     pos = _host_positions(positions)
@@ -213,6 +260,7 @@ def build_step_metadata(positions, seq_slices, block_tables, context_lens, *, bl
     P = int(partition_tokens)
     row_ctx_by_row = np.zeros(T, dtype=np.int64)
     tiles: list[tuple[int, int, int, int, int]] = []
+    stream_seqs: list[tuple[int, int, int, int]] = []
     tiled = np.zeros(T, dtype=bool)
     nparts_by_row = np.zeros(T, dtype=np.int64)
     if tot and context_lens is not None:
@@ -230,10 +278,18 @@ def build_step_metadata(positions, seq_slices, block_tables, context_lens, *, bl
         row_ctx = np.repeat(ctx - qlens, qlens) + row_i + 1
         row_ctx_by_row[row_ids] = row_ctx
         nparts_by_row[row_ids] = (row_ctx + P - 1) // P
+        if prefill_route is not None:
+            for b in range(B):
+                n, c = int(qlens[b]), int(ctx[b])
+                if n >= 16 and c <= prefill_route.max_context:
+                    s0 = int(starts[b])
+                    tiled[s0:s0 + n] = True               # served by tb_paged_prefill
+                    nparts_by_row[s0:s0 + n] = 0
+                    stream_seqs.append((s0, b, c - n, n))
         if tile_prefill:
             for b in range(B):
                 n, c = int(qlens[b]), int(ctx[b])
-                if n and tiles_sequence(n, c):
+                if n and not tiled[int(starts[b])] and tiles_sequence(n, c):
                     s0 = int(starts[b])
                     tiled[s0:s0 + n] = True               # served by tiles, not work items
                     rc = row_ctx_by_row[s0:s0 + n]
@@ -297,6 +353,12 @@ def build_step_metadata(positions, seq_slices, block_tables, context_lens, *, bl
     split_rows[:, 0] = split_ids
     split_rows[:, 1] = row_part_off[split_ids]
     split_rows[:, 2] = nparts_by_row[split_ids]
+    prefill_work, prefill_tiles_max = None, 0
+    if stream_seqs:
+        cols = np.asarray(stream_seqs, dtype=np.int64).T
+        prefill_work, prefill_tiles_max = build_prefill_work(
+            cols[0], cols[1], cols[2], cols[3], num_kv_heads=prefill_route.num_kv_heads,
+            head_dim=prefill_route.head_dim, num_xcds=prefill_route.num_xcds)
 
     return StepMetadata(
         num_tokens=T, num_seqs=B, block_size=block_size, partition_tokens=P,
@@ -315,6 +377,9 @@ def build_step_metadata(positions, seq_slices, block_tables, context_lens, *, bl
         prefill_tiles_np=tiles_np.astype(np.int32),
         split_rows_np=split_rows.astype(np.int32),
         num_blocks=int(num_blocks),
+        prefill_work_np=prefill_work,
+        num_prefill_work=0 if prefill_work is None else int(prefill_work.shape[0]),
+        prefill_max_tiles=prefill_tiles_max,
     )
 
 

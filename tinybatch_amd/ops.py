@@ -210,10 +210,34 @@ def decode_device(device: torch.device) -> DecodeDevice:
 DECODE_KERNEL_MIN_BYTES = 32 << 20
 
 
-def decode_kernel_preferred(meta: StepMetadata, *, num_kv_heads: int, head_dim: int, dtype: torch.dtype) -> bool:
+def prefill_route(dtype: torch.dtype, num_heads: int, num_kv_heads: int, head_dim: int,
+                  device: torch.device | None = None):
+    """The PrefillRoute (build_step_metadata's prefill_route) that sends whole prefill
+    sequences to tb_paged_prefill for this geometry, or None where that kernel does not
+    serve it (fp32, head dims other than 64 / 128, too many query heads per kv head).
+    With ``device``, the work of one (sequence, kv head) is placed on one of its XCDs
+    when the device runs workgroup g on XCD g mod the XCD count (DecodeDevice)."""
+    from .metadata import PrefillRoute
+
+    if dtype not in (torch.float16, torch.bfloat16) or num_kv_heads <= 0 or num_heads % num_kv_heads:
+        return None
+    lib = _lib.lib()
+    max_ctx = int(lib.tb_prefill_stream_max_context(head_dim))
+    if max_ctx <= 0 or num_heads // num_kv_heads > int(lib.tb_prefill_stream_max_group(head_dim)) \
+            or num_kv_heads > 127:
+        return None
+    xcds = 1
+    if device is not None and device.type == "cuda":
+        d = decode_device(device)
+        xcds = d.num_xcds if d.merge_in_kernel else 1
+    return PrefillRoute(num_kv_heads, head_dim, max_ctx, xcds)
+
+
+def decode_kernel_preferred(meta: StepMetadata, *, num_kv_heads: int, head_dim: int, dtype: torch.dtype,
+                            min_bytes: int = DECODE_KERNEL_MIN_BYTES) -> bool:
     """Whether a step is served faster by the streaming decode kernel: a decode-only
-    step (row b = sequence b) in fp16 / bf16 reading at least DECODE_KERNEL_MIN_BYTES
-    of K/V, with at least 32 (sequence, kv head) units (a unit stays on one XCD, so
+    step (row b = sequence b) in fp16 / bf16 reading at least ``min_bytes`` of K/V
+    (DECODE_KERNEL_MIN_BYTES by default), with at least 32 (sequence, kv head) units (a unit stays on one XCD, so
     fewer units leave XCDs idle). The plan must then be attached (attach_decode_plan)
     before meta.to()."""
     if not meta.rows_are_seqs or dtype not in (torch.float16, torch.bfloat16):
@@ -221,7 +245,7 @@ def decode_kernel_preferred(meta: StepMetadata, *, num_kv_heads: int, head_dim: 
     if meta.num_seqs * num_kv_heads < 32:
         return False
     kv_bytes = int(meta.row_ctx_np[:meta.num_seqs].astype(np.int64).sum()) * num_kv_heads * head_dim * 2 * 2
-    return kv_bytes >= DECODE_KERNEL_MIN_BYTES
+    return kv_bytes >= min_bytes
 
 
 def attach_decode_plan(meta: StepMetadata, *, num_heads: int, num_kv_heads: int, head_dim: int,
@@ -397,7 +421,7 @@ def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, 
     if k_new is not None or v_new is not None:
         if k_new is None or v_new is None:
             raise ValueError("k_new and v_new go together")
-        if not meta.decode_only or meta.num_prefill_tiles:
+        if not meta.decode_only or meta.num_prefill_tiles or meta.num_prefill_work:
             raise ValueError("fused append needs a decode-only step (one query row per sequence)")
         sm = meta.slot_mapping_np
         if sm.size and np.any((sm < 0) & (meta.row_ctx_np > 0)):
@@ -423,6 +447,13 @@ def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, 
     tail = (_ptr(meta.device_counts),
             None if rope is None else rope.cos.data_ptr(), None if rope is None else rope.sin.data_ptr(),
             0 if rope is None else rope.max_position, _lib.stream_handle(q.device))
+    if meta.num_prefill_work:   # whole prefill sequences first (their K/V are appended already)
+        if meta.prefill_work is None:
+            raise ValueError("metadata has not been uploaded (call meta.to(device))")
+        _lib.check(_lib.lib().tb_paged_prefill(
+            q.data_ptr(), qs, pool.data_ptr(), nb, out.data_ptr(), os_, meta.block_tables.data_ptr(),
+            meta.max_blocks_per_seq, meta.prefill_work.data_ptr(), meta.num_prefill_work, meta.prefill_max_tiles,
+            num_heads, hkv, d, bs, float(scale), _lib.DTYPE_CODE[q.dtype], *tail[1:]), "tb_paged_prefill")
     if noalloc:
         if workspace is not None:
             raise ValueError("noalloc takes no workspace")
