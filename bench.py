@@ -225,6 +225,7 @@ def bench_mixed(args, dev) -> int:
     rows = ops.rows_per_item(wl.dtype, wl.num_heads, wl.num_kv_heads)
     Hq = wl.num_heads
     results = {}
+    dec_kernel = "paged_attn_mfma_kernel (work items)"
     for which, w in (("step", wl), ("prefill", wl.part("prefill")), ("decode", wl.part("decode"))):
         # whole prefill sequences go to tb_paged_prefill in a prefill-only step; a
         # step with decode rows keeps the one launch of tiles and decode items
@@ -233,10 +234,11 @@ def bench_mixed(args, dev) -> int:
         meta = build_step_metadata(w.positions, w.seq_slices, w.block_tables, w.context_lens,
                                    block_size=w.block_size, num_blocks=w.num_blocks, partition_tokens=P,
                                    rows_per_item=rows, tile_prefill=not args.no_tiles, prefill_route=route)
-        if which == "decode" and args.decode_stream and ops.decode_kernel_preferred(
-                meta, num_kv_heads=wl.num_kv_heads, head_dim=wl.head_dim, dtype=wl.dtype, min_bytes=0):
-            ops.attach_decode_plan(meta, num_heads=Hq, num_kv_heads=wl.num_kv_heads, head_dim=wl.head_dim,
-                                   dtype=wl.dtype, device=dev)
+        if which == "decode" and not args.no_decode_stream and ops.decode_kernel_preferred(
+                meta, num_kv_heads=wl.num_kv_heads, head_dim=wl.head_dim, dtype=wl.dtype):
+            if ops.attach_decode_plan(meta, num_heads=Hq, num_kv_heads=wl.num_kv_heads, head_dim=wl.head_dim,
+                                      dtype=wl.dtype, device=dev):
+                dec_kernel = "paged_stream_kernel"
         meta = meta.to(dev)
         q, k, v = w.q.to(dev), w.k_new.to(dev), w.v_new.to(dev)
         out = torch.empty(w.num_tokens, Hq * w.head_dim, dtype=w.dtype, device=dev)
@@ -303,7 +305,7 @@ def bench_mixed(args, dev) -> int:
                                 else "paged_prefill_mfma_kernel" if args.no_stream_prefill
                                 else "paged_prefill_stream_kernel") + " (prefill rows)"},
         "decode_roofline": {"bound": "hbm", "achieved": round(dec_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                            "frac": round(dec_gbs / HBM_PEAK_GBS, 4)},
+                            "frac": round(dec_gbs / HBM_PEAK_GBS, 4), "kernel": dec_kernel},
         "copy_roofline": {"bound": "hbm", "achieved": round(copy_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(copy_gbs / HBM_PEAK_GBS, 4), "kernel": "block_copy_kernel"},
         "append_us_per_layer": round(ms_append / L * 1e3, 3),
@@ -409,6 +411,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="qwen-fp16-b64")
     ap.add_argument("--layers", type=int, default=0, help="layer pools to rotate (0 = auto)")
+    ap.add_argument("--batch", type=int, default=0, help="decode workloads: the first N sequences only")
     ap.add_argument("--mode", choices=["fused", "split"], default="fused")
     ap.add_argument("--kernel", choices=["auto", "decode", "items"], default="auto",
                     help="decode: streaming decode kernel (tb_paged_decode); items: work-item kernel; "
@@ -420,8 +423,9 @@ def main() -> int:
     ap.add_argument("--combine", action="store_true",
                     help="work-item kernel: merge split rows with the separate combine kernel, not inside the launch")
     ap.add_argument("--no-graph", action="store_true")
-    ap.add_argument("--decode-stream", action="store_true",
-                    help="mixed workload: the decode rows through the streaming decode kernel")
+    ap.add_argument("--no-decode-stream", action="store_true",
+                    help="mixed workload: the decode rows through work items even where the streaming "
+                         "decode kernel is preferred")
     ap.add_argument("--no-stream-prefill", action="store_true",
                     help="mixed workload: prefill sequences through the tile kernel, not tb_paged_prefill")
     ap.add_argument("--cpu-reps", type=int, default=5)
@@ -472,7 +476,8 @@ def main() -> int:
 
     big = args.workload == "llama-bf16-b256"
     t0 = time.perf_counter()
-    wl = make_decode_workload(args.workload, pool_device=(dev if big else "cpu"))
+    wl = make_decode_workload(args.workload, pool_device=(dev if big else "cpu"),
+                              **({"batch": args.batch} if args.batch else {}))
     _log(f"workload {wl.name}: B={wl.batch} NB={wl.num_blocks} mean ctx={sum(wl.context_lens)/wl.batch:.0f} "
          f"({time.perf_counter() - t0:.1f}s)")
     pool_bytes = wl.pool.numel() * wl.pool.element_size()
