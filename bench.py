@@ -120,18 +120,23 @@ def cpu_baseline_mixed(wl, reps: int, budget_s: float) -> dict:
 
 
 def kernel_source_hash() -> str:
-    """sha256 (first 16 hex digits) of the HIP sources and the C header: the kernels a
-    profile was measured on."""
+    """sha256 (first 16 hex digits) of the code of the HIP sources and the C header,
+    comments and white space left out: the kernels a profile was measured on (an edit
+    of a comment does not void a profile, any edit of code does)."""
     import hashlib
+    import re
+
+    def code(path):
+        with open(path) as f:
+            text = re.sub(r"//[^\n]*|/\*.*?\*/", " ", f.read(), flags=re.S)
+        return " ".join(text.split()).encode()
 
     h = hashlib.sha256()
     csrc = os.path.join(ROOT, "tinybatch_amd", "csrc")
     for name in sorted(os.listdir(csrc)):
         if name.endswith((".hip", ".h", ".cpp")):
-            with open(os.path.join(csrc, name), "rb") as f:
-                h.update(name.encode() + b"\0" + f.read())
-    with open(os.path.join(ROOT, "include", "tinybatch_amd.h"), "rb") as f:
-        h.update(f.read())
+            h.update(name.encode() + b"\0" + code(os.path.join(csrc, name)))
+    h.update(code(os.path.join(ROOT, "include", "tinybatch_amd.h")))
     return h.hexdigest()[:16]
 
 

@@ -7,15 +7,17 @@
 // Work: one workgroup per (sequence, kv head, pair of 16-row blocks). The new
 // rows are cut into blocks of 16; pair p holds blocks p and nb - 1 - p, so every
 // pair of a sequence sees the same number of (row, position) scores. The
-// workgroup has two waves per query head of the kv head (2 * rep waves): the
-// first rep take the later block, the others the earlier one. Every wave owns
-// its 16 rows of one head for the whole context: no partials, no merge.
+// workgroup has two waves per query head of the kv head (2 * rep waves), A and
+// B: B takes the earlier block (and writes it), then the later block's steps
+// past those A takes, so that A and B do equal work; at the end A merges B's
+// part of the later block (log-sum-exp, through LDS) and writes it. Nothing
+// goes through global memory but q, K/V and the output rows.
 //
 // Loads. The workgroup's K/V range (positions 0 .. the later block's last row)
 // moves into LDS once, as 16-position tiles in the swizzled layout of
 // tb_stream.h, by direct global->LDS loads of 1 KiB of consecutive pool bytes per
-// instruction, all issued at the start by the later block's waves (tile t by
-// wave t % rep), so the range costs one memory round trip; the query heads of
+// instruction, all issued at the start (tile t by wave t % (2 rep)), so the
+// range costs one memory round trip; the query heads of
 // the kv head share it. V rows past the context are zeroed in LDS (a stale slot
 // may hold any bits; their p is 0). One barrier, then every wave streams its
 // tiles from LDS without further synchronisation.
@@ -389,7 +391,7 @@ __global__ __launch_bounds__(pshape<D>::MAXREP / pshape<D>::HPW * 128, 1) void p
       va0[nn] = lds0 + (uint32_t)(TB + rv * RB + 16 * (c ^ stream_vswz(rv)) + half8);
     }
   }
-  // Chunk c holds steps 4c .. 4c + 3 (tiles 8c .. 8c + 7). Its steps of the
+  // Chunk c holds steps CH/2 c .. CH/2 (c + 1) - 1 (tiles CH c ..). Its steps of the
   // earlier block go to B; its steps of the later block are shared so that A and
   // B have equal work in every chunk (A the first ones, B the rest), so both
   // waves of a head group stream together while the next chunks land. B finishes
