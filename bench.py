@@ -119,6 +119,51 @@ def cpu_baseline_mixed(wl, reps: int, budget_s: float) -> dict:
                       f"{t_all * 1e3:.1f} ms; torch CPU ({cpu_model()})"}
 
 
+def cpu_baseline_e2e(weights: dict, mc, wl, reps: int, budget_s: float) -> dict:
+    """The oracle's Qwen2 forward (the reference's Qwen2Paged.forward restated op for op,
+    per-sequence gather + SDPA included) on the host cores: decode steps of the serving
+    workload's 32 requests at their first output position (context = prompt + 1), with
+    the model's own weights and dtype. Reports output tokens per second of those steps
+    (one token per request per step)."""
+    import torch
+
+    from oracle import model_reference as mref
+
+    threads = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(threads)
+    BS = 16
+    ctx = [len(p) + 1 for p in wl.prompts]
+    B = len(ctx)
+    tables, at = [], 0
+    for c in ctx:                                  # private blocks per request (no sharing on this path)
+        n = (c + BS - 1) // BS
+        tables.append(list(range(at, at + n)))
+        at += n
+    dt = next(iter(weights.values())).dtype
+    pools = [torch.zeros(at, 2, mc.n_kv_heads, BS, mc.head_dim, dtype=dt) for _ in range(mc.n_layers)]
+    ids = torch.tensor([p[-1] for p in wl.prompts])
+    pos = torch.tensor([c - 1 for c in ctx])
+    slices = [(i, i + 1) for i in range(B)]
+
+    def step():
+        mref.forward(weights, mc, ids, pos, slices, tables, ctx, pools, BS)
+
+    step()                                         # warm-up (allocator, kernels)
+    times, t_start = [], time.perf_counter()
+    for _ in range(max(reps, 1)):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > budget_s:
+            break
+    times.sort()
+    med = times[len(times) // 2]
+    return {"value": round(B / med, 2), "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{len(times)} decode steps of the {B} requests (contexts {min(ctx)}..{max(ctx)}, "
+                      f"{mc.n_layers} layers, {str(dt).replace('torch.', '')} weights), median {med * 1e3:.1f} ms "
+                      f"per step; torch CPU ({cpu_model()})"}
+
+
 def kernel_source_hash() -> str:
     """sha256 (first 16 hex digits) of the code of the HIP sources and the C header,
     comments and white space left out: the kernels a profile was measured on (an edit
@@ -323,13 +368,14 @@ def bench_mixed(args, dev) -> int:
     return 0
 
 
-def run_e2e(dev, warmup: int) -> dict:
+def run_e2e(dev, warmup: int, cpu: dict | None = None) -> dict:
     """Continuous batching of 32 random-token requests on a random-init Qwen2 at
     0.5B dimensions (bf16), 75% sharing a 400-token prefix, greedy outputs of
     U{16..256} tokens, everything submitted at t = 0. Returns output tokens per
     second of wall time, decode-only-step token rate, TTFT mean / p99 (first
     token time - submit time, the reference's engine.py:131-132) and the run's
-    configuration."""
+    configuration. With ``cpu`` ({"reps", "budget"}) also the oracle's decode-step
+    rate on the host cores (cpu_baseline_e2e) under "cpu_baseline"."""
     import statistics
 
     import torch
@@ -386,6 +432,12 @@ def run_e2e(dev, warmup: int) -> dict:
                    "max_batch_tokens": ecfg.max_batch_tokens, "max_running": ecfg.max_running,
                    "rope_theta": mc.rope_theta, "rms_eps": mc.rms_eps},
     }
+    res["cpu_baseline"] = None
+    if cpu is not None:
+        _log("timing the e2e CPU baseline (oracle forward) ...")
+        w = {k: v.detach().cpu() for k, v in model.reference_weights().items()}
+        res["cpu_baseline"] = cpu_baseline_e2e(w, mc, wl, cpu["reps"], cpu["budget"])
+        del w
     del eng, model
     torch.cuda.empty_cache()
     return res
@@ -393,7 +445,7 @@ def run_e2e(dev, warmup: int) -> dict:
 
 def bench_e2e(args, dev) -> int:
     """The end-to-end serving workload alone (run_e2e) as its own JSON line."""
-    r = run_e2e(dev, args.warmup)
+    r = run_e2e(dev, args.warmup, None if args.no_cpu else {"reps": args.cpu_reps, "budget": args.cpu_budget})
     line = {
         "metric": "e2e decode tok/s (continuous batching, random-init Qwen2 0.5B dims)",
         "value": r["tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": r["steps"], "warmup": args.warmup,
@@ -403,7 +455,7 @@ def bench_e2e(args, dev) -> int:
         "config": dict(workload=r["workload"], **r["config"]),
         **{k: r[k] for k in ("output_tokens", "wall_s", "decode_only_tok_s", "ttft_mean_ms", "ttft_p99_ms",
                               "prefix_hit_rate", "preemptions", "graph_steps", "pipelined_steps")},
-        "cpu_baseline": None,
+        "cpu_baseline": r["cpu_baseline"],
     }
     print(json.dumps(line), flush=True)
     return 0
@@ -554,7 +606,7 @@ def main() -> int:
         del storage, pools
         torch.cuda.empty_cache()
         _log("end-to-end serving run ...")
-        e2e = run_e2e(dev, 1)
+        e2e = run_e2e(dev, 1, None if args.no_cpu else {"reps": 3, "budget": 10.0})
         _log(f"e2e: {e2e['tok_s']} tok/s, TTFT mean {e2e['ttft_mean_ms']} ms, p99 {e2e['ttft_p99_ms']} ms")
 
     if decode_kernel:
