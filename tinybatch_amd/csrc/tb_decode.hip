@@ -197,7 +197,8 @@ __global__ __launch_bounds__(64 * W) void paged_stream_kernel(const stream_args 
   constexpr int STATE = S::STATE;
   static_assert(R % 2 == 0, "a step is a pair of ring slots");
   __shared__ __align__(1024) char lds_all[S::LDS];
-  __shared__ int pend_sh[W][2][4];               // per wave: its partials (unit, np | w0 << 8 | idx << 16, base)
+  __shared__ int pend_sh[W][2][4];               // per wave: its partials (unit, np | w0 << 8 | idx << 16, base,
+                                                 // sequence | kv head << 20)
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, lc = lane & 15, lg = lane >> 4;
@@ -312,6 +313,7 @@ __global__ __launch_bounds__(64 * W) void paged_stream_kernel(const stream_args 
   float m_run = -INFINITY, l_part = 0.f;
   bool pend0 = false, pend1 = false;            // partials: finished mid-stream (in pst), at the end
   int pinfo1[4] = {0, 0, 0, 0};
+  int pbh1 = 0;                                 // the end partial's sequence | kv head << 20
   const auto prs = s_rsrc(a.pieces, a.pieces_bytes);
 #pragma unroll
   for (int s = 0; s < KS; ++s) qb[s] = su32x4_t{0u, 0u, 0u, 0u};
@@ -495,6 +497,7 @@ __global__ __launch_bounds__(64 * W) void paged_stream_kernel(const stream_args 
               pend_sh[wave][0][0] = u;
               pend_sh[wave][0][1] = info1;
               pend_sh[wave][0][2] = eA.w & 0xFFFFF;
+              pend_sh[wave][0][3] = b | (h << 20);
             }
             pend0 = true;
           } else {
@@ -502,6 +505,7 @@ __global__ __launch_bounds__(64 * W) void paged_stream_kernel(const stream_args 
             pinfo1[1] = info1;
             pinfo1[2] = eA.w & 0xFFFFF;
             pinfo1[3] = __float_as_int(l_tot);
+            pbh1 = b | (h << 20);
             pend1 = true;
           }
         }
@@ -517,6 +521,7 @@ __global__ __launch_bounds__(64 * W) void paged_stream_kernel(const stream_args 
     pend_sh[wave][1][0] = pend1 ? pinfo1[0] : -1;
     pend_sh[wave][1][1] = pinfo1[1];
     pend_sh[wave][1][2] = pinfo1[2];
+    pend_sh[wave][1][3] = pbh1;
   }
   __syncthreads();
   constexpr int CPL = (8 * D / 4 + 63) / 64;
@@ -532,8 +537,10 @@ __global__ __launch_bounds__(64 * W) void paged_stream_kernel(const stream_args 
     // the group: this wave's piece and the next waves' pieces of the unit in this workgroup
     int cnt = 1;
     while (idx + cnt < np && (w0 + idx + cnt) % W != 0) ++cnt;
-    const int b = u / a.num_kv_heads, h = u - b * a.num_kv_heads;
-    // the members' states (LDS): every read in flight at once, then one log-sum-exp
+    const int bh = __builtin_amdgcn_readfirstlane(pend_sh[wave][e][3]);
+    const int b = bh & 0xFFFFF, h = bh >> 20;
+    // the members' states (LDS): every read of both column sets in flight at once,
+    // then one log-sum-exp per column
     float Mx[CPL], L[CPL];
     float4_t o[CPL];
     {
@@ -544,29 +551,32 @@ __global__ __launch_bounds__(64 * W) void paged_stream_kernel(const stream_args 
         const int sidx = pend_sh[w][0][0] == u ? 0 : 1;
         stp[m] = lds_all + w * S::WAVE_LDS + (sidx == 0 ? (int)(pst - ring) : 0);
       }
+      float2 ml[CPL][W];
+      float4_t v[CPL][W];
 #pragma unroll
       for (int q = 0; q < CPL; ++q) {
         const int c = lane + 64 * q;
         const int cc = c < n4 ? c : 0;
         const int head = (4 * cc) / D;
-        float2 ml[W];
-        float4_t v[W];
 #pragma unroll
         for (int m = 0; m < W; ++m) {
-          ml[m] = *reinterpret_cast<const float2*>(stp[m] + 4 * 8 * D + 8 * head);
-          v[m] = *reinterpret_cast<const float4_t*>(stp[m] + 4 * (head * D + (4 * cc) % D));
+          ml[q][m] = *reinterpret_cast<const float2*>(stp[m] + 4 * 8 * D + 8 * head);
+          v[q][m] = *reinterpret_cast<const float4_t*>(stp[m] + 4 * (head * D + (4 * cc) % D));
         }
+      }
+#pragma unroll
+      for (int q = 0; q < CPL; ++q) {
         float mb = -INFINITY;
 #pragma unroll
         for (int m = 0; m < W; ++m)
-          if (m < cnt) mb = fmaxf(mb, ml[m].x);
+          if (m < cnt) mb = fmaxf(mb, ml[q][m].x);
         float l = 0.f;
         float4_t acc_o = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int m = 0; m < W; ++m) {
-          const float wgt = (m < cnt && ml[m].y > 0.f) ? fast_exp2(ml[m].x - mb) : 0.f;
-          l = fmaf(ml[m].y, wgt, l);
-          acc_o += v[m] * wgt;
+          const float wgt = (m < cnt && ml[q][m].y > 0.f) ? fast_exp2(ml[q][m].x - mb) : 0.f;
+          l = fmaf(ml[q][m].y, wgt, l);
+          acc_o += v[q][m] * wgt;
         }
         Mx[q] = mb;
         L[q] = l;
