@@ -276,6 +276,7 @@ def bench_mixed(args, dev) -> int:
     Hq = wl.num_heads
     results = {}
     dec_kernel = "paged_attn_mfma_kernel (work items)"
+    step_kernels = "paged_step_mfma_kernel (prefill tiles and decode items in one launch)"
     for which, w in (("step", wl), ("prefill", wl.part("prefill")), ("decode", wl.part("decode"))):
         # whole prefill sequences go to tb_paged_prefill in a prefill-only step; a
         # step with decode rows keeps the one launch of tiles and decode items
@@ -284,6 +285,11 @@ def bench_mixed(args, dev) -> int:
         meta = build_step_metadata(w.positions, w.seq_slices, w.block_tables, w.context_lens,
                                    block_size=w.block_size, num_blocks=w.num_blocks, partition_tokens=P,
                                    rows_per_item=rows, tile_prefill=not args.no_tiles, prefill_route=route)
+        split = which == "step" and not args.no_split_step and ops.attach_split_parts(
+            meta, w.positions, w.seq_slices, w.block_tables, w.context_lens, num_heads=Hq,
+            num_kv_heads=wl.num_kv_heads, head_dim=wl.head_dim, dtype=wl.dtype, device=dev, rows=rows)
+        if split:
+            step_kernels = "paged_prefill_stream_kernel + paged_stream_kernel (split step)"
         if which == "decode" and not args.no_decode_stream and ops.decode_kernel_preferred(
                 meta, num_kv_heads=wl.num_kv_heads, head_dim=wl.head_dim, dtype=wl.dtype):
             if ops.attach_decode_plan(meta, num_heads=Hq, num_kv_heads=wl.num_kv_heads, head_dim=wl.head_dim,
@@ -341,7 +347,7 @@ def bench_mixed(args, dev) -> int:
         "config": {"workload": f"{wl.name}: 8 x 512-token prefills + 56 decodes (24 share a 32-block "
                                f"prefix) per layer, {L} layer pools; 1024-block copy over all pools",
                    "tokens": wl.num_tokens, "layers": L, "partition_tokens": P, "rows_per_item": rows,
-                   "prefill_tiles": not args.no_tiles, "graph": graph},
+                   "prefill_tiles": not args.no_tiles, "graph": graph, "step_kernels": step_kernels},
         "step_us_per_layer": round(step_ms * 1e3, 3),
         "step_algorithmic_GBps": round(step_gbs, 2),
         "prefill_us_per_layer": round(pre_ms * 1e3, 3),
@@ -483,6 +489,9 @@ def main() -> int:
     ap.add_argument("--no-decode-stream", action="store_true",
                     help="mixed workload: the decode rows through work items even where the streaming "
                          "decode kernel is preferred")
+    ap.add_argument("--no-split-step", action="store_true",
+                    help="mixed workload: the whole step as one launch of prefill tiles and decode items, not "
+                         "tb_paged_prefill + the streaming decode kernel on their own rows")
     ap.add_argument("--no-stream-prefill", action="store_true",
                     help="mixed workload: prefill sequences through the tile kernel, not tb_paged_prefill")
     ap.add_argument("--cpu-reps", type=int, default=5)

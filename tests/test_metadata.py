@@ -227,3 +227,79 @@ def test_pack_decode_step_rejects_what_the_builder_rejects():
         pack_decode_step(h, o, 4, 8, [129], [list(range(9))], **dict(kw, num_blocks=20))
     # two rows writing one slot: left to the general builder's last-writer rule
     assert not pack_decode_step(h, o, 4, 8, [5, 5], [[2], [2]], **kw)
+
+
+def _split_case(order="pre-dec"):
+    # two whole prefills (64 and 33 new rows) and three decode rows, in row order
+    BS = 16
+    pre = [(64, [1, 2, 3, 4]), (33, [5, 6, 7])]
+    dec = [(40, [8, 9, 10]), (17, [11, 12]), (100, [13, 14, 15, 16, 17, 18, 19])]
+    seqs = pre + [("d", c, t) for c, t in dec] if order == "pre-dec" else [("d", c, t) for c, t in dec] + pre
+    positions, slices, tables, ctx, r = [], [], [], [], 0
+    for s in seqs:
+        if s[0] == "d":
+            _, c, t = s
+            positions.append(c - 1)
+            slices.append((r, r + 1))
+            r += 1
+        else:
+            n, t = s
+            c = n
+            positions.extend(range(n))
+            slices.append((r, r + n))
+            r += n
+        tables.append(t)
+        ctx.append(c)
+    return positions, slices, tables, ctx, BS
+
+
+@pytest.mark.parametrize("order", ["pre-dec", "dec-pre"])
+def test_split_step_parts_rebase_each_side(order):
+    from tinybatch_amd.metadata import PrefillRoute, split_step_parts
+
+    positions, slices, tables, ctx, BS = _split_case(order)
+    route = PrefillRoute(num_kv_heads=2, head_dim=64, max_context=560)
+    parts = split_step_parts(positions, slices, tables, ctx, block_size=BS, num_blocks=32, partition_tokens=256,
+                             rows_per_item=2, prefill_route=route)
+    assert parts is not None and len(parts) == 2
+    T = len(positions)
+    assert parts[0][0] == 0 and parts[-1][1] == T and parts[0][1] == parts[1][0]   # the rows, once each
+    full = build_step_metadata(positions, slices, tables, ctx, block_size=BS, num_blocks=32, partition_tokens=256)
+    for r0, r1, m in parts:
+        assert m.num_tokens == r1 - r0
+        # the sub-step's slots are the whole step's slots of the same rows
+        assert np.array_equal(m.slot_mapping_np, full.slot_mapping_np[r0:r1])
+        if m.decode_only:
+            assert m.rows_are_seqs and m.num_seqs == 3
+            assert np.array_equal(m.row_ctx_np, full.row_ctx_np[r0:r1])
+        else:
+            assert m.num_work_items == 0 and m.num_prefill_tiles == 0 and m.num_prefill_work > 0
+
+
+def test_split_step_parts_refuse_other_shapes():
+    from tinybatch_amd.metadata import PrefillRoute, split_step_parts
+
+    positions, slices, tables, ctx, BS = _split_case()
+    kw = dict(block_size=BS, num_blocks=32, partition_tokens=256, rows_per_item=2)
+    route = PrefillRoute(num_kv_heads=2, head_dim=64, max_context=560)
+    # a prefill longer than the kernel serves
+    assert split_step_parts(positions, slices, tables, ctx, prefill_route=route._replace(max_context=48), **kw) is None
+    # decode rows on both sides of the prefills
+    p2, s2, t2, c2, _ = _split_case()
+    order = [2, 0, 1, 3, 4]
+    rows, sl, r = [], [], 0
+    for i in order:
+        b, e = s2[i]
+        rows.extend(p2[b:e])
+        sl.append((r, r + e - b))
+        r += e - b
+    assert split_step_parts(rows, sl, [t2[i] for i in order], [c2[i] for i in order], prefill_route=route,
+                            **kw) is None
+    # a short tail of new rows (not a whole prefill, not a decode row)
+    assert split_step_parts(positions[:67] + [70, 71] + positions[97:], [(0, 64), (64, 67)] + [(67, 69)] +
+                            [(69 + i, 70 + i) for i in range(3)], [tables[0], tables[1], [20, 21, 22, 23, 24]] +
+                            tables[2:], [64, 3, 72] + ctx[2:], prefill_route=route, **kw) is None
+    # no decode rows, or no prefills: nothing to split
+    assert split_step_parts(positions[:97], slices[:2], tables[:2], ctx[:2], prefill_route=route, **kw) is None
+    assert split_step_parts(positions[97:], [(i, i + 1) for i in range(3)], tables[2:], ctx[2:],
+                            prefill_route=route, **kw) is None

@@ -8,7 +8,8 @@ block sizes 16 to 64; new-row counts that are not multiples of 16 (a lone middle
 block, a last block of one row); cached prefixes (pos0 > 0); contexts at the
 longest the kernel serves; stale NaN slots past every context; a step mixing these
 sequences with decode rows and with sequences past the kernel's limit (which keep
-the tiles); the config-4 mixed step; fused RoPE equal to rotating q first."""
+the tiles); the config-4 mixed step, also split into its prefill and decode sides;
+fused RoPE equal to rotating q first."""
 import pytest
 import torch
 
@@ -114,6 +115,44 @@ def test_config4_mixed_step():
              q=wl.q, NB=wl.num_blocks, Hq=14, Hkv=2, D=64, BS=16, dtype=torch.bfloat16)
     meta = check(c)
     assert meta.num_prefill_work == 8 * 16 * 2          # 8 sequences x 16 block pairs x 2 kv heads
+
+
+def test_config4_split_step_against_the_oracle_and_the_one_launch():
+    """The config-4 step (8 whole prefills, then 56 decode rows) as two sub-steps
+    (ops.attach_split_parts: tb_paged_prefill on the prefill rows, the streaming
+    decode kernel on the decode rows): within the bar of the oracle, and of the
+    one launch of tiles and decode items the same metadata runs without its parts;
+    the drop-in cache takes the split by itself."""
+    from tinybatch_amd.kv_cache import PagedKVCache
+    from tinybatch_amd.workloads import make_mixed_workload
+
+    wl = make_mixed_workload()
+    dt, Hq, Hkv, D = wl.dtype, wl.num_heads, wl.num_kv_heads, wl.head_dim
+    want = ref.attention(wl.q, wl.pool, wl.seq_slices, wl.block_tables, wl.context_lens, Hq, Hkv)
+    meta = build_step_metadata(wl.positions, wl.seq_slices, wl.block_tables, wl.context_lens, block_size=16,
+                               num_blocks=wl.num_blocks, partition_tokens=ops.partition_tokens(dt, D),
+                               rows_per_item=ops.rows_per_item(dt, Hq, Hkv), tile_prefill=True)
+    assert ops.attach_split_parts(meta, wl.positions, wl.seq_slices, wl.block_tables, wl.context_lens, num_heads=Hq,
+                                  num_kv_heads=Hkv, head_dim=D, dtype=dt, device=DEV)
+    (r0, r1, pre), (d0, d1, dec) = meta.parts
+    assert (r0, r1, d0, d1) == (0, 4096, 4096, 4152) and dec.decode_plan_np is not None and pre.num_prefill_work
+    meta.to(DEV)
+    q, pool = wl.q.to(DEV), wl.pool.to(DEV)
+    split = ops.paged_attention(q, pool, meta, num_heads=Hq)
+    parts, meta.parts = meta.parts, None
+    one = ops.paged_attention(q, pool, meta, num_heads=Hq)
+    meta.parts = parts
+    cache = PagedKVCache(1, wl.num_blocks, 16, Hkv, D, DEV, dt)
+    cache.pools[0].copy_(pool)
+    drop_in = cache.attention(0, q, torch.tensor(wl.positions, device=DEV), wl.seq_slices, wl.block_tables,
+                              wl.context_lens, num_heads=Hq)
+    torch.cuda.synchronize()
+    assert cache._meta_cache[0]["meta"].parts is not None
+    for got in (split, one, drop_in):
+        assert torch.isfinite(got.cpu()).all()
+        torch.testing.assert_close(got.cpu().float(), want.float(), **TOL)
+    torch.testing.assert_close(split.cpu().float(), one.cpu().float(), **TOL)
+    assert torch.equal(_bits(split.cpu()), _bits(drop_in.cpu()))
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])

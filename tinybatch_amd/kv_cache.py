@@ -68,7 +68,9 @@ class PagedKVCache:
         ``num_heads`` (query heads), a decode-only step that the streaming decode
         kernel serves faster (ops.decode_kernel_preferred) also gets its plan, and
         attention() / decode_step() with this metadata then run that kernel; a
-        prefill-only step goes to tb_paged_prefill.
+        prefill-only step goes to tb_paged_prefill, and a step of whole prefills
+        beside a run of decode rows to tb_paged_prefill and the decode kernel, each
+        on its own rows (ops.attach_split_parts), when the decode rows gain by it.
         """
         pos_key = (positions, positions._version) if isinstance(positions, torch.Tensor) else list(positions)
         for e in self._meta_cache:
@@ -93,6 +95,14 @@ class PagedKVCache:
                                    block_size=self.block_size, num_blocks=self.num_blocks,
                                    partition_tokens=self.partition_tokens, rows_per_item=rows_per_item,
                                    tile_prefill=tile, prefill_route=route)
+        if num_heads is not None and context_lens is not None and self.device.type == "cuda" and tile \
+                and route is None:
+            # whole prefills beside a run of decode rows: tb_paged_prefill and the
+            # streaming decode kernel on their own rows, when the decode rows gain
+            ops.attach_split_parts(meta, positions if host_positions is None else host_positions, seq_slices,
+                                   block_tables, context_lens, num_heads=num_heads, num_kv_heads=self.n_kv_heads,
+                                   head_dim=self.head_dim, dtype=self.dtype, device=self.device,
+                                   rows=rows_per_item)
         if (num_heads is not None and context_lens is not None and self.device.type == "cuda"
                 and ops.decode_kernel_preferred(meta, num_kv_heads=self.n_kv_heads, head_dim=self.head_dim,
                                                 dtype=self.dtype)):

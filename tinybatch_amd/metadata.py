@@ -98,9 +98,16 @@ class StepMetadata:
     num_prefill_work: int = 0
     prefill_max_tiles: int = 0
     prefill_work: torch.Tensor | None = None
+    # a mixed step served as sub-steps (split_step_parts): (first row, end row, the
+    # sub-step's metadata with rows counted from the first row); the arrays above
+    # still describe the whole step (its slot mapping serves the append)
+    parts: list | None = None
 
     def to(self, device: torch.device) -> "StepMetadata":
-        """Upload every array with one host-to-device copy (views into one buffer)."""
+        """Upload every array with one host-to-device copy (views into one buffer);
+        the parts' arrays get copies of their own."""
+        for _, _, m in self.parts or ():
+            m.to(device)
         parts = [self.slot_mapping_np, self.block_tables_np.reshape(-1), self.work_np.reshape(-1),
                  self.row_part_off_np, self.prefill_tiles_np.reshape(-1), self.split_rows_np.reshape(-1)]
         extra = [x for x in (self.decode_plan_np, self.slot_map_np, self.prefill_work_np) if x is not None]
@@ -131,6 +138,46 @@ class StepMetadata:
         if self.prefill_work_np is not None:
             self.prefill_work = buf.narrow(0, int(offs[k]), parts[k].size)
         return self
+
+
+def split_step_parts(positions, seq_slices, block_tables, context_lens, *, block_size: int, num_blocks: int,
+                     partition_tokens: int, rows_per_item: int, prefill_route: "PrefillRoute") -> list | None:
+    """A mixed step whose sequences are whole prefills that ``prefill_route`` serves
+    (>= 16 new rows, context within its limit) on one side and decode rows (one
+    new row each) on the other, each side a contiguous run of rows: the two
+    sub-steps as [(row0, row1, metadata), ...] in row order, rows counted from
+    row0 (so q[row0:row1] and out[row0:row1] are the sub-step's rows). The
+    prefill side's metadata carries only its tb_paged_prefill work list. None
+    for any other step shape."""
+    B = len(seq_slices)
+    if B < 2 or context_lens is None or prefill_route is None:
+        return None
+    pos = _host_positions(positions)
+    qlens = [int(e) - int(b) for b, e in seq_slices]
+    is_pre = [n >= 16 and int(c) <= prefill_route.max_context for n, c in zip(qlens, context_lens)]
+    is_dec = [n == 1 for n in qlens]
+    if not all(p or d for p, d in zip(is_pre, is_dec)):
+        return None
+    # one change of kind in sequence order, and rows contiguous in that order
+    kinds = [0 if d else 1 for d in is_dec]
+    cut = next((i for i in range(1, B) if kinds[i] != kinds[i - 1]), None)
+    if cut is None or any(kinds[i] != kinds[cut] for i in range(cut, B)):
+        return None
+    if any(int(seq_slices[i][0]) != int(seq_slices[i - 1][1]) for i in range(1, B)):
+        return None
+    parts = []
+    for lo, hi in ((0, cut), (cut, B)):
+        r0, r1 = int(seq_slices[lo][0]), int(seq_slices[hi - 1][1])
+        sl = [(int(b) - r0, int(e) - r0) for b, e in seq_slices[lo:hi]]
+        pre = kinds[lo] == 1
+        m = build_step_metadata(pos[r0:r1], sl, block_tables[lo:hi], list(context_lens[lo:hi]),
+                                block_size=block_size, num_blocks=num_blocks, partition_tokens=partition_tokens,
+                                rows_per_item=rows_per_item, tile_prefill=pre,
+                                prefill_route=prefill_route if pre else None)
+        if pre and (m.num_work_items or m.num_prefill_tiles):
+            return None
+        parts.append((r0, r1, m))
+    return parts
 
 
 # The prefill kernel's tile shape (TB_PREFILL_TILE_ROWS / TB_PREFILL_TILE_PARTITION

@@ -266,6 +266,38 @@ def attach_decode_plan(meta: StepMetadata, *, num_heads: int, num_kv_heads: int,
                   workgroups=d.workgroups, num_xcds=d.num_xcds, waves=waves, unit_cost=unit_cost)
 
 
+def attach_split_parts(meta: StepMetadata, positions, seq_slices, block_tables, context_lens, *, num_heads: int,
+                       num_kv_heads: int, head_dim: int, dtype: torch.dtype, device: torch.device,
+                       rows: int | None = None) -> bool:
+    """For a mixed step of whole prefills (that tb_paged_prefill serves) on one side
+    and decode rows on the other (metadata.split_step_parts), attach the two
+    sub-steps to ``meta`` (before meta.to()) when the decode side is one the
+    streaming decode kernel serves faster (decode_kernel_preferred):
+    paged_attention then runs tb_paged_prefill on the prefill rows and
+    tb_paged_decode on the decode rows, in place of one launch of prefill tiles
+    and decode work items. Returns whether it did."""
+    from .metadata import split_step_parts
+
+    route = prefill_route(dtype, num_heads, num_kv_heads, head_dim, device)
+    if route is None or meta.decode_only:
+        return False
+    if rows is None:                 # query rows per work item, as the full step's metadata
+        rows = rows_per_item(dtype, num_heads, num_kv_heads)
+    parts = split_step_parts(positions, seq_slices, block_tables, context_lens, block_size=meta.block_size,
+                             num_blocks=meta.num_blocks, partition_tokens=meta.partition_tokens,
+                             rows_per_item=rows, prefill_route=route)
+    if parts is None:
+        return False
+    dec = next(m for _, _, m in parts if m.decode_only)
+    if not decode_kernel_preferred(dec, num_kv_heads=num_kv_heads, head_dim=head_dim, dtype=dtype):
+        return False
+    if not attach_decode_plan(dec, num_heads=num_heads, num_kv_heads=num_kv_heads, head_dim=head_dim,
+                              dtype=dtype, device=device):
+        return False
+    meta.parts = parts
+    return True
+
+
 def attach_xcd_slot_map(meta: StepMetadata, *, num_heads: int, num_kv_heads: int, dtype: torch.dtype,
                         device: torch.device) -> bool:
     """metadata.attach_xcd_slot_map with this device's XCDs, when the device runs workgroup
@@ -387,6 +419,19 @@ def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, 
     if meta.decode_plan is not None and not noalloc and q.dtype in (torch.float16, torch.bfloat16):
         return paged_decode(q, pool, meta, num_heads=num_heads, scale=scale, out=out, k_new=k_new, v_new=v_new,
                             rope=rope)
+    if meta.parts is not None and not noalloc and k_new is None and v_new is None:
+        # a split mixed step (attach_split_parts): each sub-step on its own rows
+        _lib.require_gpu_tensor("q", q)
+        d = pool.shape[-1]
+        if q.shape[0] != meta.num_tokens:
+            raise ValueError(f"q has {q.shape[0]} rows, metadata describes {meta.num_tokens}")
+        if out is None:
+            out = torch.empty(q.shape[0], num_heads * d, device=q.device, dtype=q.dtype)
+        elif out.shape[0] != q.shape[0]:
+            raise ValueError("out must match q's row count")
+        for r0, r1, m in meta.parts:
+            paged_attention(q[r0:r1], pool, m, num_heads=num_heads, scale=scale, out=out[r0:r1], rope=rope)
+        return out
     nb, hkv, bs, d = _check_pool(pool)
     _lib.require_gpu_tensor("q", q)
     if q.dtype != pool.dtype:
