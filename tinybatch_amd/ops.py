@@ -279,7 +279,12 @@ def attach_split_parts(meta: StepMetadata, positions, seq_slices, block_tables, 
     from .metadata import split_step_parts
 
     route = prefill_route(dtype, num_heads, num_kv_heads, head_dim, device)
-    if route is None or meta.decode_only:
+    if route is None or meta.decode_only or context_lens is None:
+        return False
+    # the decode side's size first (the sub-steps are only built when it qualifies)
+    dec_ctx = [int(c) for (b, e), c in zip(seq_slices, context_lens) if int(e) - int(b) == 1]
+    if len(dec_ctx) * num_kv_heads < 32 or \
+            sum(dec_ctx) * num_kv_heads * head_dim * 2 * 2 < DECODE_KERNEL_MIN_BYTES:
         return False
     if rows is None:                 # query rows per work item, as the full step's metadata
         rows = rows_per_item(dtype, num_heads, num_kv_heads)
