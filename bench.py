@@ -289,7 +289,8 @@ def bench_mixed(args, dev) -> int:
             meta, w.positions, w.seq_slices, w.block_tables, w.context_lens, num_heads=Hq,
             num_kv_heads=wl.num_kv_heads, head_dim=wl.head_dim, dtype=wl.dtype, device=dev, rows=rows)
         if split:
-            step_kernels = "paged_prefill_stream_kernel + paged_stream_kernel (split step)"
+            step_kernels = ("paged_prefill_stream_kernel + paged_stream_kernel (split step, each appending "
+                            "its own rows)")
         if which == "decode" and not args.no_decode_stream and ops.decode_kernel_preferred(
                 meta, num_kv_heads=wl.num_kv_heads, head_dim=wl.head_dim, dtype=wl.dtype):
             if ops.attach_decode_plan(meta, num_heads=Hq, num_kv_heads=wl.num_kv_heads, head_dim=wl.head_dim,
@@ -300,12 +301,16 @@ def bench_mixed(args, dev) -> int:
         out = torch.empty(w.num_tokens, Hq * w.head_dim, dtype=w.dtype, device=dev)
         ws = ops.workspace_for(meta, Hq, w.head_dim, dev)
         append = which == "step"
+        # a split step appends inside its two kernels (each side its own rows); the one
+        # launch of tiles and items needs the append kernel first
+        fuse = append and split
 
-        def step(meta=meta, q=q, k=k, v=v, out=out, ws=ws, append=append):
+        def step(meta=meta, q=q, k=k, v=v, out=out, ws=ws, append=append, fuse=fuse):
             for pool in pools:
-                if append:
+                if append and not fuse:
                     ops.kv_append(pool, k, v, meta.slot_mapping)
-                ops.paged_attention(q, pool, meta, num_heads=Hq, out=out, workspace=ws)
+                ops.paged_attention(q, pool, meta, num_heads=Hq, out=out, workspace=ws,
+                                    k_new=k if fuse else None, v_new=v if fuse else None)
 
         ms, graph = time_step(step, dev, args)
         results[which] = (ms / L, w)

@@ -219,17 +219,27 @@ int32_t tb_build_step_metadata(const int32_t* query_start_loc, int32_t num_seqs,
  * nb-1-p) and the kv head's query heads share it; every row's output is written
  * whole (no workspace). The rows it serves must not also be given to
  * tb_paged_attention. The K/V of the step's new rows must already be in the pool
- * (append first).
+ * (append first), unless k_new / v_new are given:
+ *   k_new, v_new (may be NULL, both or neither): the step's new K / V rows
+ *     [num_rows][num_kv_heads][head_dim] (row strides in elements, 16-byte
+ *     aligned); the kernel then reads each sequence's new rows from them and
+ *     stores them to their pool slots (the append of kv_cache.py:25-38 fused:
+ *     the pool afterwards equals tb_kv_append's, bit for bit). Needs every
+ *     sequence's first new position (pos0) to be a multiple of 16 and no RoPE
+ *     (TB_ERR_UNSUPPORTED with rope tables); with another pos0 the rows of
+ *     that sequence are wrong (nothing is read or written out of bounds).
  *   work: tb_build_prefill_work's list (device memory), num_work entries;
  *     max_tiles: the value the builder returned.
  * q, out, strides, scale, dtype, rope: as tb_paged_attention. */
 #define TB_PREFILL_STREAM_LDS (144 * 1024)
-int32_t tb_paged_prefill(const void* q, int64_t q_row_stride, const void* pool, int64_t num_blocks,
+int32_t tb_paged_prefill(const void* q, int64_t q_row_stride, void* pool, int64_t num_blocks,
                          void* out, int64_t out_row_stride, const int32_t* block_tables,
                          int32_t max_blocks_per_seq, const int32_t* work, int32_t num_work,
                          int32_t max_tiles, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
-                         int32_t block_size, float scale, int32_t dtype, const float* rope_cos,
-                         const float* rope_sin, int32_t rope_max_position, hipStream_t stream);
+                         int32_t block_size, float scale, int32_t dtype,
+                         const void* k_new, int64_t k_row_stride, const void* v_new, int64_t v_row_stride,
+                         const float* rope_cos, const float* rope_sin, int32_t rope_max_position,
+                         hipStream_t stream);
 /* The longest context (positions) and the most query heads per kv head
  * tb_paged_prefill serves at a head dim (0: none). */
 int32_t tb_prefill_stream_max_context(int32_t head_dim);

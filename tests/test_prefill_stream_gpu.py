@@ -8,8 +8,10 @@ block sizes 16 to 64; new-row counts that are not multiples of 16 (a lone middle
 block, a last block of one row); cached prefixes (pos0 > 0); contexts at the
 longest the kernel serves; stale NaN slots past every context; a step mixing these
 sequences with decode rows and with sequences past the kernel's limit (which keep
-the tiles); the config-4 mixed step, also split into its prefill and decode sides;
-fused RoPE equal to rotating q first."""
+the tiles); the config-4 mixed step, also split into its prefill and decode sides
+(with and without the appends folded into both kernels); fused RoPE equal to
+rotating q first; the fused append (new rows read from k / v and stored: the pool
+bit-exact against the oracle's append) and what it refuses."""
 import pytest
 import torch
 
@@ -170,3 +172,76 @@ def test_fused_rope_equals_rotating_first(dtype):
     out_b = ops.paged_attention(qr.contiguous(), pool, meta, num_heads=14)
     torch.cuda.synchronize()
     assert torch.equal(_bits(out_a), _bits(out_b))
+
+
+@pytest.mark.parametrize("BS", [16, 32])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fused_append_stores_the_new_rows_and_reads_them_from_k_v(BS, dtype):
+    """k_new / v_new given: the kernel reads each sequence's new rows from them (the
+    pool's new slots hold NaN before the call) and stores them: the pool afterwards
+    equals the oracle's append bit for bit, the attention is within the bar of the
+    oracle on that pool. New rows 17 .. 100 after cached prefixes of 0 and 32."""
+    qlens, cached = [17, 100, 33, 16], [0, 32, 0, 64]
+    c = case(BS + 7, 14, 2, 64, BS, dtype, qlens, cached)
+    g = torch.Generator().manual_seed(BS)
+    T = sum(qlens)
+    k = torch.randn(T, 2, 64, generator=g).to(dtype)
+    v = torch.randn(T, 2, 64, generator=g).to(dtype)
+    pos = torch.tensor(c["pos"], dtype=torch.int64)
+    want_pool = c["pool"].clone()
+    ref.kv_write(want_pool, k, v, pos, c["slices"], c["tables"], BS)
+    want = ref.attention(c["q"], want_pool, c["slices"], c["tables"], c["ctx"], 14, 2)
+    stale = c["pool"].clone()
+    for (b, e), table, p0 in zip(c["slices"], c["tables"], cached):   # the new slots: NaN before the call
+        for i in range(e - b):
+            p = p0 + i
+            stale[table[p // BS], :, :, p % BS] = float("nan")
+    meta = metadata(c)
+    assert meta.num_prefill_work and not meta.num_work_items and not meta.num_prefill_tiles
+    pool = stale.to(DEV)
+    out = ops.paged_attention(c["q"].to(DEV), pool, meta, num_heads=14, k_new=k.to(DEV), v_new=v.to(DEV))
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(pool.cpu()), _bits(want_pool))
+    got = out.cpu()
+    assert torch.isfinite(got).all()
+    torch.testing.assert_close(got.float(), want.float(), **TOL)
+
+
+def test_fused_append_refuses_what_it_cannot_serve():
+    c = case(5, 14, 2, 64, 16, torch.bfloat16, [20, 30], [8, 0])    # new rows from position 8
+    meta = metadata(c)
+    k = torch.zeros(50, 2, 64, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError, match="multiple of 16"):
+        ops.paged_attention(c["q"].to(DEV), c["pool"].to(DEV), meta, num_heads=14, k_new=k, v_new=k)
+    c = case(6, 14, 2, 64, 16, torch.bfloat16, [20, 30], [16, 0])
+    meta = metadata(c)
+    cos, sin = rope_tables(64, 1e4, 256, DEV)
+    with pytest.raises(ValueError, match="no rope"):
+        ops.paged_attention(c["q"].to(DEV), c["pool"].to(DEV), meta, num_heads=14, k_new=k, v_new=k,
+                            rope=ops.Rope(cos, sin))
+
+
+def test_config4_split_step_appending_in_both_kernels():
+    """The config-4 step split into its sides, each kernel appending its own rows
+    (no kv_append): the pool equals the oracle's append bit for bit, the
+    attention is within the bar of the oracle on that pool."""
+    from tinybatch_amd.workloads import make_mixed_workload
+
+    wl = make_mixed_workload()
+    dt, Hq, Hkv, D = wl.dtype, wl.num_heads, wl.num_kv_heads, wl.head_dim
+    want_pool = wl.pool.clone()
+    ref.kv_write(want_pool, wl.k_new, wl.v_new, torch.tensor(wl.positions, dtype=torch.int64), wl.seq_slices,
+                 wl.block_tables, 16)
+    want = ref.attention(wl.q, want_pool, wl.seq_slices, wl.block_tables, wl.context_lens, Hq, Hkv)
+    meta = build_step_metadata(wl.positions, wl.seq_slices, wl.block_tables, wl.context_lens, block_size=16,
+                               num_blocks=wl.num_blocks, partition_tokens=ops.partition_tokens(dt, D),
+                               rows_per_item=ops.rows_per_item(dt, Hq, Hkv), tile_prefill=True)
+    assert ops.attach_split_parts(meta, wl.positions, wl.seq_slices, wl.block_tables, wl.context_lens, num_heads=Hq,
+                                  num_kv_heads=Hkv, head_dim=D, dtype=dt, device=DEV)
+    meta.to(DEV)
+    pool = wl.pool.to(DEV)
+    out = ops.paged_attention(wl.q.to(DEV), pool, meta, num_heads=Hq, k_new=wl.k_new.to(DEV),
+                              v_new=wl.v_new.to(DEV))
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(pool.cpu()), _bits(want_pool))
+    torch.testing.assert_close(out.cpu().float(), want.float(), **TOL)

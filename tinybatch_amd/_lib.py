@@ -91,6 +91,7 @@ SIGNATURES = {
         c_vp, c_i64, c_vp, c_i64, c_vp, c_i64,   # q, q stride, pool, num_blocks, out, out stride
         c_vp, c_i32, c_vp, c_i32, c_i32,         # block tables, max_nb, work, num_work, max_tiles
         c_i32, c_i32, c_i32, c_i32, c_f32, c_i32,   # heads, kv heads, head_dim, block_size, scale, dtype
+        c_vp, c_i64, c_vp, c_i64,                # k_new, k stride, v_new, v stride (fused append, may be NULL)
         c_vp, c_vp, c_i32, c_vp]),               # rope cos, sin, max position, stream
     "tb_prefill_stream_max_context": (c_i32, [c_i32]),
     "tb_prefill_stream_max_group": (c_i32, [c_i32]),

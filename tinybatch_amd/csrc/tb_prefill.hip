@@ -41,7 +41,7 @@ namespace tb {
 struct prefill_args {
   const char* q;               // [T][Hq][D] rows of the step
   int64_t q_row_bytes;
-  const char* pool;            // [NB][2][Hkv][BS][D]
+  char* pool;                  // [NB][2][Hkv][BS][D]
   int64_t num_blocks;
   char* out;                   // [T][Hq*D]
   int64_t out_row_bytes;
@@ -52,6 +52,13 @@ struct prefill_args {
   int32_t log2_bs;             // block size: a power of two >= 16
   float scale_log2e;
   rope_tables rope;
+  // fused append (may be null): the step's new K / V rows [T][Hkv][D]; a sequence's
+  // new rows (positions pos0 .., pos0 a multiple of 16) are read from here and
+  // stored to their pool slots by the workgroup of block pair 0
+  const char* k_new;
+  int64_t k_new_row_bytes;
+  const char* v_new;
+  int64_t v_new_row_bytes;
 };
 
 template <int D>
@@ -360,9 +367,27 @@ __global__ __launch_bounds__(pshape<D>::MAXREP / pshape<D>::HPW * 128, 1) void p
     }
     for (int j = 0; wave + NW * j < T; ++j) {
       const int t = wave + NW * j;
+      char* const dst = lds + t * TILE;
+      if (a.k_new != nullptr && 16 * t >= pos0) {
+        // a tile of new rows, from the step's k / v rows (rows past the sequence's
+        // last one repeat it: their scores are masked and their V rows zeroed below)
+        const int nr0 = 16 * t - pos0;                 // the tile's first new row
+        const int last = nrows - 1 - nr0;
+        const char* kb = a.k_new + (int64_t)(row0 + nr0) * a.k_new_row_bytes + (int64_t)kvh * RB;
+        const char* vb = a.v_new + (int64_t)(row0 + nr0) * a.v_new_row_bytes + (int64_t)kvh * RB;
+#pragma unroll
+        for (int i = 0; i < TLD; ++i) {
+          const int f = 64 * i + lane;
+          const int r = f / VCOLS, cs = f % VCOLS;
+          const int rr = r < last ? r : last;
+          s_dma16_l2((uint32_t)(rr * a.k_new_row_bytes) + 16u * (uint32_t)(cs ^ stream_kswz(r)), kb, dst + 1024 * i);
+          s_dma16_l2((uint32_t)(rr * a.v_new_row_bytes) + 16u * (uint32_t)(cs ^ stream_vswz(r)), vb,
+                     dst + TB + 1024 * i);
+        }
+        continue;
+      }
       const int b = __builtin_amdgcn_readlane(myb, j);
       const char* base = a.pool + (int64_t)b * blk_bytes + kvh * head_bytes + (int64_t)(t & sub_mask) * TB;
-      char* const dst = lds + t * TILE;
 #pragma unroll
       for (int i = 0; i < TLD; ++i) {
         s_dma16_l2(koff[i], base, dst + 1024 * i);
@@ -413,6 +438,29 @@ __global__ __launch_bounds__(pshape<D>::MAXREP / pshape<D>::HPW * 128, 1) void p
       }
     }
     __syncthreads();
+    if (c == 0 && pair == 0 && a.k_new != nullptr) {
+      // the fused append: the workgroup of block pair 0 holds every new row of the
+      // sequence for this kv head; each wave stores the new-row tiles it loaded,
+      // from LDS (chunk f of a tile holds row f / VCOLS, chunk (f % VCOLS) ^ swizzle)
+      for (int j = 0; wave + NW * j < T; ++j) {
+        const int t = wave + NW * j;
+        if (16 * t < pos0) continue;
+        const int valid = min(16, pos0 + nrows - 16 * t);   // new rows in the tile
+        const int b = __builtin_amdgcn_readlane(myb, j);
+        char* const pk = a.pool + (int64_t)b * blk_bytes + kvh * head_bytes +
+                         (int64_t)(t & sub_mask) * TB;
+        const char* const src = lds + t * TILE;
+#pragma unroll
+        for (int i = 0; i < TLD; ++i) {
+          const int f = 64 * i + lane;
+          const int r = f / VCOLS, cs = f % VCOLS;
+          if (r < valid) {
+            st16(pk + r * RB + 16 * (cs ^ stream_kswz(r)), *reinterpret_cast<const vec16*>(src + 16 * f));
+            st16(pk + v_off + r * RB + 16 * (cs ^ stream_vswz(r)), *reinterpret_cast<const vec16*>(src + TB + 16 * f));
+          }
+        }
+      }
+    }
     const int s0 = (CH / 2) * c;
     const int nl = max(0, min(s0 + CH / 2, sl) - s0);    // later-block steps in the chunk
     const int ne = max(0, min(s0 + CH / 2, se) - s0);    // earlier-block steps in the chunk
@@ -594,12 +642,14 @@ void launch_prefill_stream(const tb::prefill_args& a, int num_work, hipStream_t 
 
 }  // namespace
 
-extern "C" int32_t tb_paged_prefill(const void* q, int64_t q_row_stride, const void* pool, int64_t num_blocks,
+extern "C" int32_t tb_paged_prefill(const void* q, int64_t q_row_stride, void* pool, int64_t num_blocks,
                                     void* out, int64_t out_row_stride, const int32_t* block_tables,
                                     int32_t max_blocks_per_seq, const int32_t* work, int32_t num_work,
                                     int32_t max_tiles, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
-                                    int32_t block_size, float scale, int32_t dtype, const float* rope_cos,
-                                    const float* rope_sin, int32_t rope_max_position, hipStream_t stream) {
+                                    int32_t block_size, float scale, int32_t dtype, const void* k_new,
+                                    int64_t k_row_stride, const void* v_new, int64_t v_row_stride,
+                                    const float* rope_cos, const float* rope_sin, int32_t rope_max_position,
+                                    hipStream_t stream) {
   TB_CHECK_ARG(num_work >= 0 && num_heads > 0 && num_kv_heads > 0 && num_heads % num_kv_heads == 0);
   if (num_work == 0) return TB_OK;
   TB_CHECK_ARG(q && pool && out && block_tables && work && num_blocks > 0 && max_blocks_per_seq > 0);
@@ -612,10 +662,18 @@ extern "C" int32_t tb_paged_prefill(const void* q, int64_t q_row_stride, const v
   TB_CHECK_ARG(max_tiles >= 0);
   if (max_tiles >= prefill_max_tiles(head_dim)) return TB_ERR_UNSUPPORTED;
   TB_CHECK_ARG(!rope_cos == !rope_sin && (!rope_cos || rope_max_position > 0));
+  TB_CHECK_ARG(!k_new == !v_new);
+  if (k_new) {
+    if (rope_cos) return TB_ERR_UNSUPPORTED;   // the stored K rows would need the rotation
+    TB_CHECK_ARG(k_row_stride >= (int64_t)num_kv_heads * head_dim && v_row_stride >= (int64_t)num_kv_heads * head_dim);
+    TB_CHECK_ARG((((uintptr_t)k_new | (uintptr_t)v_new) & 15u) == 0 && (k_row_stride * 2) % 16 == 0 &&
+                 (v_row_stride * 2) % 16 == 0);
+    TB_CHECK_ARG(16 * 2 * k_row_stride < ((int64_t)1 << 31) && 16 * 2 * v_row_stride < ((int64_t)1 << 31));
+  }
   tb::prefill_args a{};
   a.q = static_cast<const char*>(q);
   a.q_row_bytes = q_row_stride * 2;
-  a.pool = static_cast<const char*>(pool);
+  a.pool = static_cast<char*>(pool);
   a.num_blocks = num_blocks;
   a.out = static_cast<char*>(out);
   a.out_row_bytes = out_row_stride * 2;
@@ -629,6 +687,10 @@ extern "C" int32_t tb_paged_prefill(const void* q, int64_t q_row_stride, const v
   a.log2_bs = lb;
   a.scale_log2e = scale * 1.4426950408889634f;
   a.rope = tb::rope_tables{rope_cos, rope_sin, rope_max_position};
+  a.k_new = static_cast<const char*>(k_new);
+  a.k_new_row_bytes = k_row_stride * 2;
+  a.v_new = static_cast<const char*>(v_new);
+  a.v_new_row_bytes = v_row_stride * 2;
   if (dtype == TB_DTYPE_F16)
     head_dim == 64 ? launch_prefill_stream<tb::f16_t, 64>(a, num_work, stream)
                    : launch_prefill_stream<tb::f16_t, 128>(a, num_work, stream);

@@ -424,8 +424,10 @@ def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, 
     if meta.decode_plan is not None and not noalloc and q.dtype in (torch.float16, torch.bfloat16):
         return paged_decode(q, pool, meta, num_heads=num_heads, scale=scale, out=out, k_new=k_new, v_new=v_new,
                             rope=rope)
-    if meta.parts is not None and not noalloc and k_new is None and v_new is None:
-        # a split mixed step (attach_split_parts): each sub-step on its own rows
+    if meta.parts is not None and not noalloc and ((k_new is None and v_new is None) or rope is None):
+        # a split mixed step (attach_split_parts): each sub-step on its own rows; with
+        # k_new / v_new each side appends its own rows (no RoPE: the prefill kernel
+        # stores the rows as given)
         _lib.require_gpu_tensor("q", q)
         d = pool.shape[-1]
         if q.shape[0] != meta.num_tokens:
@@ -434,8 +436,12 @@ def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, 
             out = torch.empty(q.shape[0], num_heads * d, device=q.device, dtype=q.dtype)
         elif out.shape[0] != q.shape[0]:
             raise ValueError("out must match q's row count")
+        fused = k_new is not None or v_new is not None
+        if fused and (k_new is None or v_new is None or k_new.shape[0] != q.shape[0] or v_new.shape[0] != q.shape[0]):
+            raise ValueError("k_new and v_new go together, one row per row of q")
         for r0, r1, m in meta.parts:
-            paged_attention(q[r0:r1], pool, m, num_heads=num_heads, scale=scale, out=out[r0:r1], rope=rope)
+            paged_attention(q[r0:r1], pool, m, num_heads=num_heads, scale=scale, out=out[r0:r1], rope=rope,
+                            k_new=k_new[r0:r1] if fused else None, v_new=v_new[r0:r1] if fused else None)
         return out
     nb, hkv, bs, d = _check_pool(pool)
     _lib.require_gpu_tensor("q", q)
@@ -471,11 +477,22 @@ def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, 
         rope.check(d, q.device)
     ksp = vsp = None
     ks = vs = 0
+    prefill_fused = False
     if k_new is not None or v_new is not None:
         if k_new is None or v_new is None:
             raise ValueError("k_new and v_new go together")
-        if not meta.decode_only or meta.num_prefill_tiles or meta.num_prefill_work:
-            raise ValueError("fused append needs a decode-only step (one query row per sequence)")
+        if meta.num_prefill_work and not meta.num_work_items and not meta.num_prefill_tiles:
+            # whole prefill sequences only: tb_paged_prefill reads their new rows from
+            # k_new / v_new and stores them (no RoPE; new rows start on a 16-position tile)
+            if rope is not None:
+                raise ValueError("the prefill kernel's fused append takes rotated rows (no rope)")
+            if np.any(meta.prefill_work_np.reshape(-1, 4)[:meta.num_prefill_work, 2] % 16):
+                raise ValueError("the prefill kernel's fused append needs each sequence's new rows to start "
+                                 "at a multiple of 16 positions: append with kv_append first")
+            prefill_fused = True
+        elif not meta.decode_only or meta.num_prefill_tiles or meta.num_prefill_work:
+            raise ValueError("fused append needs a decode-only step (one query row per sequence) or a step of "
+                             "whole prefills only")
         sm = meta.slot_mapping_np
         if sm.size and np.any((sm < 0) & (meta.row_ctx_np > 0)):
             # a superseded writer of a shared slot: the kernel would store and read each
@@ -496,7 +513,8 @@ def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, 
             meta.row_part_off.data_ptr(), T,
             meta.split_rows.data_ptr(), meta.num_split_rows,
             max(meta.max_parts_per_row, 1), meta.partition_tokens, meta.total_partitions,
-            num_heads, hkv, d, bs, float(scale), _lib.DTYPE_CODE[q.dtype], ksp, ks, vsp, vs)
+            num_heads, hkv, d, bs, float(scale), _lib.DTYPE_CODE[q.dtype],
+            *((None, 0, None, 0) if prefill_fused else (ksp, ks, vsp, vs)))
     tail = (_ptr(meta.device_counts),
             None if rope is None else rope.cos.data_ptr(), None if rope is None else rope.sin.data_ptr(),
             0 if rope is None else rope.max_position, _lib.stream_handle(q.device))
@@ -506,7 +524,8 @@ def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, 
         _lib.check(_lib.lib().tb_paged_prefill(
             q.data_ptr(), qs, pool.data_ptr(), nb, out.data_ptr(), os_, meta.block_tables.data_ptr(),
             meta.max_blocks_per_seq, meta.prefill_work.data_ptr(), meta.num_prefill_work, meta.prefill_max_tiles,
-            num_heads, hkv, d, bs, float(scale), _lib.DTYPE_CODE[q.dtype], *tail[1:]), "tb_paged_prefill")
+            num_heads, hkv, d, bs, float(scale), _lib.DTYPE_CODE[q.dtype],
+            *((ksp, ks, vsp, vs) if prefill_fused else (None, 0, None, 0)), *tail[1:]), "tb_paged_prefill")
     if noalloc:
         if workspace is not None:
             raise ValueError("noalloc takes no workspace")
