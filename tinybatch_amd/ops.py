@@ -439,6 +439,10 @@ def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, 
         fused = k_new is not None or v_new is not None
         if fused and (k_new is None or v_new is None or k_new.shape[0] != q.shape[0] or v_new.shape[0] != q.shape[0]):
             raise ValueError("k_new and v_new go together, one row per row of q")
+        for _, _, m in meta.parts if fused else ():   # refused before any part launches
+            if m.num_prefill_work and np.any(m.prefill_work_np.reshape(-1, 4)[:m.num_prefill_work, 2] % 16):
+                raise ValueError("the prefill kernel's fused append needs each sequence's new rows to start "
+                                 "at a multiple of 16 positions: append with kv_append first")
         for r0, r1, m in meta.parts:
             paged_attention(q[r0:r1], pool, m, num_heads=num_heads, scale=scale, out=out[r0:r1], rope=rope,
                             k_new=k_new[r0:r1] if fused else None, v_new=v_new[r0:r1] if fused else None)
