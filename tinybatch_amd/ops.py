@@ -209,7 +209,12 @@ def decode_device(device: torch.device) -> DecodeDevice:
 # fixed cost per call is lower. Measured on the Qwen 0.5B layer geometry (fp16,
 # block 16, 24 rotating pools), us per call streaming / work items: 8 sequences
 # (12 MB of K/V) 11.3 / 10.2, 16 (22 MB) 11.7 / 12.3, 24 (30 MB) 12.2 / 13.1,
-# 48 (57 MB) 15.6 / 18.2.
+# 48 (57 MB) 15.6 / 18.2 (eight-wave form). With the four-wave default: 8 sequences
+# 10.9 / 9.7 (16 units), 16 sequences 10.8 / 11.9, and the engine's decode shape
+# (bf16, 32 sequences of 400..770 positions, 9.5 MB) 8.3 / 8.5 against the merged
+# items: the crossover now lies near 8 MiB at >= 32 units. The threshold stays
+# at 16 MiB: below it the gain is <= 2%, and lower would also split the engine's
+# mixed steps, whose prefill shapes were not measured split.
 DECODE_KERNEL_MIN_BYTES = 16 << 20
 
 
