@@ -256,17 +256,36 @@ def decode_kernel_preferred(meta: StepMetadata, *, num_kv_heads: int, head_dim: 
     return kv_bytes >= min_bytes
 
 
+# Head dim 64: four waves with two tile pairs in flight each for steps below this
+# many K/V bytes, eight waves with one pair from it on. Same-box runs (Qwen layer,
+# fp16, 24 pools, us per call four / eight waves): 24 sequences (30 MB) 11.4 / 12.0,
+# 32 (40 MB) 12.1 / 12.9, 64 (72 MB) 17.9 / 18.0 on one box and 18.2 / 18.1 on another.
+DECODE_EIGHT_WAVES_MIN_BYTES = 56 << 20
+
+
+def decode_waves_for(meta: StepMetadata, *, num_kv_heads: int, head_dim: int) -> int | None:
+    """The decode kernel variant (waves per workgroup) for a decode-only step, or None
+    for the library's default (head dims other than 64)."""
+    if head_dim != 64:
+        return None
+    kv_bytes = int(meta.row_ctx_np[:meta.num_seqs].astype(np.int64).sum()) * num_kv_heads * head_dim * 2 * 2
+    return 8 if kv_bytes >= DECODE_EIGHT_WAVES_MIN_BYTES else 4
+
+
 def attach_decode_plan(meta: StepMetadata, *, num_heads: int, num_kv_heads: int, head_dim: int,
                        dtype: torch.dtype, device: torch.device, waves: int | None = None,
                        unit_cost: int | None = None) -> bool:
     """metadata.attach_decode_plan with this device's workgroups and XCDs; False (the
     step stays with the work-item kernel) when the device's workgroup placement is not
-    the one the kernel's in-XCD merges assume."""
+    the one the kernel's in-XCD merges assume. ``waves`` None: at head dim 64, the
+    variant for the step's size (decode_waves_for)."""
     from .metadata import attach_decode_plan as attach
 
     d = decode_device(device)
     if not d.merge_in_kernel or d.num_xcds <= 1:
         return False
+    if waves is None:
+        waves = decode_waves_for(meta, num_kv_heads=num_kv_heads, head_dim=head_dim)
     return attach(meta, num_heads=num_heads, num_kv_heads=num_kv_heads, head_dim=head_dim, dtype=dtype,
                   workgroups=d.workgroups, num_xcds=d.num_xcds, waves=waves, unit_cost=unit_cost)
 
