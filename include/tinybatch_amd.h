@@ -182,8 +182,15 @@ int32_t tb_attention_partition_tokens(int32_t dtype, int32_t head_dim);
  *     tb_paged_attention documents, work items ordered by partition length
  *     (shortest first) and tiles by positions covered (most first), both
  *     stable, rows_per_item (1..16) consecutive rows grouped per item;
- *   counts [5] (int64): W, N, S, total_partitions, max_parts_per_row.
- * tb_step_metadata_counts gives the counts alone (the sizes to provide).
+ *   counts [6] (int64): W, N, S, total_partitions, max_parts_per_row, and the
+ *     superseded rows (rows inside a sequence whose slot_mapping is -1
+ *     because a later row writes the same slot). A fused append (k_new given
+ *     to tb_paged_attention, tb_paged_decode or tb_paged_prefill) needs
+ *     counts[5] == 0: each of those rows would attend to its own new K/V,
+ *     where the reference's sequential write lets the last writer win
+ *     (kv_cache.py:33-38); append with tb_kv_append and call without k_new.
+ * tb_step_metadata_counts gives the first five counts alone (the sizes to
+ * provide; it sees no block tables, so counts [5] suffice there).
  * Capacities below the counts: TB_ERR_INVALID_ARG (counts still written).
  * A table shorter than a context or a block id outside [0, num_blocks):
  * TB_ERR_INDEX (the reference's IndexError, kv_cache.py:35,43). partition_tokens
@@ -332,7 +339,13 @@ int32_t tb_paged_attention_noalloc(const void* q, int64_t q_row_stride,
  *     workspace and arrival counters.
  * The workspace holds the split rows' partials as for tb_paged_attention
  * (< 2 GiB). The outputs equal tb_paged_attention's bit for bit.
+ * A row's partitions are counted in 8-bit per-XCD fields of its arrival word:
+ * max_parts_per_row above TB_MERGED_MAX_PARTS returns TB_ERR_UNSUPPORTED and
+ * launches nothing (use tb_paged_attention, whose combine kernel has no such
+ * limit); tb_xcd_slot_map_slots / tb_build_xcd_slot_map refuse such steps the
+ * same way.
  */
+#define TB_MERGED_MAX_PARTS 255
 int32_t tb_paged_attention_merged(const void* q, int64_t q_row_stride, void* pool, int64_t num_blocks,
                                   void* out, int64_t out_row_stride,
                                   const int32_t* block_tables, int32_t max_blocks_per_seq,

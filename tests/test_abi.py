@@ -160,3 +160,30 @@ def test_layer_ops_reject_bad_arguments_without_launching():
     assert la(f, 896, f, 4, 151936, 896, f, need, None, bf16, None) == _lib.TB_ERR_INVALID_ARG    # no ids
     assert la(f, 896, f, 4, 151930, 896, f, need, f, bf16, None) == _lib.TB_ERR_UNSUPPORTED      # N % 16
     assert la(None, 896, None, 0, 151936, 896, None, 0, None, bf16, None) == _lib.TB_OK
+
+
+def test_merged_attention_refuses_rows_of_more_than_255_partitions_without_launching():
+    """tb_paged_attention_merged counts a row's partitions in 8-bit per-XCD fields of its
+    arrival word: 256 or more partitions of one row are refused before any launch (the
+    combine kernel of tb_paged_attention serves them)."""
+    L = _lib.lib()
+    f = ctypes.c_void_p(4096)
+    a128 = ctypes.c_void_p(1 << 20)                    # 128-byte aligned stand-in for the counters
+
+    def call(mpr):
+        tp = 2 * mpr
+        wsb = L.tb_paged_attention_workspace_bytes(tp, 14, 64)
+        return L.tb_paged_attention_merged(f, 896, f, 1 << 16, f, 896, f, 4096, f, tp, f, 2, mpr, 256, tp,
+                                           14, 2, 64, 16, 0.125, 1, None, 0, None, 0, f, wsb,
+                                           f, 8 * tp * 2, a128, 256, f, None, None, 0, None)
+
+    assert call(256) == _lib.TB_ERR_UNSUPPORTED
+    assert call(1000) == _lib.TB_ERR_UNSUPPORTED
+    # the slot-map builders refuse such steps the same way
+    import numpy as np
+    items = np.array([[0, 0, p, 256 * 300] for p in range(300)], dtype=np.int32)
+    vp = lambda x: x.ctypes.data_as(ctypes.c_void_p)
+    assert L.tb_xcd_slot_map_slots(vp(items), 300, 2, 8) == _lib.TB_ERR_UNSUPPORTED
+    out = np.zeros(4096, dtype=np.int32)
+    assert L.tb_build_xcd_slot_map(vp(items), 300, 2, 8, vp(out), 4096) == _lib.TB_ERR_UNSUPPORTED
+    assert L.tb_xcd_slot_map_slots(vp(items[:255]), 255, 2, 8) > 0

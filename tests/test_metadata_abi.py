@@ -43,7 +43,7 @@ def c_build(qlens, ctx, tables, num_blocks, bs, P, rows=1, tiles=False, num_toke
     work = np.zeros((max(cw, 1), 4), np.int32)
     tl = np.zeros((max(cn, 1), 4), np.int32)
     sp = np.zeros((max(cs, 1), 4), np.int32)
-    counts2 = np.zeros(5, dtype=np.int64)
+    counts2 = np.zeros(6, dtype=np.int64)
     pos_p = None
     if positions is not None:
         pos_a = np.ascontiguousarray(positions, dtype=np.int64)
@@ -72,8 +72,9 @@ def compare(qlens, ctx, tables, num_blocks, bs, P, rows=1, tiles=False, num_toke
     np.testing.assert_array_equal(got["work"], m.work_np.reshape(-1, 4))
     np.testing.assert_array_equal(got["tiles"], m.prefill_tiles_np.reshape(-1, 4))
     np.testing.assert_array_equal(got["split"], m.split_rows_np.reshape(-1, 4))
+    superseded = sum(int(m.slot_mapping_np[r] < 0) for b, e in slices for r in range(b, e))
     assert got["counts"].tolist() == [m.num_work_items, m.num_prefill_tiles, m.num_split_rows,
-                                      m.total_partitions, m.max_parts_per_row]
+                                      m.total_partitions, m.max_parts_per_row, superseded]
     return m
 
 
@@ -165,3 +166,17 @@ def test_errors_mirror_the_reference():
     # capacities below the counts: rejected, counts still reported
     st, got = c_build([1, 1], [300, 600], [[0] * 19, [1] * 38], 8, 16, 256, caps=(1, 0, 2))
     assert st == _lib.TB_ERR_INVALID_ARG and got["counts"][0] == 5
+
+
+def test_superseded_rows_are_counted():
+    # two decode rows whose newest positions share one slot (block 3 offset 4 in both
+    # tables): the first row's slot is -1 and counts[5] reports it, the sign a fused
+    # append cannot serve the step (the reference lets the last writer win,
+    # kv_cache.py:33-38)
+    st, got = c_build([1, 1], [21, 21], [[0, 3], [1, 3]], 8, 16, 256)
+    assert st == 0
+    assert got["slot"].tolist() == [-1, 3 * 16 + 4]
+    assert int(got["counts"][5]) == 1
+    # distinct slots: nothing superseded
+    st, got = c_build([1, 1], [21, 21], [[0, 3], [1, 2]], 8, 16, 256)
+    assert st == 0 and int(got["counts"][5]) == 0

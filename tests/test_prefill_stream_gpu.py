@@ -245,3 +245,42 @@ def test_config4_split_step_appending_in_both_kernels():
     torch.cuda.synchronize()
     assert torch.equal(_bits(pool.cpu()), _bits(want_pool))
     torch.testing.assert_close(out.cpu().float(), want.float(), **TOL)
+
+
+def test_split_step_refuses_a_slot_shared_across_its_parts():
+    """A prefill row and a decode row of one split step write the same pool slot: each
+    part's own slot mapping cannot see it, so the fused append is refused on the whole
+    step's mapping (the reference's last writer wins, kv_cache.py:33-38) before any
+    launch; without k_new the step runs."""
+    g = torch.Generator().manual_seed(11)
+    Hq, Hkv, D, BS, dt = 14, 2, 64, 16, torch.bfloat16
+    n_dec, dec_ctx = 16, 2048 + 5                     # 16 x 2 units, 32 Ki positions: the decode kernel's side
+    nb_dec = (dec_ctx + BS - 1) // BS
+    NB = 2 + n_dec * nb_dec
+    pool = torch.randn(NB, 2, Hkv, BS, D, generator=g).to(dt)
+    pre_table = [0, 1]                                # 32 new rows at positions 0..31
+    tables = [pre_table] + [list(range(2 + i * nb_dec, 2 + (i + 1) * nb_dec)) for i in range(n_dec)]
+    tables[1][-1] = 1                                 # decode row 0's newest slot: block 1, offset 4 = position 20
+    slices, pos, ctx = [(0, 32)], list(range(32)), [32]
+    for i in range(n_dec):
+        slices.append((32 + i, 33 + i))
+        pos.append(dec_ctx - 1)
+        ctx.append(dec_ctx)
+    T = 32 + n_dec
+    meta = build_step_metadata(pos, slices, tables, ctx, block_size=BS, num_blocks=NB,
+                               partition_tokens=ops.partition_tokens(dt, D),
+                               rows_per_item=ops.rows_per_item(dt, Hq, Hkv), tile_prefill=True)
+    assert meta.slot_mapping_np[20] == -1             # the prefill row is superseded by the decode row
+    assert ops.attach_split_parts(meta, pos, slices, tables, ctx, num_heads=Hq, num_kv_heads=Hkv, head_dim=D,
+                                  dtype=dt, device=DEV)
+    for _, _, m in meta.parts:                        # neither part's own mapping sees the shared slot
+        assert not ((m.slot_mapping_np < 0) & (m.row_ctx_np > 0)).any()
+    meta.to(DEV)
+    q = torch.randn(T, Hq, D, generator=g).to(dt).to(DEV)
+    k = torch.randn(T, Hkv, D, generator=g).to(dt).to(DEV)
+    dpool = pool.to(DEV)
+    before = dpool.clone()
+    with pytest.raises(ValueError, match="write one pool slot"):
+        ops.paged_attention(q, dpool, meta, num_heads=Hq, k_new=k, v_new=k)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(dpool), _bits(before))   # nothing launched

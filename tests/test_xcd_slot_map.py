@@ -65,3 +65,19 @@ def test_items_out_of_row_order_and_empty():
     w = np.array([[5, 0, 1, 9], [2, 0, 0, 9], [5, 0, 0, 9], [2, 0, 1, 9]], dtype=np.int32)
     check(w, 4, 2, 8)
     assert build_xcd_slot_map(np.zeros((0, 4), np.int32), 0, 2, 8).size == 0
+
+
+def test_attach_refuses_rows_of_more_than_255_partitions():
+    """The merged launch counts a row's partitions in 8-bit per-XCD fields: a step with a
+    row of 256 or more partitions gets no slot map (its split rows go to the combine
+    kernel), one of 255 does."""
+    import torch
+
+    from tinybatch_amd.metadata import attach_xcd_slot_map
+
+    for ctx, want in ((256 * 255, True), (256 * 255 + 1, False), (256 * 400, False)):
+        blocks = (ctx + 15) // 16
+        meta = build_step_metadata([ctx - 1, 9], [(0, 1), (1, 2)], [list(range(blocks)), [0]], [ctx, 10],
+                                   block_size=16, num_blocks=blocks, partition_tokens=256)
+        assert meta.max_parts_per_row == (ctx + 255) // 256
+        assert attach_xcd_slot_map(meta, num_heads=14, num_kv_heads=2, dtype=torch.float16, num_xcds=8) is want

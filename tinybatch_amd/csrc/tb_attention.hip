@@ -1284,6 +1284,8 @@ static int32_t paged_attention_impl(const void* q, int64_t q_row_stride, void* p
   const bool merged = slot_map != nullptr;
   if (merged) {   // split rows merged inside the launch of the 16-bit work-item kernel
     if (eb != 2 || num_prefill_tiles > 0 || group != rep || device_counts) return TB_ERR_UNSUPPORTED;
+    // a row's partitions are counted in 8-bit per-XCD fields of its arrival word
+    if (max_parts_per_row > TB_MERGED_MAX_PARTS) return TB_ERR_UNSUPPORTED;
     TB_CHECK_ARG(slot_count >= num_work_items * num_kv_heads && arrivals && violations);
     TB_CHECK_ARG(((uintptr_t)arrivals & 127u) == 0 && (int64_t)arrival_units >= (int64_t)num_rows * num_kv_heads);
     TB_CHECK_ARG(max_parts_per_row <= 1 ||

@@ -161,6 +161,7 @@ extern "C" int32_t tb_build_step_metadata(const int32_t* query_start_loc, int32_
   counts[2] = c.split;
   counts[3] = c.parts;
   counts[4] = c.max_parts;
+  counts[5] = 0;
   if (c.work > work_capacity || c.tiles > tile_capacity || c.split > split_capacity) return TB_ERR_INVALID_ARG;
   if ((c.work && !work_items) || (c.tiles && !prefill_tiles) || (c.split && !split_rows)) return TB_ERR_INVALID_ARG;
   if (c.work >= INDEX_LIMIT || c.parts >= INDEX_LIMIT || max_blocks_per_seq >= INDEX_LIMIT) return TB_ERR_INVALID_ARG;
@@ -211,6 +212,11 @@ extern "C" int32_t tb_build_step_metadata(const int32_t* query_start_loc, int32_
       }
     }
   }
+  // superseded rows: inside a sequence, slot -1 (a fused append cannot serve the step)
+  int64_t superseded = 0;
+  for (int b = 0; b < num_seqs; ++b)
+    for (int i = 0; i < s.q(b); ++i) superseded += slot_mapping[s.qsl[b] + i] < 0;
+  counts[5] = superseded;
 
   // partition offsets per row, split-row records
   for (int r = 0; r <= num_tokens; ++r) row_part_offsets[r] = 0;
@@ -295,6 +301,7 @@ int32_t xcd_slot_lists(const int32_t* work_items, int32_t num_work_items, int32_
   for (int i = 0; i < num_work_items;) {
     int j = i;
     while (j < num_work_items && by_row[j].first == by_row[i].first) ++j;
+    if (j - i > TB_MERGED_MAX_PARTS) return TB_ERR_UNSUPPORTED;   // 8-bit arrival fields
     groups.push_back({i, j - i});
     i = j;
   }

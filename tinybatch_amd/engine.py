@@ -243,8 +243,9 @@ class LLMEngine:
         tok = torch.tensor(token_ids, dtype=torch.int64).pin_memory().to(self.device, non_blocking=True)
         pos = torch.tensor(positions, dtype=torch.int64).pin_memory().to(self.device, non_blocking=True)
         # the step's metadata, built from the host lists (no device round trip) and shared by every layer
-        self.kv_cache.step_metadata(pos, seq_slices, block_tables, context_lens,
-                                    self.kv_cache.rows_per_item(self.model.cfg.n_heads), host_positions=positions)
+        hq = self.model.cfg.n_heads
+        self.kv_cache.step_metadata(pos, seq_slices, block_tables, context_lens, self.kv_cache.rows_per_item(hq),
+                                    host_positions=positions, num_heads=hq)
         logits = self.model.forward(tok, pos, seq_slices, block_tables, context_lens, self.kv_cache)
         return self._sample(logits, ordered)
 

@@ -74,9 +74,12 @@ class PagedKVCache:
         """
         pos_key = (positions, positions._version) if isinstance(positions, torch.Tensor) else list(positions)
         for e in self._meta_cache:
+            # write() (no context lengths) takes any entry of the step; attention() only one
+            # built for its row grouping and query heads (the heads decide the kernel routing)
             if (_same_positions(e["pos"], pos_key) and e["slices"] == [tuple(x) for x in seq_slices]
                     and e["tables"] == block_tables
-                    and (context_lens is None or (e["ctx"] == context_lens and e["rows"] == rows_per_item))):
+                    and (context_lens is None or (e["ctx"] == context_lens and e["rows"] == rows_per_item
+                                                  and e["heads"] == num_heads))):
                 return e["meta"]
         # 16-bit pools serve long runs of new rows (prefills) with the tile kernel; a
         # step of prefills only (every sequence >= 16 new rows, its context within
@@ -112,7 +115,7 @@ class PagedKVCache:
         entry = {"pos": pos_key, "slices": [tuple(x) for x in seq_slices],
                  "tables": [list(t) for t in block_tables],
                  "ctx": None if context_lens is None else list(context_lens), "rows": rows_per_item,
-                 "meta": meta}
+                 "heads": num_heads, "meta": meta}
         self._meta_cache = [entry] + self._meta_cache[:1]
         return meta
 

@@ -184,6 +184,9 @@ def split_step_parts(positions, seq_slices, block_tables, context_lens, *, block
 # in include/tinybatch_amd.h): query rows per tile, positions per tile partition.
 TILE_ROWS = 64
 TILE_PARTITION = 1024
+# partitions of one row the merged launch counts (8-bit per-XCD arrival fields,
+# TB_MERGED_MAX_PARTS)
+MERGED_MAX_PARTS = 255
 
 
 class PrefillRoute(NamedTuple):
@@ -637,6 +640,10 @@ def attach_xcd_slot_map(meta: StepMetadata, *, num_heads: int, num_kv_heads: int
     16 query heads per kv head and no capacity counts; returns whether it does."""
     if (dtype not in (torch.float16, torch.bfloat16) or meta.num_prefill_tiles > 0 or meta.num_split_rows == 0
             or num_heads // num_kv_heads > 16 or meta.device_buffer is not None or meta.num_work_items == 0):
+        return False
+    if meta.max_parts_per_row > MERGED_MAX_PARTS:
+        # the merged launch counts a row's partitions in 8-bit fields; the combine
+        # kernel serves such steps
         return False
     meta.slot_map_np = build_xcd_slot_map(meta.work_np, meta.num_work_items, num_kv_heads, num_xcds)
     return meta.slot_map_np.size > 0

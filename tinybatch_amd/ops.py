@@ -463,6 +463,13 @@ def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, 
         fused = k_new is not None or v_new is not None
         if fused and (k_new is None or v_new is None or k_new.shape[0] != q.shape[0] or v_new.shape[0] != q.shape[0]):
             raise ValueError("k_new and v_new go together, one row per row of q")
+        if fused:
+            # a slot written by rows of both parts: each part's own slot mapping cannot
+            # see it, the whole step's can (the superseded writer holds -1)
+            sm = meta.slot_mapping_np
+            if sm.size and np.any((sm < 0) & (meta.row_ctx_np > 0)):
+                raise ValueError("two rows of the step write one pool slot; the fused append cannot serve "
+                                 "the step: append with kv_append, then call paged_attention without k_new")
         for _, _, m in meta.parts if fused else ():   # refused before any part launches
             if m.num_prefill_work and np.any(m.prefill_work_np.reshape(-1, 4)[:m.num_prefill_work, 2] % 16):
                 raise ValueError("the prefill kernel's fused append needs each sequence's new rows to start "
