@@ -385,8 +385,9 @@ int32_t tb_build_xcd_slot_map(const int32_t* work_items, int32_t num_work_items,
  * The work is a plan (tb_build_decode_plan) for plan_workgroups workgroups of
  * plan_waves waves, one workgroup per CU: every wave streams its own share of
  * the step's 16-position tiles (sequence, kv head, 16 positions) through a ring
- * in LDS; a (sequence, kv head) unit cut over several waves is merged by the
- * workgroup whose partial arrives last.
+ * in LDS; a (sequence, kv head) unit cut over several waves is merged first per
+ * workgroup, by the wave whose piece arrives last there, then by the workgroup
+ * whose partial completes the unit.
  *   workspace: >= tb_paged_decode_workspace_bytes(max_pieces, ...) bytes of
  *     device memory, 128-byte aligned, for the partials (max_pieces >= the
  *     plan's pieces).
@@ -395,13 +396,24 @@ int32_t tb_build_xcd_slot_map(const int32_t* work_items, int32_t num_work_items,
  *     (allocate it zeroed) and left zero by every call, so one buffer serves
  *     every later call. The partials of a unit are written and merged inside one
  *     XCD: the plan assumes that workgroup g runs on XCD g % num_xcds (verify
- *     with tb_decode_xcc_probe); `violations` (device uint32) is incremented
- *     for every unit whose partials ran on more than one XCD (its output may
- *     then be wrong). Calls that may overlap in time need their own workspace
- *     and arrival counters.
- * RoPE (rope_cos != NULL) and the fused append: as tb_paged_attention. The
- * newest positions of the rows must map to distinct pool slots.
+ *     with tb_decode_xcc_probe). Calls that may overlap in time need their own
+ *     workspace and arrival counters.
+ *   violations (device uint32): the call's error count, incremented for every
+ *     unit whose partials ran on more than one XCD (its output may then be
+ *     wrong), for every worker whose plan count is malformed (its tiles are
+ *     not streamed), and once when k_new is given with a plan marked
+ *     TB_DECODE_SHARED_NEWEST (then nothing is appended or written). Zero
+ *     before a call and still zero after it means every output row is right;
+ *     after a nonzero count the outputs are unusable and the arrival counters
+ *     must be zeroed again.
+ * RoPE (rope_cos != NULL) and the fused append: as tb_paged_attention. With
+ * k_new the newest positions of the rows must map to distinct pool slots
+ * (the reference's sequential write lets the last writer win a shared slot,
+ * kv_cache.py:33-38): tb_build_decode_plan marks a plan where they do not,
+ * and such a fused call is refused as above; append with tb_kv_append and
+ * call without k_new instead.
  */
+#define TB_DECODE_SHARED_NEWEST (1 << 30)
 int32_t tb_paged_decode(const void* q, int64_t q_row_stride, void* pool, int64_t num_blocks,
                         void* out, int64_t out_row_stride, int32_t num_seqs,
                         const int32_t* plan, int32_t plan_workgroups, int32_t plan_waves, int32_t plan_stride,
@@ -434,6 +446,9 @@ int32_t tb_decode_variant_supported(int32_t head_dim, int32_t waves);
  *    context_lens[b] | piece index << 24,
  *    -1 for a unit one worker holds whole, else first partial slot |
  *      (pieces - 1) << 20 | (wave of piece 0) << 28).
+ * Each count word is the worker's entry count, with TB_DECODE_SHARED_NEWEST
+ * set in every word when two sequences' newest positions (context_lens[b] - 1)
+ * map to one pool slot (a plan tb_paged_decode serves only without k_new).
  * tb_decode_plan_shape gives the entries of the busiest worker (stride must be
  * at least that, and even) and the partial slots (max_pieces); both return
  * TB_ERR_UNSUPPORTED when a unit would be cut over more than 255 workers (use

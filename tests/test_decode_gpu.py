@@ -194,7 +194,7 @@ def test_drop_in_cache_runs_the_decode_kernel_on_large_steps():
         else:
             cache.write(0, k, v, pos, slices, c["tables"])
             out = cache.attention(0, q, pos, slices, c["tables"], c["ctx"])
-            meta = cache.step_metadata(pos, slices, c["tables"], c["ctx"], cache.rows_per_item(14))
+            meta = cache.step_metadata(pos, slices, c["tables"], c["ctx"], cache.rows_per_item(14), num_heads=14)
         torch.cuda.synchronize()
         assert meta.decode_plan is not None, f"fused={fused}: the step did not take the decode kernel"
         assert torch.equal(_bits(cache.pools[0].cpu()), _bits(want_pool)), f"fused={fused}"
@@ -228,3 +228,75 @@ def test_shared_slot_refused_by_the_fused_append():
     with pytest.raises(ValueError, match="one pool slot"):
         ops.paged_attention(c["q"].to(DEV), c["pool"].to(DEV), meta, num_heads=14, k_new=c["k"].to(DEV),
                             v_new=c["v"].to(DEV))
+
+
+def _c_decode(c, meta, q, pool, out, k, v, bufs, violations, plan=None):
+    """tb_paged_decode through the C ABI with a private error counter and buffers."""
+    from tinybatch_amd import _lib
+
+    plan = meta.decode_plan if plan is None else plan
+    D, Hq, Hkv = c["D"], c["Hq"], c["Hkv"]
+    return _lib.lib().tb_paged_decode(
+        q.data_ptr(), Hq * D, pool.data_ptr(), pool.shape[0], out.data_ptr(), Hq * D, len(c["ctx"]),
+        plan.data_ptr(), meta.decode_workgroups, meta.decode_waves, meta.decode_stride, Hq, Hkv, D, c["BS"],
+        float(D ** -0.5), _lib.DTYPE_CODE[c["dtype"]], None if k is None else k.data_ptr(), Hkv * D,
+        None if v is None else v.data_ptr(), Hkv * D, bufs.pieces.data_ptr(), bufs.pieces.numel(),
+        meta.decode_pieces, bufs.arrivals.data_ptr(), bufs.units, violations.data_ptr(), None, None, 0,
+        _lib.stream_handle(DEV))
+
+
+def test_c_abi_refuses_a_fused_call_on_a_plan_with_a_shared_newest_slot():
+    """Two rows whose newest positions share a pool slot: the plan builder marks every
+    count word, and a fused tb_paged_decode on it counts one error and writes nothing
+    (the reference's last writer wins, kv_cache.py:33-38); the same plan without k_new,
+    after the slot-mapped append, serves the step."""
+    c = case(21, 40, 14, 2, 64, 16, torch.float16, ctx=[900 + 37 * i for i in range(40)], nan_stale=False)
+    c["tables"][5][-1] = c["tables"][2][-1]
+    c["ctx"][5] = (len(c["tables"][5]) - 1) * 16 + (c["ctx"][2] - 1) % 16 + 1   # row 5's newest slot = row 2's
+    meta = decode_meta(c["ctx"], c["tables"], c["NB"], 16, 14, 2, 64, torch.float16)
+    workers = meta.decode_workgroups * meta.decode_waves
+    assert np.all(meta.decode_plan_np[:workers] & (1 << 30))   # TB_DECODE_SHARED_NEWEST
+    q, k, v = c["q"].to(DEV), c["k"].to(DEV), c["v"].to(DEV)
+    pool = c["pool"].to(DEV)
+    out = torch.full((40, 14 * 64), 7.0, dtype=torch.float16, device=DEV)
+    bufs = ops.DecodeBuffers(DEV, ops.decode_workspace_bytes(meta, 14, 2, 64), meta.decode_units)
+    viol = torch.zeros(1, dtype=torch.int32, device=DEV)
+    assert _c_decode(c, meta, q, pool, out, k, v, bufs, viol) == 0
+    torch.cuda.synchronize()
+    assert int(viol.item()) == 1
+    assert torch.equal(_bits(pool.cpu()), _bits(c["pool"])) and bool((out == 7.0).all())
+    # unfused: the append (last writer wins) and then attention from the pool
+    want, want_pool = oracle(c)
+    ops.kv_append(pool, k, v, meta.slot_mapping)
+    assert _c_decode(c, meta, q, pool, out, None, None, bufs, viol) == 0
+    torch.cuda.synchronize()
+    assert int(viol.item()) == 1
+    assert torch.equal(_bits(pool.cpu()), _bits(want_pool))
+    torch.testing.assert_close(out.cpu().float(), want.float(), **TOL)
+
+
+def test_malformed_plan_count_is_counted():
+    """A worker count the plan builder never writes (odd, or past the stride): that
+    worker streams nothing and the call's error count says so, instead of rows left
+    silently unwritten."""
+    c = case(22, 64, 14, 2, 64, 16, torch.float16, nan_stale=False)
+    meta = decode_meta(c["ctx"], c["tables"], c["NB"], 16, 14, 2, 64, torch.float16)
+    q = c["q"].to(DEV)
+    pool = c["pool"].to(DEV)
+    out = torch.empty(64, 14 * 64, dtype=torch.float16, device=DEV)
+    workers = meta.decode_workgroups * meta.decode_waves
+    for bad in (int(meta.decode_plan_np[0]) + 1, meta.decode_stride + 2):
+        host = meta.decode_plan_np.copy()
+        host[0] = bad
+        plan = torch.from_numpy(host).to(DEV)
+        bufs = ops.DecodeBuffers(DEV, ops.decode_workspace_bytes(meta, 14, 2, 64), meta.decode_units)
+        viol = torch.zeros(1, dtype=torch.int32, device=DEV)
+        assert _c_decode(c, meta, q, pool, out, None, None, bufs, viol, plan=plan) == 0
+        torch.cuda.synchronize()
+        assert int(viol.item()) == 1, bad
+    # the valid plan, fresh counters: no error
+    bufs = ops.DecodeBuffers(DEV, ops.decode_workspace_bytes(meta, 14, 2, 64), meta.decode_units)
+    viol = torch.zeros(1, dtype=torch.int32, device=DEV)
+    assert _c_decode(c, meta, q, pool, out, None, None, bufs, viol) == 0
+    torch.cuda.synchronize()
+    assert int(viol.item()) == 0 and workers > 0

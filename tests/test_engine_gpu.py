@@ -284,3 +284,53 @@ def test_decode_graphs_refuse_a_step_with_a_shared_slot():
     assert graphs.run([1, 2], [19, 35], [[3, 6], [0, 5, 6]], ctx) is None
     ids = graphs.run([1, 2], [19, 35], [[3, 6], [0, 5, 7]], ctx)
     assert len(ids) == 2 and all(0 <= t < mc.vocab_size for t in ids)
+
+
+def test_merge_error_recomputes_the_step_without_in_launch_merges():
+    """A nonzero in-launch merge error count (as a unit merged across two XCDs would
+    leave) seen at an eager step's token copy: the engine switches merges off for the
+    device and recomputes the step through the work items, so the tokens equal a clean
+    run's; PagedKVCache.check raises on the same count."""
+    from tinybatch_amd import ops
+
+    mc = small_cfg(layers=2, heads=4, kv_heads=2)
+    ecfg = EngineConfig(dtype="float32", num_blocks=96, block_size=16, max_batch_tokens=160, max_running=5,
+                        decode_graphs=False)
+    model = Qwen2Paged(mc, DEV, torch.float32, seed=3)
+    g = torch.Generator().manual_seed(9)
+    prompts = [torch.randint(0, mc.vocab_size, (n,), generator=g).tolist() for n in (20, 33, 7)]
+    clean = LLMEngine(ecfg, model=model).generate(prompts, max_new_tokens=5)
+    dd = ops.decode_device(DEV)
+    assert dd.merge_in_kernel
+    try:
+        cache = PagedKVCache(1, 8, 16, 2, 64, DEV, torch.float16)
+        dd.violations.fill_(1)
+        with pytest.raises(RuntimeError, match="merge errors"):
+            cache.check()
+        eng = LLMEngine(ecfg, model=model)
+        got = eng.generate(prompts, max_new_tokens=5)          # the first step sees the count
+        assert eng.merge_failures == 1 and not dd.merge_in_kernel
+        assert dd.errors() == 0
+        assert got == clean
+        cache.check()                                           # nothing left to report
+    finally:
+        dd.merge_in_kernel = True                               # later tests keep the decode kernel
+        dd.violations.zero_()
+
+
+def test_engine_prefill_steps_take_the_whole_sequence_prefill_kernel():
+    """The engine's metadata is built with its query heads, so a prefill-only bf16 step
+    routes its whole sequences to tb_paged_prefill (work list, no tiles or items)."""
+    mc = small_cfg(layers=2, heads=4, kv_heads=2)
+    ecfg = EngineConfig(dtype="bfloat16", num_blocks=96, block_size=16, max_batch_tokens=512, max_running=4,
+                        decode_graphs=False)
+    eng = LLMEngine(ecfg, model=Qwen2Paged(mc, DEV, torch.bfloat16, seed=3))
+    g = torch.Generator().manual_seed(10)
+    for n in (40, 64, 100):
+        eng.add_request(torch.randint(0, mc.vocab_size, (n,), generator=g).tolist(), max_new_tokens=2)
+    eng.step()                                                  # the three prefills
+    assert eng.last_step_prefills == 3
+    meta = eng.kv_cache._meta_cache[0]["meta"]
+    assert meta.num_prefill_work > 0 and meta.num_work_items == 0 and meta.num_prefill_tiles == 0
+    while eng.has_work():
+        eng.step()

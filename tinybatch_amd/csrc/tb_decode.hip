@@ -214,7 +214,18 @@ __global__ __launch_bounds__(64 * W) void paged_stream_kernel(const stream_args 
   s_dma16(ent_g + lane, ents);                   // the entry array is padded by 64 entries
   int n = k < a.workers ? __builtin_amdgcn_readfirstlane(a.counts[k]) : 0;
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  if (n < 0 || n > a.stride || (n & 1)) n = 0;   // the plan builder never makes one
+  {
+    // count word: tiles | newest slots shared by two sequences << 30. A malformed count
+    // (the plan builder never makes one) and a fused append the plan cannot serve are
+    // refused: nothing is streamed or written, and the call's error count says so
+    const bool shared_newest = (n >> 30) & 1;
+    const int cnt = n & 0x3FFFFFFF;
+    const bool bad = n < 0 || cnt > a.stride || (cnt & 1);
+    const bool refused = shared_newest && a.k_new != nullptr;
+    if ((bad || (refused && k == 0)) && lane == 0)
+      __hip_atomic_fetch_add(a.violations, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    n = (bad || refused) ? 0 : cnt;
+  }
   int4 ev = *reinterpret_cast<const int4*>(ents + 16 * lane);   // the issuing cursor's entries, lane = tile
 
   const bool fused = a.k_new != nullptr;
@@ -889,8 +900,23 @@ extern "C" int32_t tb_build_decode_plan(const int32_t* context_lens, int32_t num
   int32_t* const counts = plan;
   int32_t* const entries = plan + (size_t)(workers + 3) / 4 * 4;
   stream_layout lay;
-  return stream_assign(context_lens, num_seqs, num_kv_heads, head_dim, block_tables, max_blocks_per_seq, block_size,
-                       num_blocks, workgroups, waves, num_xcds, unit_cost, stride, counts, entries, lay);
+  const int32_t rc = stream_assign(context_lens, num_seqs, num_kv_heads, head_dim, block_tables, max_blocks_per_seq,
+                                   block_size, num_blocks, workgroups, waves, num_xcds, unit_cost, stride, counts,
+                                   entries, lay);
+  if (rc != TB_OK) return rc;
+  // Two sequences whose newest positions share a pool slot: the fused append would
+  // let each attend to its own new K/V, where the reference's sequential write lets
+  // the last one win (kv_cache.py:33-38). Every count word carries the mark (bit
+  // 30); the kernel refuses a fused call on such a plan.
+  std::vector<int64_t> newest(num_seqs);
+  for (int b = 0; b < num_seqs; ++b) {
+    const int p = context_lens[b] - 1;
+    newest[b] = (int64_t)block_tables[(int64_t)b * max_blocks_per_seq + p / block_size] * block_size + p % block_size;
+  }
+  std::sort(newest.begin(), newest.end());
+  if (std::adjacent_find(newest.begin(), newest.end()) != newest.end())
+    for (int k = 0; k < workers; ++k) counts[k] |= TB_DECODE_SHARED_NEWEST;
+  return TB_OK;
 }
 
 extern "C" size_t tb_paged_decode_piece_bytes(int32_t num_heads, int32_t num_kv_heads, int32_t head_dim) {

@@ -36,6 +36,7 @@ from dataclasses import dataclass, field
 
 import torch
 
+from . import ops
 from .block_manager import BlockManager
 from .config import EngineConfig
 from .decode_graphs import DecodeGraphs
@@ -72,6 +73,7 @@ class LLMEngine:
         self.last_step_prefills = 0
         self.graph_steps = 0
         self.pipelined_steps = 0
+        self.merge_failures = 0         # eager steps recomputed after an in-launch merge error
         self.graphs = (DecodeGraphs(self.model, self.kv_cache, self.cfg.max_running, self.cfg.max_model_len)
                        if self.cfg.decode_graphs else None)
         self.swap_outs = 0
@@ -239,15 +241,33 @@ class LLMEngine:
 
     def _forward_eager(self, ordered, token_ids, positions, seq_slices, block_tables, context_lens) -> list[int]:
         """Launch by launch: per layer the separate append (its last writer wins on
-        a shared slot) then attention, as the reference's forward orders them."""
+        a shared slot) then attention, as the reference's forward orders them.
+
+        The step's attention may merge split rows inside its launches (the decode
+        kernel, the merged launch), which assume a workgroup placement on the XCDs. The
+        device's error count rides on the step's one synchronising copy (the sampled
+        ids); if a merge reported an error the step's outputs are unusable, so merges
+        are switched off for the rest of the process and the step runs again through
+        the work items (re-appending the same rows to the same slots)."""
         tok = torch.tensor(token_ids, dtype=torch.int64).pin_memory().to(self.device, non_blocking=True)
         pos = torch.tensor(positions, dtype=torch.int64).pin_memory().to(self.device, non_blocking=True)
-        # the step's metadata, built from the host lists (no device round trip) and shared by every layer
         hq = self.model.cfg.n_heads
-        self.kv_cache.step_metadata(pos, seq_slices, block_tables, context_lens, self.kv_cache.rows_per_item(hq),
-                                    host_positions=positions, num_heads=hq)
-        logits = self.model.forward(tok, pos, seq_slices, block_tables, context_lens, self.kv_cache)
-        return self._sample(logits, ordered)
+        guard = ops.decode_device(self.device) if self.device.type == "cuda" else None
+        for attempt in range(2):
+            # the step's metadata, built from the host lists (no device round trip) and shared by every layer
+            self.kv_cache.step_metadata(pos, seq_slices, block_tables, context_lens,
+                                        self.kv_cache.rows_per_item(hq), host_positions=positions, num_heads=hq)
+            logits = self.model.forward(tok, pos, seq_slices, block_tables, context_lens, self.kv_cache)
+            errs = guard.errors_async() if guard is not None else None
+            ids = self._sample(logits, ordered)          # synchronises: errs holds the count
+            if errs is None or int(errs[0]) == 0:
+                return ids
+            if attempt == 1:
+                break
+            self.merge_failures += 1
+            guard.disable_merges()
+            self.kv_cache.clear_metadata()
+        raise RuntimeError("attention kept reporting merge errors with in-launch merges switched off")
 
     def _finish_step(self, ordered: list[Request], next_ids: list[int]) -> list[StepOutput]:
         now = time.perf_counter()

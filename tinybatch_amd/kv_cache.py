@@ -119,6 +119,24 @@ class PagedKVCache:
         self._meta_cache = [entry] + self._meta_cache[:1]
         return meta
 
+    def check(self) -> None:
+        """Raise RuntimeError when an in-launch merge of this device reported an error
+        since the last check (a unit's partials on two XCDs: the placement the decode
+        kernel and the merged launch assume did not hold), so attention outputs since
+        then cannot be trusted. Synchronises the device; a caller checks at a point it
+        synchronises anyway (the engine does it with each eager step's token copy and
+        recomputes the step, ops.DecodeDevice.disable_merges)."""
+        if self.device.type != "cuda":
+            return
+        n = ops.decode_device(self.device).errors()
+        if n:
+            raise RuntimeError(f"{n} in-launch merge errors on {self.device}: attention outputs since the last "
+                               "check are unusable (ops.DecodeDevice.disable_merges, then recompute)")
+
+    def clear_metadata(self) -> None:
+        """Forget the cached step metadata (its kernel routing), e.g. after disable_merges."""
+        self._meta_cache = []
+
     # ---- reference API -----------------------------------------------------
     def write(self, layer: int, k: torch.Tensor, v: torch.Tensor, positions: torch.Tensor,
               seq_slices: list[tuple[int, int]], block_tables: list[list[int]],

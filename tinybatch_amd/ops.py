@@ -174,7 +174,31 @@ class DecodeDevice:
         self.workgroups = cus
         nx = cus // 32 if cus % 32 == 0 and cus >= 32 else 1
         self.num_xcds, self.merge_in_kernel = self._verify(device, cus, nx)
+        # the error count of the in-launch merges (tb_paged_decode, tb_paged_attention_merged):
+        # nonzero after a call whose outputs cannot be trusted (a unit's partials on two
+        # XCDs, a malformed plan, a refused fused append)
         self.violations = torch.zeros(1, dtype=torch.int32, device=device)
+        self._host_errors = torch.zeros(1, dtype=torch.int32).pin_memory()
+
+    def errors_async(self) -> torch.Tensor:
+        """Queue a copy of the error count on the current stream into pinned host memory;
+        the returned tensor holds it once the stream passes that point (read it after the
+        next synchronisation, e.g. the step's token copy)."""
+        self._host_errors.copy_(self.violations, non_blocking=True)
+        return self._host_errors
+
+    def errors(self) -> int:
+        """The error count now (synchronises the device)."""
+        return int(self.violations.item())
+
+    def disable_merges(self) -> None:
+        """After a nonzero error count: no more in-launch merges on this device (every
+        later step goes to the work-item kernel, whose split rows a separate kernel
+        merges), and the count back to zero."""
+        self.merge_in_kernel = False
+        self.violations.zero_()
+        for key in [k for k in _DECODE_WORKSPACES if k[0] == self.device.index]:
+            del _DECODE_WORKSPACES[key]      # arrival counters a failed call may have left nonzero
 
     @staticmethod
     def _verify(device, cus: int, nx: int) -> tuple[int, bool]:
@@ -256,20 +280,13 @@ def decode_kernel_preferred(meta: StepMetadata, *, num_kv_heads: int, head_dim: 
     return kv_bytes >= min_bytes
 
 
-# Head dim 64: four waves with two tile pairs in flight each for steps below this
-# many K/V bytes, eight waves with one pair from it on. Same-box runs (Qwen layer,
-# fp16, 24 pools, us per call four / eight waves): 24 sequences (30 MB) 11.4 / 12.0,
-# 32 (40 MB) 12.1 / 12.9, 64 (72 MB) 17.9 / 18.0 on one box and 18.2 / 18.1 on another.
-DECODE_EIGHT_WAVES_MIN_BYTES = 56 << 20
-
-
 def decode_waves_for(meta: StepMetadata, *, num_kv_heads: int, head_dim: int) -> int | None:
-    """The decode kernel variant (waves per workgroup) for a decode-only step, or None
-    for the library's default (head dims other than 64)."""
-    if head_dim != 64:
-        return None
-    kv_bytes = int(meta.row_ctx_np[:meta.num_seqs].astype(np.int64).sum()) * num_kv_heads * head_dim * 2 * 2
-    return 8 if kv_bytes >= DECODE_EIGHT_WAVES_MIN_BYTES else 4
+    """The decode kernel variant (waves per workgroup) for a decode-only step: None, the
+    library's default for the head dim (tb_decode_defaults). At head dim 64 that is four
+    waves with two tile pairs in flight each; same-box graph runs on the Qwen layer
+    (fp16, 64 sequences, 24 pools, us per call four / six / eight waves): 17.94 / 18.23 /
+    18.10 on one box, 17.59 / - / 18.05 on another (bench.py --decode-waves picks another)."""
+    return None
 
 
 def attach_decode_plan(meta: StepMetadata, *, num_heads: int, num_kv_heads: int, head_dim: int,
@@ -277,8 +294,8 @@ def attach_decode_plan(meta: StepMetadata, *, num_heads: int, num_kv_heads: int,
                        unit_cost: int | None = None) -> bool:
     """metadata.attach_decode_plan with this device's workgroups and XCDs; False (the
     step stays with the work-item kernel) when the device's workgroup placement is not
-    the one the kernel's in-XCD merges assume. ``waves`` None: at head dim 64, the
-    variant for the step's size (decode_waves_for)."""
+    the one the kernel's in-XCD merges assume. ``waves`` None: the library's default
+    variant (decode_waves_for)."""
     from .metadata import attach_decode_plan as attach
 
     d = decode_device(device)
