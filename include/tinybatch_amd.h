@@ -465,6 +465,37 @@ int32_t tb_build_decode_plan(const int32_t* context_lens, int32_t num_seqs, int3
                              int32_t num_xcds, int32_t unit_cost, int32_t stride, int32_t* plan,
                              size_t plan_words);
 
+/* The same plan built on the device (replaces tb_build_decode_plan's per-tile
+ * host work and the upload of its entries; the reference builds its step
+ * metadata as host lists, src/tinybatch/engine.py:99-126). Host part,
+ * tb_build_decode_segments (nothing allocated, no device call): the assignment
+ * of tb_build_decode_plan, written as the count words (counts [workers],
+ * TB_DECODE_SHARED_NEWEST included when block_tables is given; may be NULL to
+ * skip that mark) and one descriptor per (worker, unit) segment, int32 x 8 =
+ *   (worker, first entry in the worker's list, b | h << 20, first tile of the
+ *    unit, tiles | unit's last tile << 30, context_lens[b], piece index,
+ *    the entries' fourth word),
+ * at most num_seqs * num_kv_heads + workgroups * waves of them
+ * (segment_capacity); *max_entries and *pieces as tb_decode_plan_shape.
+ * Device part, tb_expand_decode_plan: writes every tile entry of the plan at
+ * `plan` (device memory of tb_decode_plan_words(workers, stride) int32, the
+ * count words copied to its start by the caller) from the descriptors and the
+ * step's device block tables (int32 [num_seqs][max_blocks_per_seq]), one
+ * workgroup per descriptor, on `stream`; the entries equal tb_build_decode_plan's.
+ * A block id outside [0, num_blocks) or past its table is counted in `errors`
+ * (device uint32) and replaced by block 0 (validate the tables on the host, as
+ * tb_build_step_metadata does, to raise instead). */
+int32_t tb_build_decode_segments(const int32_t* context_lens, int32_t num_seqs, int32_t num_kv_heads,
+                                 int32_t head_dim, const int32_t* block_tables, int32_t max_blocks_per_seq,
+                                 int32_t block_size, int32_t workgroups, int32_t waves, int32_t num_xcds,
+                                 int32_t unit_cost, int32_t* counts, int32_t* segments,
+                                 int32_t segment_capacity, int32_t* num_segments, int32_t* max_entries,
+                                 int32_t* pieces);
+int32_t tb_expand_decode_plan(const int32_t* segments, int32_t num_segments, const int32_t* block_tables,
+                              int32_t max_blocks_per_seq, int32_t block_size, int64_t num_blocks,
+                              int32_t num_kv_heads, int32_t head_dim, int32_t workers, int32_t stride,
+                              int32_t* plan, uint32_t* errors, hipStream_t stream);
+
 /* Records, for each of `workgroups` workgroups of one launch, the XCD it ran on
  * (device int32 [workgroups]): the check behind the in-launch merges. */
 int32_t tb_decode_xcc_probe(int32_t workgroups, int32_t* out, hipStream_t stream);

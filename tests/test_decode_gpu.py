@@ -255,7 +255,7 @@ def test_c_abi_refuses_a_fused_call_on_a_plan_with_a_shared_newest_slot():
     c["ctx"][5] = (len(c["tables"][5]) - 1) * 16 + (c["ctx"][2] - 1) % 16 + 1   # row 5's newest slot = row 2's
     meta = decode_meta(c["ctx"], c["tables"], c["NB"], 16, 14, 2, 64, torch.float16)
     workers = meta.decode_workgroups * meta.decode_waves
-    assert np.all(meta.decode_plan_np[:workers] & (1 << 30))   # TB_DECODE_SHARED_NEWEST
+    assert np.all(meta.decode_plan[:workers].cpu().numpy() & (1 << 30))   # TB_DECODE_SHARED_NEWEST
     q, k, v = c["q"].to(DEV), c["k"].to(DEV), c["v"].to(DEV)
     pool = c["pool"].to(DEV)
     out = torch.full((40, 14 * 64), 7.0, dtype=torch.float16, device=DEV)
@@ -285,8 +285,9 @@ def test_malformed_plan_count_is_counted():
     pool = c["pool"].to(DEV)
     out = torch.empty(64, 14 * 64, dtype=torch.float16, device=DEV)
     workers = meta.decode_workgroups * meta.decode_waves
-    for bad in (int(meta.decode_plan_np[0]) + 1, meta.decode_stride + 2):
-        host = meta.decode_plan_np.copy()
+    plan_host = meta.decode_plan.cpu().numpy()
+    for bad in (int(plan_host[0]) + 1, meta.decode_stride + 2):
+        host = plan_host.copy()
         host[0] = bad
         plan = torch.from_numpy(host).to(DEV)
         bufs = ops.DecodeBuffers(DEV, ops.decode_workspace_bytes(meta, 14, 2, 64), meta.decode_units)
@@ -300,3 +301,67 @@ def test_malformed_plan_count_is_counted():
     assert _c_decode(c, meta, q, pool, out, None, None, bufs, viol) == 0
     torch.cuda.synchronize()
     assert int(viol.item()) == 0 and workers > 0
+
+
+@pytest.mark.parametrize("name,batch,waves", [("qwen-fp16-b64", 0, 4), ("qwen-fp16-b64", 0, 8),
+                                              ("llama-bf16-b256", 48, 4)])
+def test_device_built_plan_equals_the_host_plan(name, batch, waves):
+    """The plan the device writes from the segment descriptors (tb_expand_decode_plan)
+    is the host builder's, word for word: count words and every worker's entries."""
+    from tinybatch_amd.metadata import attach_decode_plan as attach
+
+    wl = make_decode_workload(name, **({"batch": batch} if batch else {}))
+    dd = ops.decode_device(DEV)
+    metas = []
+    for on_device in (False, True):
+        meta = build_step_metadata(wl.positions, wl.seq_slices, wl.block_tables, wl.context_lens,
+                                   block_size=16, num_blocks=wl.num_blocks,
+                                   partition_tokens=ops.partition_tokens(wl.dtype, wl.head_dim))
+        assert attach(meta, num_heads=wl.num_heads, num_kv_heads=wl.num_kv_heads, head_dim=wl.head_dim,
+                      dtype=wl.dtype, workgroups=dd.workgroups, num_xcds=dd.num_xcds, waves=waves,
+                      on_device=on_device)
+        metas.append(meta.to(DEV))
+    torch.cuda.synchronize()
+    host, dev = (m.decode_plan.cpu().numpy() for m in metas)
+    W = dd.workgroups * waves
+    stride = metas[0].decode_stride
+    assert metas[1].decode_stride == stride and metas[1].decode_pieces == metas[0].decode_pieces
+    np.testing.assert_array_equal(dev[:W], host[:W])
+    base = (W + 3) // 4 * 4
+    he = host[base:base + W * stride * 4].reshape(W, stride, 4)
+    de = dev[base:base + W * stride * 4].reshape(W, stride, 4)
+    for k in range(W):
+        n = int(host[k]) & 0x3FFFFFFF
+        np.testing.assert_array_equal(de[k, :n], he[k, :n])
+    assert dd.errors() == 0
+
+
+def test_device_built_plan_counts_bad_block_ids_instead_of_reading_outside_the_pool():
+    """A table entry outside the pool reaching tb_expand_decode_plan (the host builders
+    raise IndexError first): counted in the error word and replaced by block 0."""
+    from tinybatch_amd import _lib
+    from tinybatch_amd.metadata import build_decode_segments
+
+    ctx = [100, 70]
+    tables = np.array([[3, 4, 5, 6, 7, 8, 9], [0, 1, 2, 10, 11, 0, 0]], dtype=np.int32)
+    counts, segs, waves, stride, pieces = build_decode_segments(ctx, tables, block_size=16, num_kv_heads=2,
+                                                                 head_dim=64, workgroups=8, num_xcds=8, waves=4)
+    bad = tables.copy()
+    bad[1, 2] = 1 << 20                                     # outside a 12-block pool
+    W = 32
+    plan = torch.zeros(int(_lib.lib().tb_decode_plan_words(W, stride)), dtype=torch.int32, device=DEV)
+    segs_d = torch.from_numpy(segs).to(DEV)
+    tab_d = torch.from_numpy(bad).to(DEV)
+    errs = torch.zeros(1, dtype=torch.int32, device=DEV)
+    assert _lib.lib().tb_expand_decode_plan(segs_d.data_ptr(), segs.shape[0], tab_d.data_ptr(), 7, 16, 12, 2, 64, W,
+                                            stride, plan.data_ptr(), errs.data_ptr(), _lib.stream_handle(DEV)) == 0
+    torch.cuda.synchronize()
+    # the tile in block index 2 of both kv heads' units (and a pad that repeats it) is counted
+    assert int(errs.item()) >= 2
+    base = (W + 3) // 4 * 4
+    host = plan.cpu().numpy()
+    ents = host[base:base + W * stride * 4].reshape(W, stride, 4)
+    blk_bytes = 2 * 2 * 16 * 64 * 2
+    for k in range(W):
+        n = int(host[k]) & 0x3FFFFFFF
+        assert np.all((ents[k, :n, 0].astype(np.int64) << 8) < 12 * blk_bytes)   # inside the pool

@@ -198,3 +198,74 @@ def test_the_decode_kernel_is_chosen_for_large_decode_steps():
     meta = build_step_metadata(small.positions, small.seq_slices, small.block_tables, small.context_lens,
                                block_size=16, num_blocks=small.num_blocks, partition_tokens=256)
     assert not ops.decode_kernel_preferred(meta, num_kv_heads=2, head_dim=64, dtype=torch.float16)
+
+
+def expand_on_host(counts, segs, tables, *, bs, hkv, D, workers, stride):
+    """The descriptors of tb_build_decode_segments expanded as tb_expand_decode_plan
+    does on the device (a restatement in numpy, for the host-side check)."""
+    plan = np.zeros((workers + 3) // 4 * 4 + (workers * stride + 64) * 4, dtype=np.int32)
+    plan[:counts.size] = counts
+    ents = plan[(workers + 3) // 4 * 4:].reshape(-1, 4)
+    tb = 32 * D
+    tile_bytes = tb * (bs // 16)
+    blk_bytes = 2 * hkv * tile_bytes
+    for k, pos_first, bh, tu0, info, ctx, piece, e3 in segs.tolist():
+        n, unit_end = info & 0x3FFFFFFF, bool(info & (1 << 30))
+        b, h = bh & 0xFFFFF, bh >> 20
+        for i in range(n + (n & 1)):
+            pad = i >= n
+            tu = tu0 + (n - 1 if pad else i)
+            pos0 = 16 * tu
+            off = int(tables[b, pos0 // bs]) * blk_bytes + h * tile_bytes + ((pos0 % bs) // 16) * tb
+            rows = min(16, ctx - pos0)
+            y = b | (h << 20) | ((rows - 1) << 24) | (E_LAST if (not pad and unit_end and i == n - 1) else 0) \
+                | (E_NULL if pad else 0)
+            ents[k * stride + pos_first + i] = [np.int64(off >> 8).astype(np.int32), y, ctx | (piece << 24), e3]
+    return plan
+
+
+@pytest.mark.parametrize("ctx,hkv,D,bs,waves", [
+    ([2631, 2025, 2714, 2772, 17, 1, 16, 33] * 3, 2, 64, 16, 4),
+    ([900 + 37 * i for i in range(40)], 2, 64, 32, 8),
+    ([5000, 1200, 30000, 64, 1024], 8, 128, 16, 4),
+    ([1, 2, 3, 15, 16, 17, 31, 32, 33], 2, 64, 64, 6),
+])
+def test_segments_expand_to_the_host_plan(ctx, hkv, D, bs, waves):
+    """tb_build_decode_segments' counts and descriptors, expanded entry by entry, give
+    exactly the words of tb_build_decode_plan (the device builds the same plan)."""
+    from tinybatch_amd.metadata import build_decode_segments
+
+    rng = np.random.default_rng(3)
+    tables, nb = tables_for(ctx, bs, rng)
+    G, nx = 32, 8
+    host = build_decode_plan(ctx, tables, block_size=bs, num_blocks=nb, num_kv_heads=hkv, head_dim=D, workgroups=G,
+                             num_xcds=nx, waves=waves)
+    seg = build_decode_segments(ctx, tables, block_size=bs, num_kv_heads=hkv, head_dim=D, workgroups=G,
+                                num_xcds=nx, waves=waves)
+    plan, w, stride, pieces = host
+    counts, segs, w2, stride2, pieces2 = seg
+    assert (w, stride, pieces) == (w2, stride2, pieces2)
+    assert segs.shape[0] <= len(ctx) * hkv + G * waves
+    got = expand_on_host(counts, segs, tables, bs=bs, hkv=hkv, D=D, workers=G * waves, stride=stride)
+    W = G * waves
+    np.testing.assert_array_equal(got[:W], plan[:W])
+    cw, cs = decode(plan, W, stride)
+    gw, gs = decode(got, W, stride)
+    for k in range(W):
+        n = int(cw[k])
+        np.testing.assert_array_equal(gs[k, :n], cs[k, :n])
+
+
+def test_segments_carry_the_shared_newest_mark():
+    from tinybatch_amd.metadata import build_decode_segments
+
+    rng = np.random.default_rng(4)
+    ctx = [40, 40]
+    tables, nb = tables_for(ctx, 16, rng)
+    tables[1, 2] = tables[0, 2]                       # both newest positions (39) in one block, offset 7
+    counts = build_decode_segments(ctx, tables, block_size=16, num_kv_heads=2, head_dim=64, workgroups=8,
+                                   num_xcds=8, waves=4)[0]
+    assert np.all(counts[:32] & (1 << 30))
+    host = build_decode_plan(ctx, tables, block_size=16, num_blocks=nb, num_kv_heads=2, head_dim=64, workgroups=8,
+                             num_xcds=8, waves=4)[0]
+    np.testing.assert_array_equal(counts[:32], host[:32])

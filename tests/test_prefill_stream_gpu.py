@@ -137,7 +137,7 @@ def test_config4_split_step_against_the_oracle_and_the_one_launch():
     assert ops.attach_split_parts(meta, wl.positions, wl.seq_slices, wl.block_tables, wl.context_lens, num_heads=Hq,
                                   num_kv_heads=Hkv, head_dim=D, dtype=dt, device=DEV)
     (r0, r1, pre), (d0, d1, dec) = meta.parts
-    assert (r0, r1, d0, d1) == (0, 4096, 4096, 4152) and dec.decode_plan_np is not None and pre.num_prefill_work
+    assert (r0, r1, d0, d1) == (0, 4096, 4096, 4152) and dec.decode_segments_np is not None and pre.num_prefill_work
     meta.to(DEV)
     q, pool = wl.q.to(DEV), wl.pool.to(DEV)
     split = ops.paged_attention(q, pool, meta, num_heads=Hq)

@@ -87,6 +87,10 @@ SIGNATURES = {
     "tb_build_decode_plan": (c_i32, [c_vp, c_i32, c_i32, c_i32, c_vp, c_i32, c_i32, c_i64, c_i32, c_i32, c_i32,
                                      c_i32, c_i32, c_vp, c_sz]),
     "tb_decode_xcc_probe": (c_i32, [c_i32, c_vp, c_vp]),
+    "tb_build_decode_segments": (c_i32, [c_vp, c_i32, c_i32, c_i32, c_vp, c_i32, c_i32, c_i32, c_i32, c_i32,
+                                         c_i32, c_vp, c_vp, c_i32, c_vp, c_vp, c_vp]),
+    "tb_expand_decode_plan": (c_i32, [c_vp, c_i32, c_vp, c_i32, c_i32, c_i64, c_i32, c_i32, c_i32, c_i32, c_vp,
+                                      c_vp, c_vp]),
     "tb_paged_prefill": (c_i32, [
         c_vp, c_i64, c_vp, c_i64, c_vp, c_i64,   # q, q stride, pool, num_blocks, out, out stride
         c_vp, c_i32, c_vp, c_i32, c_i32,         # block tables, max_nb, work, num_work, max_tiles

@@ -664,6 +664,7 @@ struct stream_layout {
 };
 
 constexpr int E_LAST = 1 << 28;   // the unit's last tile
+constexpr int SEG_LAST = 1 << 30; // a segment descriptor holds its unit's last tile
 constexpr int E_NULL = 1 << 29;   // a padding tile (no positions)
 
 // The assignment of a step's tiles to workers, and (with `entries`) their entries.
@@ -673,7 +674,8 @@ constexpr int E_NULL = 1 << 29;   // a padding tile (no positions)
 int32_t stream_assign(const int32_t* context_lens, int32_t num_seqs, int32_t num_kv_heads, int32_t head_dim,
                       const int32_t* block_tables, int32_t max_blocks_per_seq, int32_t block_size,
                       int64_t num_blocks, int32_t workgroups, int32_t waves, int32_t num_xcds, int32_t unit_cost,
-                      int32_t stride, int32_t* counts, int32_t* entries, stream_layout& lay) {
+                      int32_t stride, int32_t* counts, int32_t* entries, stream_layout& lay,
+                      int32_t* segs = nullptr, int64_t seg_capacity = 0, int64_t* nsegs = nullptr) {
   if (!context_lens || num_seqs < 0 || num_kv_heads <= 0 || workgroups <= 0 || waves <= 0 || waves > 16 ||
       num_xcds <= 0 || num_xcds > 8 || workgroups < num_xcds || (head_dim != 64 && head_dim != 128) ||
       unit_cost < 0 || unit_cost > 64)
@@ -766,6 +768,22 @@ int32_t stream_assign(const int32_t* context_lens, int32_t num_seqs, int32_t num
         const int64_t s0 = std::max(t0, start(kk)), s1 = std::min(t1, end[kk]);   // the segment
         const int g = (int)(kk / waves) * num_xcds + x;            // the workgroup, and its wave
         const int k = g * waves + (int)(kk % waves);
+        if (segs) {                                                // one descriptor per segment
+          if (*nsegs >= seg_capacity) return TB_ERR_INVALID_ARG;
+          int32_t* d = segs + 8 * (*nsegs)++;
+          d[0] = k;
+          d[1] = cnt[kk];                                          // its first entry in the worker's list
+          d[2] = b | (h << 20);
+          d[3] = (int32_t)(s0 - t0);                               // its first tile of the unit
+          d[4] = (int32_t)(s1 - s0) | (s1 == t1 ? SEG_LAST : 0);
+          d[5] = ctx;
+          d[6] = (int32_t)(kk - k0);                               // piece index
+          d[7] = np > 1 ? (base | ((np - 1) << 20) | ((int)(k0 % waves) << 28)) : -1;
+        }
+        if (!entries) {                                            // counts only
+          cnt[kk] += (int32_t)((s1 - s0) + ((s1 - s0) & 1));
+          continue;
+        }
         for (int64_t t = s0; t < s1 + ((s1 - s0) & 1); ++t) {      // the segment, then a pad if odd
           const bool pad = t >= s1;
           const int64_t tt = pad ? s1 - 1 : t;
@@ -813,6 +831,47 @@ int32_t stream_assign(const int32_t* context_lens, int32_t num_seqs, int32_t num
 
 
 namespace tb {
+
+// The tile entries of a decode plan from its segment descriptors (tb_build_decode_segments)
+// and the step's block tables on the device: one workgroup per descriptor, a thread per
+// entry (the segment's tiles, then a pad that repeats its last tile when the count is
+// odd). The same entries tb_build_decode_plan writes on the host. A block id outside
+// [0, num_blocks) or past its table is counted in `errors` and replaced by block 0,
+// so the decode kernel never reads outside the pool.
+__global__ void expand_plan_kernel(const int32_t* segs, const int32_t* tables, int32_t max_blocks_per_seq,
+                                   int32_t log2_bs, int64_t num_blocks, int32_t num_kv_heads, int32_t head_dim,
+                                   int4* entries, int32_t stride, uint32_t* errors) {
+  const int32_t* d = segs + 8 * (int64_t)blockIdx.x;
+  const int k = d[0], pos_first = d[1], bh = d[2], tu0 = d[3];
+  const int n = d[4] & 0x3FFFFFFF;
+  const bool unit_end = d[4] & (1 << 30);
+  const int ctx = d[5], piece = d[6], e3 = d[7];
+  const int b = bh & 0xFFFFF, h = bh >> 20;
+  const int bs = 1 << log2_bs;
+  const int64_t tb = 16 * 2 * (int64_t)head_dim;            // bytes of a 16-row K (or V) tile
+  const int64_t tile_bytes = tb << (log2_bs - 4);           // one kv head's K rows of a block
+  const int64_t blk_bytes = 2 * (int64_t)num_kv_heads * tile_bytes;
+  const int nent = n + (n & 1);
+  for (int i = threadIdx.x; i < nent; i += blockDim.x) {
+    const bool pad = i >= n;
+    const int tu = tu0 + (pad ? n - 1 : i);                  // tile of the unit
+    const int pos0 = 16 * tu;
+    const int bi = pos0 >> log2_bs;
+    int32_t blk = bi < max_blocks_per_seq ? tables[(int64_t)b * max_blocks_per_seq + bi] : -1;
+    if (blk < 0 || blk >= num_blocks) {
+      __hip_atomic_fetch_add(errors, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      blk = 0;
+    }
+    const int64_t off = (int64_t)blk * blk_bytes + h * tile_bytes + (int64_t)((pos0 & (bs - 1)) >> 4) * tb;
+    const int rows = ctx - pos0 < 16 ? ctx - pos0 : 16;
+    int4 e;
+    e.x = (int32_t)(uint32_t)(off >> 8);
+    e.y = b | (h << 20) | ((rows - 1) << 24) | (!pad && unit_end && i == n - 1 ? E_LAST_D : 0) | (pad ? E_NULL_D : 0);
+    e.z = ctx | (piece << 24);
+    e.w = e3;
+    entries[(int64_t)k * stride + pos_first + i] = e;
+  }
+}
 
 __global__ void xcc_probe_kernel(int32_t* out) {
   unsigned x;
@@ -917,6 +976,62 @@ extern "C" int32_t tb_build_decode_plan(const int32_t* context_lens, int32_t num
   if (std::adjacent_find(newest.begin(), newest.end()) != newest.end())
     for (int k = 0; k < workers; ++k) counts[k] |= TB_DECODE_SHARED_NEWEST;
   return TB_OK;
+}
+
+extern "C" int32_t tb_build_decode_segments(const int32_t* context_lens, int32_t num_seqs, int32_t num_kv_heads,
+                                            int32_t head_dim, const int32_t* block_tables,
+                                            int32_t max_blocks_per_seq, int32_t block_size, int32_t workgroups,
+                                            int32_t waves, int32_t num_xcds, int32_t unit_cost, int32_t* counts,
+                                            int32_t* segments, int32_t segment_capacity, int32_t* num_segments,
+                                            int32_t* max_entries, int32_t* pieces) {
+  if (!counts || !segments || !num_segments || segment_capacity <= 0 || workgroups <= 0 || waves <= 0)
+    return TB_ERR_INVALID_ARG;
+  if (block_tables && (max_blocks_per_seq <= 0 || block_size < 16 || (block_size & (block_size - 1))))
+    return TB_ERR_INVALID_ARG;
+  const int workers = workgroups * waves;
+  stream_layout lay;
+  int64_t ns = 0;
+  for (int k = 0; k < workers; ++k) counts[k] = 0;
+  const int32_t rc = stream_assign(context_lens, num_seqs, num_kv_heads, head_dim, nullptr, 0, 16, 0, workgroups,
+                                   waves, num_xcds, unit_cost, 0, counts, nullptr, lay, segments,
+                                   segment_capacity, &ns);
+  if (rc != TB_OK) return rc;
+  *num_segments = (int32_t)ns;
+  if (max_entries) *max_entries = lay.max_entries;
+  if (pieces) *pieces = lay.pieces;
+  if (block_tables) {   // the shared-newest-slot mark, as tb_build_decode_plan
+    std::vector<int64_t> newest(num_seqs);
+    for (int b = 0; b < num_seqs; ++b) {
+      const int p = context_lens[b] - 1;
+      if (p / block_size >= max_blocks_per_seq) return TB_ERR_INDEX;
+      newest[b] = (int64_t)block_tables[(int64_t)b * max_blocks_per_seq + p / block_size] * block_size + p % block_size;
+    }
+    std::sort(newest.begin(), newest.end());
+    if (std::adjacent_find(newest.begin(), newest.end()) != newest.end())
+      for (int k = 0; k < workers; ++k) counts[k] |= TB_DECODE_SHARED_NEWEST;
+  }
+  return TB_OK;
+}
+
+extern "C" int32_t tb_expand_decode_plan(const int32_t* segments, int32_t num_segments, const int32_t* block_tables,
+                                         int32_t max_blocks_per_seq, int32_t block_size, int64_t num_blocks,
+                                         int32_t num_kv_heads, int32_t head_dim, int32_t workers, int32_t stride,
+                                         int32_t* plan, uint32_t* errors, hipStream_t stream) {
+  if (num_segments < 0 || workers <= 0 || stride <= 0 || (stride & 1) || num_kv_heads <= 0 || num_kv_heads > 16 ||
+      (head_dim != 64 && head_dim != 128) || block_size < 16 || (block_size & (block_size - 1)) ||
+      max_blocks_per_seq <= 0 || num_blocks <= 0)
+    return TB_ERR_INVALID_ARG;
+  if (num_segments == 0) return TB_OK;
+  if (!segments || !block_tables || !plan || !errors || (((uintptr_t)plan) & 15u)) return TB_ERR_INVALID_ARG;
+  int log2_bs = 0;
+  while ((1 << log2_bs) < block_size) ++log2_bs;
+  // every tile offset >> 8 fits the entry's 32 bits
+  const int64_t blk_bytes = 2 * (int64_t)num_kv_heads * block_size * 2 * head_dim;
+  if (num_blocks > (((int64_t)1 << 40) / blk_bytes)) return TB_ERR_UNSUPPORTED;
+  int4* entries = reinterpret_cast<int4*>(plan + (size_t)(workers + 3) / 4 * 4);
+  hipLaunchKernelGGL(tb::expand_plan_kernel, dim3(num_segments), dim3(128), 0, stream, segments, block_tables,
+                     max_blocks_per_seq, log2_bs, num_blocks, num_kv_heads, head_dim, entries, stride, errors);
+  TB_RETURN_LAUNCH_STATUS();
 }
 
 extern "C" size_t tb_paged_decode_piece_bytes(int32_t num_heads, int32_t num_kv_heads, int32_t head_dim) {

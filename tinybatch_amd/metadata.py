@@ -87,6 +87,12 @@ class StepMetadata:
     decode_pieces: int = 0
     decode_units: int = 0
     decode_plan: torch.Tensor | None = None
+    # the same plan built on the device by meta.to (attach_decode_plan(on_device=True)):
+    # the count words and the segment descriptors (tb_build_decode_segments)
+    decode_counts_np: np.ndarray | None = None
+    decode_segments_np: np.ndarray | None = None
+    decode_kv_heads: int = 0
+    decode_head_dim: int = 0
     num_blocks: int = 0          # blocks of the pool the step's tables index
     # slot map of the work-item kernel with split rows merged inside the launch
     # (tb_paged_attention_merged): set by attach_xcd_slot_map
@@ -110,7 +116,8 @@ class StepMetadata:
             m.to(device)
         parts = [self.slot_mapping_np, self.block_tables_np.reshape(-1), self.work_np.reshape(-1),
                  self.row_part_off_np, self.prefill_tiles_np.reshape(-1), self.split_rows_np.reshape(-1)]
-        extra = [x for x in (self.decode_plan_np, self.slot_map_np, self.prefill_work_np) if x is not None]
+        extra = [x for x in (self.decode_plan_np, self.slot_map_np, self.prefill_work_np, self.decode_counts_np,
+                             self.decode_segments_np) if x is not None]
         parts += extra
         sizes = [pad4(p.size) for p in parts]
         host = np.zeros(sum(sizes), dtype=np.int32)
@@ -137,6 +144,11 @@ class StepMetadata:
             k += 1
         if self.prefill_work_np is not None:
             self.prefill_work = buf.narrow(0, int(offs[k]), parts[k].size)
+            k += 1
+        if self.decode_segments_np is not None:
+            counts = buf.narrow(0, int(offs[k]), parts[k].size)
+            segs = buf.narrow(0, int(offs[k + 1]), parts[k + 1].size)
+            self.decode_plan = _expand_decode_plan(self, counts, segs, device)
         return self
 
 
@@ -587,18 +599,93 @@ def build_decode_plan(context_lens, block_tables, *, block_size: int, num_blocks
     return plan, waves, stride, pieces.value
 
 
+def build_decode_segments(context_lens, block_tables, *, block_size: int, num_kv_heads: int, head_dim: int,
+                          workgroups: int, num_xcds: int, waves: int | None = None, unit_cost: int | None = None):
+    """tb_build_decode_segments: the host half of a decode plan built on the device
+    (count words [workers padded to 4], descriptors int32 [n, 8], waves, stride, partial
+    slots), or None when the kernel does not serve the step."""
+    import ctypes
+
+    from . import _lib
+
+    dflt = decode_defaults(head_dim)
+    if dflt is None:
+        return None
+    waves = dflt[0] if waves is None else int(waves)
+    unit_cost = dflt[1] if unit_cost is None else int(unit_cost)
+    L = _lib.lib()
+    if not L.tb_decode_variant_supported(head_dim, waves):
+        raise ValueError(f"the decode kernel has no {waves}-wave variant for head_dim {head_dim}")
+    ctx = np.ascontiguousarray(np.asarray(context_lens, dtype=np.int32).reshape(-1))
+    B = int(ctx.size)
+    if B == 0 or np.any(ctx <= 0):
+        raise ValueError("a decode plan needs >= 1 sequence, each with >= 1 position")
+    tables = np.ascontiguousarray(np.asarray(block_tables, dtype=np.int32).reshape(B, -1))
+    workers = workgroups * waves
+    counts = np.zeros((workers + 3) // 4 * 4, dtype=np.int32)
+    cap = B * num_kv_heads + workers
+    segs = np.zeros((cap, 8), dtype=np.int32)
+    vp = lambda a: a.ctypes.data_as(ctypes.c_void_p)   # noqa: E731
+    ns, me, pieces = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+    st = L.tb_build_decode_segments(vp(ctx), B, num_kv_heads, head_dim, vp(tables), tables.shape[1], block_size,
+                                    workgroups, waves, num_xcds, unit_cost, vp(counts), vp(segs), cap,
+                                    ctypes.byref(ns), ctypes.byref(me), ctypes.byref(pieces))
+    if st == _lib.TB_ERR_UNSUPPORTED:
+        return None
+    if st == _lib.TB_ERR_INDEX:
+        raise IndexError("a block table is too short for its context")
+    _lib.check(st, "tb_build_decode_segments")
+    stride = max(2, (me.value + 1) // 2 * 2)
+    return counts, segs[:ns.value].copy(), waves, stride, pieces.value
+
+
+def _expand_decode_plan(meta: StepMetadata, counts: torch.Tensor, segs: torch.Tensor,
+                        device: torch.device) -> torch.Tensor:
+    """The decode plan on the device: the count words, then the tile entries written by
+    tb_expand_decode_plan from the descriptors and the uploaded block tables, on the
+    device's current stream."""
+    from . import _lib, ops
+
+    workers = meta.decode_workgroups * meta.decode_waves
+    words = int(_lib.lib().tb_decode_plan_words(workers, meta.decode_stride))
+    plan = torch.empty(words, dtype=torch.int32, device=device)
+    plan[:counts.numel()].copy_(counts)
+    hkv, d = meta.decode_kv_heads, meta.decode_head_dim
+    _lib.check(_lib.lib().tb_expand_decode_plan(
+        segs.data_ptr(), int(meta.decode_segments_np.shape[0]), meta.block_tables.data_ptr(),
+        meta.max_blocks_per_seq, meta.block_size, meta.num_blocks, hkv, d, workers, meta.decode_stride,
+        plan.data_ptr(), ops.decode_device(device).violations.data_ptr(), _lib.stream_handle(device)),
+        "tb_expand_decode_plan")
+    return plan
+
+
 def attach_decode_plan(meta: StepMetadata, *, num_heads: int, num_kv_heads: int, head_dim: int,
                        dtype: torch.dtype, workgroups: int, num_xcds: int, waves: int | None = None,
-                       unit_cost: int | None = None) -> bool:
+                       unit_cost: int | None = None, on_device: bool = False) -> bool:
     """Give a decode-only step (row b = sequence b) the plan of the decode kernel, to be
     uploaded with the rest of its metadata by ``meta.to``. Returns whether it applies:
     16-bit rows, head_dim 64 / 128, at most 8 query heads per kv head, at most 16 kv
-    heads, blocks of >= 16 positions."""
+    heads, blocks of >= 16 positions. With ``on_device`` the host only assigns the
+    tiles (tb_build_decode_segments) and ``meta.to`` writes the plan's entries on the
+    device (tb_expand_decode_plan); the plan is the same."""
     if (not meta.rows_are_seqs or dtype not in (torch.float16, torch.bfloat16) or meta.block_size < 16
             or meta.device_buffer is not None or meta.num_blocks <= 0 or num_heads % num_kv_heads
             or num_heads // num_kv_heads > 8 or num_kv_heads > 16):
         return False
     B = meta.num_seqs
+    if on_device:
+        got = build_decode_segments(meta.row_ctx_np[:B], meta.block_tables_np[:B], block_size=meta.block_size,
+                                    num_kv_heads=num_kv_heads, head_dim=head_dim, workgroups=workgroups,
+                                    num_xcds=num_xcds, waves=waves, unit_cost=unit_cost)
+        if got is None:
+            return False
+        counts, segs, w, stride, pieces = got
+        meta.decode_counts_np, meta.decode_segments_np = counts, segs
+        meta.decode_workgroups, meta.decode_waves, meta.decode_stride = workgroups, w, stride
+        meta.decode_units = B * num_kv_heads
+        meta.decode_pieces = pieces
+        meta.decode_kv_heads, meta.decode_head_dim = num_kv_heads, head_dim
+        return True
     got = build_decode_plan(meta.row_ctx_np[:B], meta.block_tables_np[:B], block_size=meta.block_size,
                             num_blocks=meta.num_blocks, num_kv_heads=num_kv_heads, head_dim=head_dim,
                             workgroups=workgroups, num_xcds=num_xcds, waves=waves, unit_cost=unit_cost)

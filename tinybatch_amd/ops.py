@@ -291,8 +291,10 @@ def decode_waves_for(meta: StepMetadata, *, num_kv_heads: int, head_dim: int) ->
 
 def attach_decode_plan(meta: StepMetadata, *, num_heads: int, num_kv_heads: int, head_dim: int,
                        dtype: torch.dtype, device: torch.device, waves: int | None = None,
-                       unit_cost: int | None = None) -> bool:
-    """metadata.attach_decode_plan with this device's workgroups and XCDs; False (the
+                       unit_cost: int | None = None, on_device: bool = True) -> bool:
+    """metadata.attach_decode_plan with this device's workgroups and XCDs (by default the
+    plan's entries are written on the device by meta.to: the host assigns the tiles
+    only); False (the
     step stays with the work-item kernel) when the device's workgroup placement is not
     the one the kernel's in-XCD merges assume. ``waves`` None: the library's default
     variant (decode_waves_for)."""
@@ -304,7 +306,8 @@ def attach_decode_plan(meta: StepMetadata, *, num_heads: int, num_kv_heads: int,
     if waves is None:
         waves = decode_waves_for(meta, num_kv_heads=num_kv_heads, head_dim=head_dim)
     return attach(meta, num_heads=num_heads, num_kv_heads=num_kv_heads, head_dim=head_dim, dtype=dtype,
-                  workgroups=d.workgroups, num_xcds=d.num_xcds, waves=waves, unit_cost=unit_cost)
+                  workgroups=d.workgroups, num_xcds=d.num_xcds, waves=waves, unit_cost=unit_cost,
+                  on_device=on_device)
 
 
 def attach_split_parts(meta: StepMetadata, positions, seq_slices, block_tables, context_lens, *, num_heads: int,
