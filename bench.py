@@ -250,6 +250,12 @@ MFMA_PEAK_TFLOPS_16 = 2500.0
 
 
 def bench_mixed(args, dev) -> int:
+    """The mixed step (run_mixed) as its own JSON line."""
+    print(json.dumps(run_mixed(args, dev, with_cpu=not args.no_cpu)), flush=True)
+    return 0
+
+
+def run_mixed(args, dev, with_cpu: bool = True) -> dict:
     """Mixed engine step (8 x 512-token prefills + 56 decodes, shared prefix) and a
     1024-block compaction round, on rotating layer pools. Times the whole layer
     step (append + attention), the prefill rows alone (MFMA-bound: reported in
@@ -330,7 +336,7 @@ def bench_mixed(args, dev) -> int:
     ms_copy, _ = time_step(plan.launch, dev, args)
     _log(f"copy: {ms_copy * 1e3:.2f} us for {L} layer pools")
     cpu = None
-    if not args.no_cpu:
+    if with_cpu:
         _log("timing the CPU baseline (oracle) ...")
         cpu = cpu_baseline_mixed(wl, args.cpu_reps, args.cpu_budget)
 
@@ -375,8 +381,9 @@ def bench_mixed(args, dev) -> int:
                             "bytes_per_layer": b["append"], "kernel": "kv_append_kernel"},
         "cpu_baseline": cpu,
     }
-    print(json.dumps(line), flush=True)
-    return 0
+    del storage, pools
+    torch.cuda.empty_cache()
+    return line
 
 
 def run_e2e(dev, warmup: int, cpu: dict | None = None) -> dict:
@@ -504,6 +511,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (profiling runs)")
     ap.add_argument("--no-e2e", action="store_true",
                     help="headline: skip the end-to-end serving run whose tok/s and TTFT join the line")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="headline: skip the Llama-geometry and mixed-step sub-objects of the line")
     ap.add_argument("--partition", type=int, default=0)
     ap.add_argument("--no-tiles", action="store_true", help="mixed step: prefill rows as row groups, not tiles")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -518,9 +527,7 @@ def main() -> int:
 
     import torch
 
-    from tinybatch_amd import _lib, ops
-    from tinybatch_amd.metadata import build_step_metadata
-    from tinybatch_amd.workloads import make_decode_workload
+    from tinybatch_amd import _lib
 
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
@@ -545,10 +552,88 @@ def main() -> int:
     if args.workload == "qwen2-0.5b-e2e":
         return bench_e2e(args, dev)
 
-    big = args.workload == "llama-bf16-b256"
+    line = run_decode(args, dev, args.workload, batch=args.batch, with_cpu=not args.no_cpu)
+    if args.workload == "qwen-fp16-b64" and not args.batch and not args.no_extra:
+        # the other configurations in the same invocation, each with its own roofline
+        # and CPU baseline: the Llama-geometry decode at sigma 0.5 and 1.0, the mixed step
+        sub = argparse.Namespace(**vars(args))
+        sub.layers, sub.partition, sub.decode_waves, sub.unit_cost, sub.kernel = 0, 0, 0, -1, "auto"
+        for key, name in (("llama", "llama-bf16-b256"), ("llama_sigma1", "llama-bf16-b256-s1")):
+            _log(f"{name} ...")
+            line[key] = run_decode(sub, dev, name, with_cpu=not args.no_cpu)
+        _log("mixed step ...")
+        sub.no_tiles = sub.no_stream_prefill = sub.no_split_step = sub.no_decode_stream = False
+        line["mixed"] = run_mixed(sub, dev, with_cpu=not args.no_cpu)
+    if not args.no_e2e and args.workload == "qwen-fp16-b64" and not args.batch:
+        # the metric's second half: the serving workload through the engine, same invocation
+        _log("end-to-end serving run ...")
+        e2e = run_e2e(dev, 1, None if args.no_cpu else {"reps": 3, "budget": 10.0})
+        _log(f"e2e: {e2e['tok_s']} tok/s, TTFT mean {e2e['ttft_mean_ms']} ms, p99 {e2e['ttft_p99_ms']} ms")
+        line["e2e_tok_s"] = e2e["tok_s"]
+        line["ttft_mean_ms"] = e2e["ttft_mean_ms"]
+        line["ttft_p99_ms"] = e2e["ttft_p99_ms"]
+        line["e2e"] = e2e
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def host_step_cost(wl, dev, reps: int = 5) -> dict:
+    """Host work of one decode step's metadata, median over ``reps``: the step arrays from
+    the host lists (build_step_metadata), the decode plan's tile assignment
+    (tb_build_decode_segments), and the upload with the device-side plan expansion
+    (meta.to, synchronised); for comparison the plan built entry by entry on the host
+    (tb_build_decode_plan) and uploaded whole."""
+    import torch
+
+    from tinybatch_amd import ops
+    from tinybatch_amd.metadata import build_step_metadata
+
+    P = ops.partition_tokens(wl.dtype, wl.head_dim)
+    kw = dict(num_heads=wl.num_heads, num_kv_heads=wl.num_kv_heads, head_dim=wl.head_dim, dtype=wl.dtype,
+              device=dev)
+    res = {k: [] for k in ("metadata", "plan", "upload", "plan_host", "upload_host")}
+    for _ in range(reps + 1):
+        t0 = time.perf_counter()
+        meta = build_step_metadata(wl.positions, wl.seq_slices, wl.block_tables, wl.context_lens,
+                                   block_size=wl.block_size, num_blocks=wl.num_blocks, partition_tokens=P)
+        t1 = time.perf_counter()
+        ops.attach_decode_plan(meta, **kw)
+        t2 = time.perf_counter()
+        meta.to(dev)
+        torch.cuda.synchronize()
+        t3 = time.perf_counter()
+        meta2 = build_step_metadata(wl.positions, wl.seq_slices, wl.block_tables, wl.context_lens,
+                                    block_size=wl.block_size, num_blocks=wl.num_blocks, partition_tokens=P)
+        t4 = time.perf_counter()
+        ops.attach_decode_plan(meta2, on_device=False, **kw)
+        t5 = time.perf_counter()
+        meta2.to(dev)
+        torch.cuda.synchronize()
+        t6 = time.perf_counter()
+        for k, v in (("metadata", t1 - t0), ("plan", t2 - t1), ("upload", t3 - t2), ("plan_host", t5 - t4),
+                     ("upload_host", t6 - t5)):
+            res[k].append(v * 1e3)
+    med = {k: round(sorted(v[1:])[len(v[1:]) // 2], 3) for k, v in res.items()}   # first rep: warm-up
+    return {"metadata_ms": med["metadata"], "plan_ms": med["plan"], "upload_and_device_plan_ms": med["upload"],
+            "host_built_plan_ms": med["plan_host"], "host_built_plan_upload_ms": med["upload_host"],
+            "plan_bytes_host_built": int(meta2.decode_plan.numel() * 4) if meta2.decode_plan is not None else 0,
+            "reps": reps}
+
+
+def run_decode(args, dev, name: str, *, batch: int = 0, with_cpu: bool = True) -> dict:
+    """One decode workload: append + paged attention per layer pool, captured in a graph
+    and timed (time_step); returns the bench line's fields for it (metric, value in
+    algorithmic GB/s, roofline per call, CPU baseline, the host cost of a step's
+    metadata and plan)."""
+    import torch
+
+    from tinybatch_amd import ops
+    from tinybatch_amd.metadata import build_step_metadata
+    from tinybatch_amd.workloads import make_decode_workload
+
+    big = name.startswith("llama")
     t0 = time.perf_counter()
-    wl = make_decode_workload(args.workload, pool_device=(dev if big else "cpu"),
-                              **({"batch": args.batch} if args.batch else {}))
+    wl = make_decode_workload(name, pool_device=(dev if big else "cpu"), **({"batch": batch} if batch else {}))
     _log(f"workload {wl.name}: B={wl.batch} NB={wl.num_blocks} mean ctx={sum(wl.context_lens)/wl.batch:.0f} "
          f"({time.perf_counter() - t0:.1f}s)")
     pool_bytes = wl.pool.numel() * wl.pool.element_size()
@@ -559,6 +644,8 @@ def main() -> int:
     for l in range(L):
         storage[l].copy_(src)
     del src
+    if wl.pool.is_cuda:
+        wl.pool = None                                         # the draw lives on in the layer pools
     pools = [storage[l] for l in range(L)]
     P = args.partition or ops.partition_tokens(wl.dtype, wl.head_dim)
     meta = build_step_metadata(wl.positions, wl.seq_slices, wl.block_tables, wl.context_lens,
@@ -601,27 +688,32 @@ def main() -> int:
     if decode_kernel or merged:
         viol = int(ops.decode_device(dev).violations.item())
         if viol:
-            raise RuntimeError(f"{viol} units merged across XCDs: the workgroup placement assumption failed")
+            raise RuntimeError(f"{viol} in-launch merge errors: the workgroup placement assumption failed")
+    host = None
+    if decode_kernel:
+        _log("host cost of a step's metadata and plan ...")
+        host = host_step_cost(wl, dev)
+        # the model's attention time per step: Qwen2.5-0.5B has 24 layers, Llama-3-8B 32
+        model_layers = 32 if big else 24
+        attn_ms = per_launch_ms * model_layers
+        host["model_layers"] = model_layers
+        host["attention_ms_per_step"] = round(attn_ms, 4)
+        host["plan_frac_of_attention"] = round((host["plan_ms"] + host["upload_and_device_plan_ms"]) / attn_ms, 4)
+        host["host_built_plan_frac_of_attention"] = round(
+            (host["host_built_plan_ms"] + host["host_built_plan_upload_ms"]) / attn_ms, 4)
+    del storage, pools
+    torch.cuda.empty_cache()
 
     cpu = None
-    if not args.no_cpu:
+    if with_cpu:
         _log("timing the CPU baseline (oracle) ...")
         if big:
-            wl_cpu = make_decode_workload(args.workload, pool_device="cpu", batch=16)
+            wl_cpu = make_decode_workload(name, pool_device="cpu", batch=16)
         else:
             wl_cpu = wl
         cpu = cpu_baseline(wl_cpu, args.cpu_reps, args.cpu_budget)
         if big:
             cpu["sample"] += " (first 16 sequences of the workload)"
-
-    e2e = None
-    if not args.no_e2e and args.workload == "qwen-fp16-b64":
-        # the metric's second half: the serving workload through the engine, same invocation
-        del storage, pools
-        torch.cuda.empty_cache()
-        _log("end-to-end serving run ...")
-        e2e = run_e2e(dev, 1, None if args.no_cpu else {"reps": 3, "budget": 10.0})
-        _log(f"e2e: {e2e['tok_s']} tok/s, TTFT mean {e2e['ttft_mean_ms']} ms, p99 {e2e['ttft_p99_ms']} ms")
 
     if decode_kernel:
         kernel = "paged_stream_kernel"
@@ -629,7 +721,7 @@ def main() -> int:
         attn = "paged_attn_valu_kernel" if wl.dtype == torch.float32 else "paged_attn_mfma_kernel"
         kernel = attn if merged else attn + " + combine_partials_kernel"
     kernel += "" if fused else " + kv_append_kernel"
-    line = {
+    return {
         "metric": METRIC,
         "value": round(gbs, 2),
         "unit": "GB/s",
@@ -646,8 +738,8 @@ def main() -> int:
             "workload": f"{wl.name}: decode step, append 1 token/seq + paged attention, {L} layer pools",
             "batch": wl.batch, "num_heads": wl.num_heads, "num_kv_heads": wl.num_kv_heads,
             "head_dim": wl.head_dim, "block_size": wl.block_size, "num_blocks": wl.num_blocks,
-            "mean_context": round(sum(wl.context_lens) / wl.batch, 1), "layers": L,
-            "mode": args.mode, "graph": graph,
+            "mean_context": round(sum(wl.context_lens) / wl.batch, 1), "max_context": max(wl.context_lens),
+            "layers": L, "mode": args.mode, "graph": graph,
             "kernel": (f"decode ({meta.decode_waves} waves per workgroup)" if decode_kernel else
                        ("items, split rows merged in the launch" if merged else "items")),
             "partition_tokens": P,
@@ -659,15 +751,9 @@ def main() -> int:
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": kernel,
             "avg_launch_us": round(per_launch_ms * 1e3, 3),
         },
+        "host_step": host,
         "cpu_baseline": cpu,
     }
-    if e2e is not None:
-        line["e2e_tok_s"] = e2e["tok_s"]
-        line["ttft_mean_ms"] = e2e["ttft_mean_ms"]
-        line["ttft_p99_ms"] = e2e["ttft_p99_ms"]
-        line["e2e"] = e2e
-    print(json.dumps(line), flush=True)
-    return 0
 
 
 if __name__ == "__main__":

@@ -1,9 +1,12 @@
 """The Llama-3-8B-geometry decode step at its full size on the GPU: 32 query /
 8 KV heads, head_dim 128, bf16, 256 sequences with log-normal contexts (median
-8192, sigma 0.5, clipped to [1024, 32768]), one pool sized to fit every
-sequence (135,657 blocks of 64 KiB, 8.9 GB), values N(0,1) drawn on the GPU.
+8192, sigma 0.5 or 1.0, clipped to [1024, 32768]), one pool sized to fit every
+sequence (135,657 blocks of 64 KiB, 8.9 GB, at sigma 0.5; 175,571 blocks, 11.5
+GB, 13 contexts at the 32768 clip, at sigma 1.0), values N(0,1) drawn on the GPU.
 
-The whole batch runs through the fused append + attention launch. Sixteen
+The whole batch runs through the fused append + attention launch, once through
+the work items and once through the streaming decode kernel (its plan built on
+the device; the second append writes the same rows again). Sixteen
 sequences are then checked against the oracle: their blocks before the step
 (and after it) are brought back to the host, their tables remapped onto a
 compact pool, and the oracle's append + attention run there. Byte offsets of
@@ -24,8 +27,9 @@ pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda", 0)
 
 
-def test_config3_full_pool_fused_decode_bf16():
-    wl = make_decode_workload("llama-bf16-b256", pool_device=DEV)
+@pytest.mark.parametrize("name", ["llama-bf16-b256", "llama-bf16-b256-s1"])
+def test_config3_full_pool_fused_decode_bf16(name):
+    wl = make_decode_workload(name, pool_device=DEV)
     blk_bytes = wl.pool[0].numel() * wl.pool.element_size()
     past_4g = (1 << 32) // blk_bytes
     assert wl.num_blocks > past_4g and wl.batch == 256
@@ -37,6 +41,7 @@ def test_config3_full_pool_fused_decode_bf16():
     last_owner = next(b for b, t in enumerate(wl.block_tables) if wl.num_blocks - 1 in t)
     g = torch.Generator().manual_seed(31)
     pick = {order[0], order[1], order[-1], order[-2], last_owner}
+    pick |= set([b for b in range(wl.batch) if ctx[b] == max(ctx)][:6])      # contexts at the clip (sigma 1.0)
     for b in torch.randperm(wl.batch, generator=g).tolist():
         if len(pick) >= 16:
             break
@@ -49,14 +54,21 @@ def test_config3_full_pool_fused_decode_bf16():
     flat = torch.tensor(sum(used, []), dtype=torch.int64, device=DEV)
     before = wl.pool.index_select(0, flat).cpu()
 
-    meta = build_step_metadata(wl.positions, wl.seq_slices, wl.block_tables, ctx, block_size=wl.block_size,
-                               num_blocks=wl.num_blocks,
-                               partition_tokens=ops.partition_tokens(wl.dtype, wl.head_dim)).to(DEV)
-    out = ops.paged_attention(wl.q.to(DEV), wl.pool, meta, num_heads=wl.num_heads, k_new=wl.k_new.to(DEV),
-                              v_new=wl.v_new.to(DEV))
+    outs = {}
+    for kernel in ("items", "decode"):
+        meta = build_step_metadata(wl.positions, wl.seq_slices, wl.block_tables, ctx, block_size=wl.block_size,
+                                   num_blocks=wl.num_blocks,
+                                   partition_tokens=ops.partition_tokens(wl.dtype, wl.head_dim))
+        if kernel == "decode":
+            assert ops.attach_decode_plan(meta, num_heads=wl.num_heads, num_kv_heads=wl.num_kv_heads,
+                                          head_dim=wl.head_dim, dtype=wl.dtype, device=DEV)
+        meta.to(DEV)
+        out = ops.paged_attention(wl.q.to(DEV), wl.pool, meta, num_heads=wl.num_heads, k_new=wl.k_new.to(DEV),
+                                  v_new=wl.v_new.to(DEV))
+        outs[kernel] = out[torch.tensor(pick, device=DEV)].cpu()
     after = wl.pool.index_select(0, flat).cpu()
-    got = out[torch.tensor(pick, device=DEV)].cpu()
     torch.cuda.synchronize()
+    assert ops.decode_device(DEV).errors() == 0
 
     # the oracle on a compact pool holding just these blocks
     tables, at = [], 0
@@ -69,7 +81,8 @@ def test_config3_full_pool_fused_decode_bf16():
                            tables, wl.num_heads, wl.num_kv_heads, wl.block_size)
     assert torch.equal(after.view(torch.int16), want_pool.view(torch.int16)), "appended rows differ"
     assert not torch.equal(before.view(torch.int16), after.view(torch.int16))
-    err = (got.float() - want.float()).abs().max().item()
-    print(f"[config3] {len(pick)} sequences, contexts {min(ctx[b] for b in pick)}..{max(ctx[b] for b in pick)}: "
-          f"attention max|err| {err:.3e}", flush=True)
-    torch.testing.assert_close(got.float(), want.float(), atol=2e-2, rtol=2e-2)
+    for kernel, got in outs.items():
+        err = (got.float() - want.float()).abs().max().item()
+        print(f"[config3] {name} {kernel}: {len(pick)} sequences, contexts {min(ctx[b] for b in pick)}.."
+              f"{max(ctx[b] for b in pick)}: attention max|err| {err:.3e}", flush=True)
+        torch.testing.assert_close(got.float(), want.float(), atol=2e-2, rtol=2e-2)

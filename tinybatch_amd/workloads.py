@@ -8,6 +8,9 @@ Shapes follow the layer geometries the data path is measured on:
 * ``llama-bf16-b256`` Llama-3-8B layer (32 / 8 heads, head_dim 128), bf16, 256
   sequences with log-normal cached lengths (median 8192, sigma 0.5) clipped to
   [1024, 32768], pool sized to fit every sequence.
+* ``llama-bf16-b256-s1`` the same with sigma 1.0: a heavier tail, many contexts
+  at the 32768 clip (the distribution's sigma is not given; 0.5 and 1.0 are
+  both measured).
 Each decode step appends one token per sequence at position L (the cached
 length) and then attends over ctx = L + 1 positions, as LLMEngine.step does
 for running sequences (reference src/tinybatch/engine.py:114-120).
@@ -94,6 +97,8 @@ SPECS = {
                           num_blocks=32768, seed=2),
     "llama-bf16-b256": dict(Hq=32, Hkv=8, D=128, BS=16, dtype=torch.bfloat16, B=256,
                             lens=("lognormal", 8192, 0.5, 1024, 32768), num_blocks=None, seed=3),
+    "llama-bf16-b256-s1": dict(Hq=32, Hkv=8, D=128, BS=16, dtype=torch.bfloat16, B=256,
+                               lens=("lognormal", 8192, 1.0, 1024, 32768), num_blocks=None, seed=5),
 }
 
 
