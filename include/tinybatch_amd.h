@@ -229,12 +229,14 @@ int32_t tb_build_step_metadata(const int32_t* query_start_loc, int32_t num_seqs,
  * (append first), unless k_new / v_new are given:
  *   k_new, v_new (may be NULL, both or neither): the step's new K / V rows
  *     [num_rows][num_kv_heads][head_dim] (row strides in elements, 16-byte
- *     aligned); the kernel then reads each sequence's new rows from them and
- *     stores them to their pool slots (the append of kv_cache.py:25-38 fused:
- *     the pool afterwards equals tb_kv_append's, bit for bit). Needs every
- *     sequence's first new position (pos0) to be a multiple of 16 and no RoPE
- *     (TB_ERR_UNSUPPORTED with rope tables); with another pos0 the rows of
- *     that sequence are wrong (nothing is read or written out of bounds).
+ *     aligned); the kernel then reads each sequence's new rows from them (the
+ *     cached rows of a 16-position tile that holds the first new position from
+ *     the pool) and stores them to their pool slots (the append of
+ *     kv_cache.py:25-38 fused: the pool afterwards equals tb_kv_append's, bit
+ *     for bit). With rope tables the K rows are rotated at their positions
+ *     first, as tb_kv_append_rope does (model.py:125,128). The new rows' slots
+ *     must not be written by another row of the step (slot_mapping's superseded
+ *     rows, tb_build_step_metadata's counts[5], must be 0).
  *   work: tb_build_prefill_work's list (device memory), num_work entries;
  *     max_tiles: the value the builder returned.
  * q, out, strides, scale, dtype, rope: as tb_paged_attention. */

@@ -176,12 +176,15 @@ def test_fused_rope_equals_rotating_first(dtype):
 
 @pytest.mark.parametrize("BS", [16, 32])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_fused_append_stores_the_new_rows_and_reads_them_from_k_v(BS, dtype):
+@pytest.mark.parametrize("cached", [[0, 32, 0, 64], [0, 37, 5, 71]])
+def test_fused_append_stores_the_new_rows_and_reads_them_from_k_v(BS, dtype, cached):
     """k_new / v_new given: the kernel reads each sequence's new rows from them (the
     pool's new slots hold NaN before the call) and stores them: the pool afterwards
     equals the oracle's append bit for bit, the attention is within the bar of the
-    oracle on that pool. New rows 17 .. 100 after cached prefixes of 0 and 32."""
-    qlens, cached = [17, 100, 33, 16], [0, 32, 0, 64]
+    oracle on that pool. New rows 16 .. 100 after cached prefixes of 0 .. 71
+    positions, also ones whose first new row lies inside a 16-position tile (the
+    tile's earlier rows then come from the pool)."""
+    qlens = [17, 100, 33, 16]
     c = case(BS + 7, 14, 2, 64, BS, dtype, qlens, cached)
     g = torch.Generator().manual_seed(BS)
     T = sum(qlens)
@@ -207,18 +210,40 @@ def test_fused_append_stores_the_new_rows_and_reads_them_from_k_v(BS, dtype):
     torch.testing.assert_close(got.float(), want.float(), **TOL)
 
 
-def test_fused_append_refuses_what_it_cannot_serve():
-    c = case(5, 14, 2, 64, 16, torch.bfloat16, [20, 30], [8, 0])    # new rows from position 8
+@pytest.mark.parametrize("D,Hq,Hkv", [(64, 14, 2), (128, 16, 4)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fused_append_with_rope_equals_rotating_then_appending(D, Hq, Hkv, dtype):
+    """RoPE in the fused append (the reference rotates k, then writes it,
+    model.py:125,128): the kernel rotates the new K rows in LDS, stores them and
+    attends with them; pool and output equal, bit for bit, the rotating append
+    kernel followed by the unfused call (new rows also starting inside a tile)."""
+    qlens, cached = [40, 17, 100], [0, 9, 48]
+    c = case(31 + D, Hq, Hkv, D, 16, dtype, qlens, cached)
+    g = torch.Generator().manual_seed(D)
+    T = sum(qlens)
+    k = torch.randn(T, Hkv, D, generator=g).to(dtype).to(DEV)
+    v = torch.randn(T, Hkv, D, generator=g).to(dtype).to(DEV)
+    cos, sin = rope_tables(D, 1e6, 512, DEV)
+    rope = ops.Rope(cos, sin)
     meta = metadata(c)
-    k = torch.zeros(50, 2, 64, dtype=torch.bfloat16, device=DEV)
-    with pytest.raises(ValueError, match="multiple of 16"):
-        ops.paged_attention(c["q"].to(DEV), c["pool"].to(DEV), meta, num_heads=14, k_new=k, v_new=k)
-    c = case(6, 14, 2, 64, 16, torch.bfloat16, [20, 30], [16, 0])
-    meta = metadata(c)
-    cos, sin = rope_tables(64, 1e4, 256, DEV)
-    with pytest.raises(ValueError, match="no rope"):
-        ops.paged_attention(c["q"].to(DEV), c["pool"].to(DEV), meta, num_heads=14, k_new=k, v_new=k,
-                            rope=ops.Rope(cos, sin))
+    q = c["q"].to(DEV)
+    pool_a = c["pool"].to(DEV)
+    out_a = ops.paged_attention(q, pool_a, meta, num_heads=Hq, k_new=k, v_new=v, rope=rope)
+    pool_b = c["pool"].to(DEV)
+    pos = torch.tensor(c["pos"], dtype=torch.int64, device=DEV)
+    ops.kv_append(pool_b, k, v, meta.slot_mapping, rope=rope, positions=pos)
+    out_b = ops.paged_attention(q, pool_b, meta, num_heads=Hq, rope=rope)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(pool_a.cpu()), _bits(pool_b.cpu()))
+    assert torch.equal(_bits(out_a.cpu()), _bits(out_b.cpu()))
+    # and against the oracle: rotate q and the new k on the host, append, attend
+    qkv = torch.cat([q.reshape(T, -1), k.reshape(T, -1), v.reshape(T, -1)], 1)
+    qr, kr = layer_ops.rope_qk(qkv.contiguous(), pos, cos, sin, Hq, Hkv, D)
+    want_pool = c["pool"].clone()
+    ref.kv_write(want_pool, kr.cpu(), v.cpu(), pos.cpu(), c["slices"], c["tables"], 16)
+    want = ref.attention(qr.cpu(), want_pool, c["slices"], c["tables"], c["ctx"], Hq, Hkv)
+    assert torch.equal(_bits(pool_a.cpu()), _bits(want_pool))
+    torch.testing.assert_close(out_a.cpu().float(), want.float(), **TOL)
 
 
 def test_config4_split_step_appending_in_both_kernels():

@@ -52,9 +52,10 @@ struct prefill_args {
   int32_t log2_bs;             // block size: a power of two >= 16
   float scale_log2e;
   rope_tables rope;
-  // fused append (may be null): the step's new K / V rows [T][Hkv][D]; a sequence's
-  // new rows (positions pos0 .., pos0 a multiple of 16) are read from here and
-  // stored to their pool slots by the workgroup of block pair 0
+  // fused append (may be null): the step's new K / V rows [T][Hkv][D] (K before
+  // RoPE when rope tables are given); a sequence's new rows (positions pos0 ..) are
+  // read from here, K rotated in LDS, and stored to their pool slots by the
+  // workgroup of block pair 0
   const char* k_new;
   int64_t k_new_row_bytes;
   const char* v_new;
@@ -368,26 +369,28 @@ __global__ __launch_bounds__(pshape<D>::MAXREP / pshape<D>::HPW * 128, 1) void p
     for (int j = 0; wave + NW * j < T; ++j) {
       const int t = wave + NW * j;
       char* const dst = lds + t * TILE;
-      if (a.k_new != nullptr && 16 * t >= pos0) {
-        // a tile of new rows, from the step's k / v rows (rows past the sequence's
-        // last one repeat it: their scores are masked and their V rows zeroed below)
-        const int nr0 = 16 * t - pos0;                 // the tile's first new row
-        const int last = nrows - 1 - nr0;
-        const char* kb = a.k_new + (int64_t)(row0 + nr0) * a.k_new_row_bytes + (int64_t)kvh * RB;
-        const char* vb = a.v_new + (int64_t)(row0 + nr0) * a.v_new_row_bytes + (int64_t)kvh * RB;
+      const int b = __builtin_amdgcn_readlane(myb, j);
+      const char* base = a.pool + (int64_t)b * blk_bytes + kvh * head_bytes + (int64_t)(t & sub_mask) * TB;
+      if (a.k_new != nullptr && 16 * t + 15 >= pos0) {
+        // a tile holding new rows: those from the step's k / v rows (rows past the
+        // sequence's last one repeat it: their scores are masked and their V rows
+        // zeroed below), the tile's rows before pos0 from the pool
+        const char* kb = a.k_new + (int64_t)row0 * a.k_new_row_bytes + (int64_t)kvh * RB;
+        const char* vb = a.v_new + (int64_t)row0 * a.v_new_row_bytes + (int64_t)kvh * RB;
 #pragma unroll
         for (int i = 0; i < TLD; ++i) {
           const int f = 64 * i + lane;
           const int r = f / VCOLS, cs = f % VCOLS;
-          const int rr = r < last ? r : last;
-          s_dma16_l2((uint32_t)(rr * a.k_new_row_bytes) + 16u * (uint32_t)(cs ^ stream_kswz(r)), kb, dst + 1024 * i);
-          s_dma16_l2((uint32_t)(rr * a.v_new_row_bytes) + 16u * (uint32_t)(cs ^ stream_vswz(r)), vb,
-                     dst + TB + 1024 * i);
+          const int nr = 16 * t + r - pos0;            // the row's index among the new rows
+          const int rr = nr < nrows - 1 ? nr : nrows - 1;
+          const uint32_t kc = 16u * (uint32_t)(cs ^ stream_kswz(r)), vc = 16u * (uint32_t)(cs ^ stream_vswz(r));
+          const char* ks = nr >= 0 ? kb + (int64_t)rr * a.k_new_row_bytes + kc : base + (int64_t)r * RB + kc;
+          const char* vs = nr >= 0 ? vb + (int64_t)rr * a.v_new_row_bytes + vc : base + v_off + (int64_t)r * RB + vc;
+          s_dma16_l2p(ks, dst + 1024 * i);
+          s_dma16_l2p(vs, dst + TB + 1024 * i);
         }
         continue;
       }
-      const int b = __builtin_amdgcn_readlane(myb, j);
-      const char* base = a.pool + (int64_t)b * blk_bytes + kvh * head_bytes + (int64_t)(t & sub_mask) * TB;
 #pragma unroll
       for (int i = 0; i < TLD; ++i) {
         s_dma16_l2(koff[i], base, dst + 1024 * i);
@@ -430,6 +433,27 @@ __global__ __launch_bounds__(pshape<D>::MAXREP / pshape<D>::HPW * 128, 1) void p
       int after = 0;
       for (int tt = wave; tt < T; tt += NW) after += tt >= CH * (c + 1);
       s_vm_wait_le(2 * TLD * after);
+      if (a.k_new != nullptr && a.rope.cos != nullptr) {
+        // RoPE of the new K rows this wave loaded (the reference rotates k before the
+        // write, model.py:125,128): chunk cs of a row pairs with chunk cs + VCOLS/2
+        // (dims i and i + D/2), at the row's position; the bits of tb_kv_append_rope
+        for (int tt = wave; tt < min(T, CH * (c + 1)); tt += NW) {
+          if (tt < CH * c || 16 * tt + 15 < pos0) continue;
+          char* const kt = lds + tt * TILE;
+          for (int f = lane; f < 16 * (VCOLS / 2); f += 64) {
+            const int r = f / (VCOLS / 2), cs = f % (VCOLS / 2);
+            const int p = 16 * tt + r;
+            if (p < pos0 || p >= ctx) continue;
+            vec16* const x1 = reinterpret_cast<vec16*>(kt + r * RB + 16 * (cs ^ stream_kswz(r)));
+            vec16* const x2 = reinterpret_cast<vec16*>(kt + r * RB + 16 * ((cs + VCOLS / 2) ^ stream_kswz(r)));
+            vec16 v1 = *x1, v2 = *x2;
+            const int64_t rr = a.rope.row(p, D / 2) + 8 * cs;
+            rope_pair<typename smath<Tag>::scalar_t>(v1, v2, a.rope.cos + rr, a.rope.sin + rr);
+            *x1 = v1;
+            *x2 = v2;
+          }
+        }
+      }
       if ((T - 1) / CH == c && (T - 1) % NW == wave && 16 * T > ctx) {   // V rows past the context: zeros
         char* const vt = lds + (T - 1) * TILE + TB;
         const int r0 = ctx - 16 * (T - 1);
@@ -444,8 +468,9 @@ __global__ __launch_bounds__(pshape<D>::MAXREP / pshape<D>::HPW * 128, 1) void p
       // from LDS (chunk f of a tile holds row f / VCOLS, chunk (f % VCOLS) ^ swizzle)
       for (int j = 0; wave + NW * j < T; ++j) {
         const int t = wave + NW * j;
-        if (16 * t < pos0) continue;
-        const int valid = min(16, pos0 + nrows - 16 * t);   // new rows in the tile
+        if (16 * t + 15 < pos0) continue;
+        const int first = max(0, pos0 - 16 * t);           // the tile's rows first .. valid - 1 are new
+        const int valid = min(16, pos0 + nrows - 16 * t);
         const int b = __builtin_amdgcn_readlane(myb, j);
         char* const pk = a.pool + (int64_t)b * blk_bytes + kvh * head_bytes +
                          (int64_t)(t & sub_mask) * TB;
@@ -454,7 +479,7 @@ __global__ __launch_bounds__(pshape<D>::MAXREP / pshape<D>::HPW * 128, 1) void p
         for (int i = 0; i < TLD; ++i) {
           const int f = 64 * i + lane;
           const int r = f / VCOLS, cs = f % VCOLS;
-          if (r < valid) {
+          if (r >= first && r < valid) {
             st16(pk + r * RB + 16 * (cs ^ stream_kswz(r)), *reinterpret_cast<const vec16*>(src + 16 * f));
             st16(pk + v_off + r * RB + 16 * (cs ^ stream_vswz(r)), *reinterpret_cast<const vec16*>(src + TB + 16 * f));
           }
@@ -664,7 +689,6 @@ extern "C" int32_t tb_paged_prefill(const void* q, int64_t q_row_stride, void* p
   TB_CHECK_ARG(!rope_cos == !rope_sin && (!rope_cos || rope_max_position > 0));
   TB_CHECK_ARG(!k_new == !v_new);
   if (k_new) {
-    if (rope_cos) return TB_ERR_UNSUPPORTED;   // the stored K rows would need the rotation
     TB_CHECK_ARG(k_row_stride >= (int64_t)num_kv_heads * head_dim && v_row_stride >= (int64_t)num_kv_heads * head_dim);
     TB_CHECK_ARG((((uintptr_t)k_new | (uintptr_t)v_new) & 15u) == 0 && (k_row_stride * 2) % 16 == 0 &&
                  (v_row_stride * 2) % 16 == 0);

@@ -81,6 +81,11 @@ __device__ __forceinline__ void s_dma16_l2(uint32_t off, const void* base, const
                : "memory");
 }
 
+// The same with a per-lane 64-bit address and no non-temporal hint.
+__device__ __forceinline__ void s_dma16_l2p(const void* src, const void* lds_dst) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(s_lds_addr(lds_dst)) : "memory");
+}
+
 // Wait until at most n vector memory instructions of this wave are outstanding
 // (they complete in issue order); n is wave-uniform.
 template <int LO, int HI>

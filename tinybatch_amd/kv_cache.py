@@ -25,6 +25,7 @@ the step's arguments change.
 """
 from __future__ import annotations
 
+import numpy as np
 import torch
 
 from . import _lib, ops
@@ -173,6 +174,33 @@ class PagedKVCache:
         rows = self.rows_per_item(hq)
         meta = self._lookup_or_build(positions, seq_slices, block_tables, context_lens, q.shape[0], rows, hq)
         return ops.paged_attention(q, self.pools[layer], meta, num_heads=hq, scale=scale, out=out, rope=rope)
+
+    def append_attention(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, positions,
+                         seq_slices, block_tables, context_lens, *, num_heads: int | None = None,
+                         scale: float | None = None, out: torch.Tensor | None = None,
+                         rope: ops.Rope | None = None) -> torch.Tensor:
+        """write() then attention() (model.py:128-147) with the append folded into the
+        attention kernels where the step's kernels can do both: decode-only steps, steps
+        of whole prefills (tb_paged_prefill) and mixed steps split into those two sides,
+        when no slot is written by two rows of the step; otherwise the two calls. With
+        ``rope`` q and k are the projections before rotation."""
+        hq = num_heads if num_heads is not None else q.shape[1]
+        rows = self.rows_per_item(hq)
+        meta = self._lookup_or_build(positions, seq_slices, block_tables, context_lens, q.shape[0], rows, hq)
+        if self._fusable(meta):
+            return ops.paged_attention(q, self.pools[layer], meta, num_heads=hq, scale=scale, out=out, rope=rope,
+                                       k_new=k, v_new=v)
+        self.write(layer, k, v, positions, seq_slices, block_tables, rope=rope)
+        return ops.paged_attention(q, self.pools[layer], meta, num_heads=hq, scale=scale, out=out, rope=rope)
+
+    @staticmethod
+    def _fusable(meta: StepMetadata) -> bool:
+        sm = meta.slot_mapping_np
+        if sm.size and np.any((sm < 0) & (meta.row_ctx_np > 0)):
+            return False                                  # a superseded writer: the separate append
+        if meta.parts is not None or meta.decode_only:
+            return True
+        return bool(meta.num_prefill_work and not meta.num_work_items and not meta.num_prefill_tiles)
 
     def decode_step(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, meta: StepMetadata,
                     *, num_heads: int | None = None, scale: float | None = None,

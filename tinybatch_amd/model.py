@@ -176,9 +176,9 @@ class Qwen2Paged:
         """Logits [n_seqs, vocab] (fp32) for the last token of each sequence (model.py:101-158)."""
         rope = self.rope if self.fused_rope else None
 
-        def attention(i, q, k, v):
-            kv_cache.write(i, k, v, positions, seq_slices, block_tables, rope=rope)
-            return kv_cache.attention(i, q, positions, seq_slices, block_tables, context_lens, rope=rope)
+        def attention(i, q, k, v):   # the append (kv_cache.write) folded into attention where it can be
+            return kv_cache.append_attention(i, q, k, v, positions, seq_slices, block_tables, context_lens,
+                                             rope=rope)
 
         x = self.run_layers(token_ids, positions, attention, fused_rope=self.fused_rope)
         last = torch.tensor([e - 1 for _, e in seq_slices], device=x.device)

@@ -468,10 +468,9 @@ def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, 
     if meta.decode_plan is not None and not noalloc and q.dtype in (torch.float16, torch.bfloat16):
         return paged_decode(q, pool, meta, num_heads=num_heads, scale=scale, out=out, k_new=k_new, v_new=v_new,
                             rope=rope)
-    if meta.parts is not None and not noalloc and ((k_new is None and v_new is None) or rope is None):
+    if meta.parts is not None and not noalloc:
         # a split mixed step (attach_split_parts): each sub-step on its own rows; with
-        # k_new / v_new each side appends its own rows (no RoPE: the prefill kernel
-        # stores the rows as given)
+        # k_new / v_new each side appends its own rows (K rotated first with ``rope``)
         _lib.require_gpu_tensor("q", q)
         d = pool.shape[-1]
         if q.shape[0] != meta.num_tokens:
@@ -490,10 +489,6 @@ def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, 
             if sm.size and np.any((sm < 0) & (meta.row_ctx_np > 0)):
                 raise ValueError("two rows of the step write one pool slot; the fused append cannot serve "
                                  "the step: append with kv_append, then call paged_attention without k_new")
-        for _, _, m in meta.parts if fused else ():   # refused before any part launches
-            if m.num_prefill_work and np.any(m.prefill_work_np.reshape(-1, 4)[:m.num_prefill_work, 2] % 16):
-                raise ValueError("the prefill kernel's fused append needs each sequence's new rows to start "
-                                 "at a multiple of 16 positions: append with kv_append first")
         for r0, r1, m in meta.parts:
             paged_attention(q[r0:r1], pool, m, num_heads=num_heads, scale=scale, out=out[r0:r1], rope=rope,
                             k_new=k_new[r0:r1] if fused else None, v_new=v_new[r0:r1] if fused else None)
@@ -538,12 +533,7 @@ def paged_attention(q: torch.Tensor, pool: torch.Tensor, meta: StepMetadata, *, 
             raise ValueError("k_new and v_new go together")
         if meta.num_prefill_work and not meta.num_work_items and not meta.num_prefill_tiles:
             # whole prefill sequences only: tb_paged_prefill reads their new rows from
-            # k_new / v_new and stores them (no RoPE; new rows start on a 16-position tile)
-            if rope is not None:
-                raise ValueError("the prefill kernel's fused append takes rotated rows (no rope)")
-            if np.any(meta.prefill_work_np.reshape(-1, 4)[:meta.num_prefill_work, 2] % 16):
-                raise ValueError("the prefill kernel's fused append needs each sequence's new rows to start "
-                                 "at a multiple of 16 positions: append with kv_append first")
+            # k_new / v_new (K rotated in the kernel with ``rope``) and stores them
             prefill_fused = True
         elif not meta.decode_only or meta.num_prefill_tiles or meta.num_prefill_work:
             raise ValueError("fused append needs a decode-only step (one query row per sequence) or a step of "
