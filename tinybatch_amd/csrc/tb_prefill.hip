@@ -141,12 +141,12 @@ __device__ __forceinline__ su32x4_t ones_operand() {
 
 // The online-softmax state of HPW heads x 16 rows (lane (lg, lc) holds row lc):
 // the row's reference max m (p <= 2^8 against it; -inf until the row has seen a
-// position, with -m taken as 0 then, so that masked scores give p = 0), its O^T
-// column (acc[h][nn] = O^T[16 nn + 4 lg + jj][row lc]) and its sum (every element
-// of l[h]).
+// position, with -m taken as 0 then, so that masked scores give p = 0), the raw
+// score above which m must move (thr = (m + 8) / (scale log2 e)), its O^T column
+// (acc[h][nn] = O^T[16 nn + 4 lg + jj][row lc]) and its sum (every element of l[h]).
 template <int NSL, int HPW>
 struct pstate {
-  float m[HPW], negm[HPW];
+  float m[HPW], negm[HPW], thr[HPW];
   float4_t acc[HPW][NSL];
   float4_t l[HPW];
   __device__ __forceinline__ void reset() {
@@ -154,6 +154,7 @@ struct pstate {
     for (int h = 0; h < HPW; ++h) {
       m[h] = -INFINITY;
       negm[h] = 0.f;
+      thr[h] = -INFINITY;
       l[h] = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int nn = 0; nn < NSL; ++nn) acc[h][nn] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -167,7 +168,7 @@ struct pstate {
 template <typename Tag, int D, int HPW>
 __device__ __forceinline__ void pstep(pstate<D / 16, HPW>& st, const su32x4_t (&q)[HPW][D / 32], uint32_t lds_tile,
                                       const uint32_t (&ka0)[D / 32], const uint32_t (&va0)[D / 16], int t, bool bnull,
-                                      int prow, int first_pos, float sl2e, su32x4_t ones) {
+                                      int prow, int first_pos, float sl2e, float inv_sl2e, su32x4_t ones) {
   using S = pshape<D>;
   using M = smath<Tag>;
   constexpr int KS = S::KS, NSL = S::NSL, TILE = S::TILE;
@@ -209,9 +210,9 @@ __device__ __forceinline__ void pstep(pstate<D / 16, HPW>& st, const su32x4_t (&
   bool grow = false;
 #pragma unroll
   for (int h = 0; h < HPW; ++h) {
-    lm[h] = max3_f32(max_f32(sa[h][0], sa[h][1]), sa[h][2], sa[h][3]);
-    lm[h] = max3_f32(lm[h], max_f32(sb[h][0], sb[h][1]), max_f32(sb[h][2], sb[h][3]));
-    grow = grow || lm[h] * sl2e > st.m[h] + 8.f;
+    lm[h] = max3_f32(max3_f32(sa[h][0], sa[h][1], sa[h][2]), max3_f32(sa[h][3], sb[h][0], sb[h][1]),
+                     max_f32(sb[h][2], sb[h][3]));
+    grow = grow || lm[h] > st.thr[h];
   }
   if (__any(grow)) {
 #pragma unroll
@@ -222,6 +223,7 @@ __device__ __forceinline__ void pstep(pstate<D / 16, HPW>& st, const su32x4_t (&
         const float alpha = fast_exp2(st.m[h] - m_new);   // 0 while m = -inf
         st.m[h] = m_new;
         st.negm[h] = -m_new;
+        st.thr[h] = (m_new + 8.f) * inv_sl2e;
 #pragma unroll
         for (int nn = 0; nn < NSL; ++nn) st.acc[h][nn] *= alpha;
         st.l[h] *= alpha;
@@ -404,7 +406,7 @@ __global__ __launch_bounds__(pshape<D>::MAXREP / pshape<D>::HPW * 128, 1) void p
   }
 
   // ---- the wave's tasks over their tiles, chunk by chunk as the chunks land ----
-  const float sl2e = a.scale_log2e;
+  const float sl2e = a.scale_log2e, inv_sl2e = 1.f / a.scale_log2e;
   const su32x4_t ones = ones_operand<Tag>();
   uint32_t ka0[KS], va0[NSL];                       // tile 0's addresses of this lane
   {
@@ -503,7 +505,7 @@ __global__ __launch_bounds__(pshape<D>::MAXREP / pshape<D>::HPW * 128, 1) void p
       const int bk = e_step ? pair : blk_l;
       const int tk = e_step ? TE : TL;
       pstep<Tag, D, HPW>(st, qa, lds0 + 2 * k * TILE, ka0, va0, 2 * k, 2 * k + 1 >= tk,
-                         pos0 + min(16 * bk + lc, nrows - 1), pos0 + 16 * bk, sl2e, ones);
+                         pos0 + min(16 * bk + lc, nrows - 1), pos0 + 16 * bk, sl2e, inv_sl2e, ones);
       if (e_step && i == ne_me - 1 && k + 1 >= se) {   // the earlier block is done: written whole
         pwrite<Tag, D, HPW>(a, st, row0, nrows, pair, hd0, nh);
         st.reset();
