@@ -5,6 +5,7 @@ import pytest
 import torch
 
 from oracle import model_reference as mref
+from tinybatch_amd import ops
 from tinybatch_amd.block_manager import BlockManager
 from tinybatch_amd.config import EngineConfig
 from tinybatch_amd.engine import LLMEngine
@@ -193,6 +194,95 @@ def test_decode_graph_replays_match_eager_steps_bf16():
         assert torch.equal(a[:sum(len(t) for t in tables)].view(torch.int16)[:, 1],
                            b[:sum(len(t) for t in tables)].view(torch.int16)[:, 1]) or \
             torch.allclose(a.float(), b.float(), atol=2e-2, rtol=2e-2)
+
+
+def _prefilled_caches(model, mc, lens, n, BS=16, NB=256, seed=8):
+    g = torch.Generator().manual_seed(seed)
+    tables, at = [], 0
+    for L in lens:
+        k = L // BS + 1
+        tables.append(list(range(at, at + k)))
+        at += k
+    prompts = [torch.randint(0, mc.vocab_size, (L,), generator=g).tolist() for L in lens]
+    ids = torch.tensor(sum(prompts, []), device=DEV)
+    pos = torch.tensor(sum([list(range(L)) for L in lens], []), device=DEV)
+    slices, at = [], 0
+    for L in lens:
+        slices.append((at, at + L))
+        at += L
+    caches = [PagedKVCache(mc.n_layers, NB, BS, mc.n_kv_heads, mc.head_dim, DEV, model.dtype) for _ in range(n)]
+    for cache in caches:
+        model.forward(ids, pos, slices, tables, lens, cache)
+    return caches, tables, prompts
+
+
+def test_merged_decode_graphs_equal_the_work_item_graphs_bf16():
+    """Captured decode steps on the merged launch (split rows merged inside the
+    attention launch, slot map in the staging buffer) against the same steps on
+    the work items and their combine launch: identical token ids and identical
+    pools, step after step, and no merge errors."""
+    from tinybatch_amd.decode_graphs import DecodeGraphs
+    if not ops.decode_device(DEV).merge_in_kernel:
+        pytest.skip("the device's workgroup placement does not allow in-launch merges")
+    mc = small_cfg(layers=2, heads=14, kv_heads=2, vocab=500)
+    model = Qwen2Paged(mc, DEV, torch.bfloat16, seed=7)
+    P = ops.partition_tokens(torch.bfloat16, mc.head_dim)
+    lens = [37, 3 * P + 5, 16, P + 1, 129, 2 * P]
+    caches, tables, prompts = _prefilled_caches(model, mc, lens, 2)
+    merged = DecodeGraphs(model, caches[0], max_batch=8, max_model_len=4 * P)
+    items = DecodeGraphs(model, caches[1], max_batch=8, max_model_len=4 * P)
+    items.merged = False                         # before the first capture
+    assert merged.merged and merged.slots > 0
+    toks, ctx = [p[-1] for p in prompts], list(lens)
+    for _ in range(4):
+        positions = list(ctx)
+        ctx = [c + 1 for c in ctx]
+        a = merged.run(toks, positions, tables, ctx)
+        b = items.run(toks, positions, tables, ctx)
+        assert a == b
+        toks = a
+    torch.cuda.synchronize()
+    assert ops.decode_device(DEV).errors() == 0 and merged.merged
+    n = sum(len(t) for t in tables)
+    for layer in range(mc.n_layers):
+        assert torch.equal(caches[0].pools[layer][:n].view(torch.int16), caches[1].pools[layer][:n].view(torch.int16))
+
+
+def test_engine_recomputes_captured_steps_after_a_merge_error():
+    """A merge error reported by a captured (pipelined) decode step: the engine runs
+    that step and the one queued from its ids again, eagerly, the graphs move to the
+    work items, and every request ends with the tokens of an undisturbed run."""
+    if not ops.decode_device(DEV).merge_in_kernel:
+        pytest.skip("the device's workgroup placement does not allow in-launch merges")
+    mc = small_cfg(layers=2, heads=14, kv_heads=2, vocab=500)
+    P = ops.partition_tokens(torch.bfloat16, mc.head_dim)
+    g = torch.Generator().manual_seed(11)
+    prompts = [torch.randint(0, mc.vocab_size, (n,), generator=g).tolist() for n in (P + 40, 2 * P + 3, 70, 300)]
+    budget = 12
+
+    def run(inject_at):
+        ecfg = EngineConfig(dtype="bfloat16", num_blocks=256, block_size=16, max_batch_tokens=4096, max_running=8,
+                            max_model_len=4 * P, decode_graphs=True, pipeline_decode=True)
+        eng = LLMEngine(ecfg, model=Qwen2Paged(mc, DEV, torch.bfloat16, seed=9))
+        reqs = [eng.add_request(p, max_new_tokens=budget) for p in prompts]
+        assert eng.graphs.merged
+        while eng.has_work():
+            if eng.pipelined_steps == inject_at:
+                ops.decode_device(DEV).violations.fill_(1)   # as a merge across two XCDs would count
+            eng.step()
+        return eng, [list(r.output_token_ids) for r in reqs]
+
+    clean, want = run(inject_at=-1)
+    assert clean.merge_failures == 0 and clean.pipelined_steps > 4
+    dd = ops.decode_device(DEV)
+    try:
+        hit, got = run(inject_at=3)
+        assert hit.merge_failures == 1 and not hit.graphs.merged and not dd.merge_in_kernel
+        assert got == want
+        assert dd.errors() == 0
+    finally:
+        dd.merge_in_kernel = True                               # later tests keep in-launch merges
+        dd.violations.zero_()
 
 
 @pytest.mark.parametrize("graphs", [True, False])

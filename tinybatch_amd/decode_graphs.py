@@ -16,6 +16,20 @@ graph, captured once, whose launches read fixed device buffers:
   to 32 rows the LM head and the argmax are one fused kernel that never
   writes the logits).
 
+Attention in the captured step is one launch per layer. A 16-bit model on a
+device whose workgroups land on its XCDs round robin (ops.DecodeDevice) runs
+tb_paged_attention_merged: the partitions of a split row run on one XCD and
+the last one to finish merges them, with no combine launch. Its grid is the
+bucket's slot capacity (the bound of the slot map's longest-first packing:
+num_xcds * (ceil(items * kv heads / num_xcds) + partitions per row)); the
+step's slot map (tb_build_xcd_slot_map over its work items, padded with -1,
+whose workgroups exit at once) rides in the staging buffer. The device's
+merge error count is copied back with every step's token ids: a nonzero count
+makes ``collect`` raise MergeErrors after switching the graphs to the work
+items and their combine launch (recaptured on next use) and in-launch merges
+off on the device. Otherwise (fp32, no split rows, another placement) the
+work-item kernel reads the device counts, and a combine launch merges split rows.
+
 Per step the host packs the tokens, positions and metadata straight into one
 pinned staging buffer (pack_decode_step: the arrays build_step_metadata would
 give, built for decode rows only), copies it with one host-to-device copy, and
@@ -36,10 +50,16 @@ import torch.nn.functional as F
 
 from . import layer_ops, ops
 from .kv_cache import PagedKVCache
-from .metadata import StepMetadata, decode_staging_offsets, pack_decode_step
+from .metadata import MERGED_MAX_PARTS, StepMetadata, decode_staging_offsets, pack_decode_step
 from .model import Qwen2Paged
 
 DEFAULT_BUCKETS = (1, 2, 4, 8, 16, 24, 32, 48, 64, 96, 128, 192, 256)
+
+
+class MergeErrors(RuntimeError):
+    """A captured step's in-launch merges reported errors: its token ids, and those of
+    any step launched from them, cannot be used. The graphs have switched to the work
+    items and their combine launch; the steps must be computed again."""
 
 
 class DecodeGraphs:
@@ -60,14 +80,23 @@ class DecodeGraphs:
         # comes from the host; r >= 0: row r of the previous step's ids)
         self.offs = decode_staging_offsets(B, self.max_nb, self.max_parts)
         n = int(self.offs[-1])
-        nbytes = 4 * n + 24 * B
+        # the merged launch (see the module docstring): its slot map follows the int64 tail
+        d = ops.decode_device(self.dev)
+        self.num_xcds = d.num_xcds
+        self.merged = (d.merge_in_kernel and d.num_xcds > 1 and model.dtype in (torch.float16, torch.bfloat16)
+                       and c.n_heads // c.n_kv_heads <= 16 and 1 < self.max_parts <= MERGED_MAX_PARTS)
+        self.slots = self._slot_capacity(B) if self.merged else 0
+        nbytes = 4 * n + 24 * B + 4 * self.slots
         self.dev_buf = torch.zeros(nbytes, dtype=torch.uint8, device=self.dev)
         self.host_bufs = [torch.zeros(nbytes, dtype=torch.uint8).pin_memory() for _ in range(2)]
         self.dev_i32 = self.dev_buf[:4 * n].view(torch.int32)
         self.host_nps = [h[:4 * n].view(torch.int32).numpy() for h in self.host_bufs]
-        self.host_tps = [h[4 * n:].view(torch.int64).view(3, B).numpy() for h in self.host_bufs]
-        tail = self.dev_buf[4 * n:].view(torch.int64).view(3, B)
+        self.host_tps = [h[4 * n:4 * n + 24 * B].view(torch.int64).view(3, B).numpy() for h in self.host_bufs]
+        tail = self.dev_buf[4 * n:4 * n + 24 * B].view(torch.int64).view(3, B)
         self.tok, self.pos, self.src = tail[0], tail[1], tail[2]
+        self.dev_slots = self.dev_buf[4 * n + 24 * B:].view(torch.int32)
+        self.host_slots = [h[4 * n + 24 * B:].view(torch.int32).numpy() for h in self.host_bufs]
+        self.host_errs = [torch.zeros(1, dtype=torch.int32).pin_memory() for _ in range(2)]
         self.ids = torch.zeros(B, dtype=torch.int64, device=self.dev)
         self.host_ids = [torch.zeros(B, dtype=torch.int64).pin_memory() for _ in range(2)]
         self.turn = 0       # which staging / id buffer the next launch uses
@@ -81,6 +110,11 @@ class DecodeGraphs:
         self.head_ws = torch.empty(max(int(head_bytes), 16), dtype=torch.uint8, device=self.dev)
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
         self.pool = None    # graph memory pool shared by the buckets
+
+    def _slot_capacity(self, Bp: int) -> int:
+        """Slots of the merged launch for a bucket: the longest-first packing's bound."""
+        X, hkv = self.num_xcds, self.model.cfg.n_kv_heads
+        return X * (-(-Bp * self.max_parts * hkv // X) + self.max_parts)
 
     # ---- metadata at capacity ---------------------------------------------------
     def _view(self, i: int, n: int) -> torch.Tensor:
@@ -102,6 +136,8 @@ class DecodeGraphs:
         m.split_rows = self._view(4, Bp * 4).view(Bp, 4)
         m.prefill_tiles = m.split_rows            # never read: no tiles in a decode step
         m.device_counts = self._view(5, 4)
+        if self.merged:
+            m.slot_map = self.dev_slots[:self._slot_capacity(Bp)]
         return m
 
     # ---- the captured step -------------------------------------------------------
@@ -133,6 +169,8 @@ class DecodeGraphs:
         meta = self._meta(Bp)
         torch.cuda.synchronize(self.dev)                            # no step in flight reads the buffers
         self.dev_i32[int(self.offs[5]):int(self.offs[5]) + 4].zero_()   # no work: warm-up launches exit at once
+        if self.merged:
+            meta.slot_map.fill_(-1)                                 # no slot runs an item in the warm-up
         self.src.zero_()                                            # in-range source rows for the warm-up
         ids = self.ids.clone()          # the last step's tokens, which the next launch may read
         stream = torch.cuda.Stream(device=self.dev)
@@ -184,6 +222,16 @@ class DecodeGraphs:
             # read its own. Nothing is queued: the caller runs this step unfused.
             self.turn ^= 1
             return None
+        if self.merged:
+            import ctypes
+
+            from . import _lib
+            W = int(h[self.offs[5]])
+            work = h[self.offs[2]:self.offs[2] + 4 * W]
+            vp = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+            _lib.check(_lib.lib().tb_build_xcd_slot_map(vp(work), W, self.model.cfg.n_kv_heads, self.num_xcds,
+                                                        vp(self.host_slots[k]), self._slot_capacity(Bp)),
+                       "tb_build_xcd_slot_map")
         tp[0, :B] = tokens
         tp[1, :B] = positions
         tp[2, :B] = -1 if src_rows is None else src_rows
@@ -192,6 +240,8 @@ class DecodeGraphs:
         self.dev_buf.copy_(self.host_bufs[k], non_blocking=True)
         g.replay()
         self.host_ids[k][:Bp].copy_(self.ids[:Bp], non_blocking=True)
+        if self.merged:
+            self.host_errs[k].copy_(ops.decode_device(self.dev).violations, non_blocking=True)
         ev = torch.cuda.Event()
         ev.record()
         self.last_use[k] = ev
@@ -202,6 +252,12 @@ class DecodeGraphs:
         before the launch after next, which reuses the step's id buffer."""
         B, k, ev = handle
         ev.synchronize()
+        if self.merged and int(self.host_errs[k][0]) != 0:
+            torch.cuda.synchronize(self.dev)         # nothing in flight uses the graphs or the counters
+            ops.decode_device(self.dev).disable_merges()
+            self.merged = False
+            self.graphs.clear()                      # recaptured with the work items on next use
+            raise MergeErrors("a captured decode step's in-launch merges reported errors")
         return self.host_ids[k][:B].tolist()
 
     def run(self, tokens: list[int], positions: list[int], block_tables: list[list[int]],

@@ -39,7 +39,7 @@ import torch
 from . import ops
 from .block_manager import BlockManager
 from .config import EngineConfig
-from .decode_graphs import DecodeGraphs
+from .decode_graphs import DecodeGraphs, MergeErrors
 from .kv_cache import PagedKVCache
 from .model import ModelConfig, Qwen2Paged
 from .scheduler import Request, Scheduler, Status
@@ -188,12 +188,19 @@ class LLMEngine:
             if len(r.output_token_ids) >= r.max_new_tokens or r.context_len() >= self.cfg.max_model_len:
                 self.scheduler.finish(r)
         self._inflight = {"reqs": ordered, "handle": handle, "idx": idx,
-                          "row_of": {r.req_id: i for i, r in enumerate(ordered)}}
+                          "row_of": {r.req_id: i for i, r in enumerate(ordered)},
+                          "tokens": tokens, "src": src, "ctx": ctx}
         return self._collect(prev) if prev is not None else []
 
     def _collect(self, rec: dict) -> list[StepOutput]:
         """A queued step's tokens into its requests' placeholders."""
-        ids = self.graphs.collect(rec["handle"])
+        if "ids" in rec:                      # computed again after a merge error
+            ids = rec["ids"]
+        else:
+            try:
+                ids = self.graphs.collect(rec["handle"])
+            except MergeErrors:
+                ids = self._recompute_queued(rec)
         if self._inflight is rec:
             self._inflight = None
         now = time.perf_counter()
@@ -215,6 +222,40 @@ class LLMEngine:
         self.steps += 1
         return outputs
 
+    def _recompute_queued(self, rec: dict) -> list[int]:
+        """A captured step whose in-launch merges reported errors (the graphs now run
+        the work items and in-launch merges are off): that step again, eagerly, and the
+        step queued after it from its ids, whose ids are kept for its own collect and
+        written where the next launch reads its source rows. Running a step again
+        appends its rows to the same slots; a step with a request that finished at its
+        launch (its blocks are freed) cannot be run again, which raises."""
+        self.merge_failures += 1
+        self.kv_cache.clear_metadata()
+        nxt = self._inflight if self._inflight is not None and self._inflight is not rec else None
+        steps = [rec] + ([nxt] if nxt is not None else [])
+        if any(not r.block_table for st in steps for r in st["reqs"]):
+            raise RuntimeError("a captured decode step reported in-launch merge errors after some of its "
+                               "requests finished (their blocks are freed): its tokens cannot be computed again")
+
+        def again(st, prev_ids):
+            toks = []
+            for i, (r, s) in enumerate(zip(st["reqs"], st["src"])):
+                if s < 0:
+                    toks.append(st["tokens"][i])
+                elif prev_ids is not None:
+                    toks.append(prev_ids[s])
+                else:                         # the previous step's token, collected before this one
+                    toks.append(r.output_token_ids[st["idx"][i] - 1])
+            n, ctx = len(toks), st["ctx"]
+            return self._forward_eager(st["reqs"], toks, [c - 1 for c in ctx], [(i, i + 1) for i in range(n)],
+                                       [r.block_table for r in st["reqs"]], ctx)
+
+        ids = again(rec, None)
+        if nxt is not None:
+            nxt["ids"] = again(nxt, ids)
+            self.graphs.ids[:len(nxt["ids"])].copy_(torch.tensor(nxt["ids"], dtype=torch.int64))
+        return ids
+
     def _step_sync(self) -> list[StepOutput]:
         batch = self.scheduler.schedule()
         self._swap(batch)
@@ -232,7 +273,12 @@ class LLMEngine:
         token_ids, positions, seq_slices, block_tables, context_lens = self.build_step(prefill, decode)
         if (graphs and self.graphs is not None and not prefill and all(r.temperature <= 0.0 for r in ordered)
                 and self.graphs.bucket(len(ordered)) is not None):
-            next_ids = self.graphs.run(token_ids, positions, block_tables, context_lens)
+            try:
+                next_ids = self.graphs.run(token_ids, positions, block_tables, context_lens)
+            except MergeErrors:               # the step again, eagerly (in-launch merges are off now)
+                self.merge_failures += 1
+                self.kv_cache.clear_metadata()
+                next_ids = None
             if next_ids is not None:
                 self.graph_steps += 1
                 return self._finish_step(ordered, next_ids)

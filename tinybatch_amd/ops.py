@@ -176,9 +176,11 @@ class DecodeDevice:
         self.num_xcds, self.merge_in_kernel = self._verify(device, cus, nx)
         # the error count of the in-launch merges (tb_paged_decode, tb_paged_attention_merged):
         # nonzero after a call whose outputs cannot be trusted (a unit's partials on two
-        # XCDs, a malformed plan, a refused fused append)
-        self.violations = torch.zeros(1, dtype=torch.int32, device=device)
-        self._host_errors = torch.zeros(1, dtype=torch.int32).pin_memory()
+        # XCDs, a malformed plan, a refused fused append); ordinary tensors even when the
+        # device is first used under inference mode (they are updated in place later)
+        with torch.inference_mode(False):
+            self.violations = torch.zeros(1, dtype=torch.int32, device=device)
+            self._host_errors = torch.zeros(1, dtype=torch.int32).pin_memory()
 
     def errors_async(self) -> torch.Tensor:
         """Queue a copy of the error count on the current stream into pinned host memory;
