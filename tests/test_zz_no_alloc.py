@@ -2,7 +2,9 @@
 library's static per-GPU scratch) against tb_paged_attention with a caller
 workspace: the same kernels, so the same bits, on two calls in a row, the
 second smaller than the first (the scratch keeps the first call's partials,
-which the second must not read)."""
+which the second must not read); the call makes no allocation through torch's
+allocator (its allocation count is unchanged across it); and the call captured
+in a HIP graph gives the same bits on every replay, with other work between."""
 import pytest
 import torch
 
@@ -29,8 +31,11 @@ def _both(wl, fused: bool):
     outs = [torch.full((wl.batch, wl.num_heads * wl.head_dim), float("nan"), dtype=wl.dtype, device=DEV)
             for _ in range(2)]
     ops.paged_attention(q, pools[0], meta, num_heads=wl.num_heads, out=outs[0], **kv)
+    torch.cuda.synchronize()
+    allocs = torch.cuda.memory_stats(DEV)["allocation.all.allocated"]
     ops.paged_attention(q, pools[1], meta, num_heads=wl.num_heads, out=outs[1], noalloc=True, **kv)
     torch.cuda.synchronize()
+    assert torch.cuda.memory_stats(DEV)["allocation.all.allocated"] == allocs
     return outs, pools
 
 
@@ -54,3 +59,30 @@ def test_noalloc_needs_an_output_buffer():
                                partition_tokens=ops.partition_tokens(wl.dtype, wl.head_dim)).to(DEV)
     with pytest.raises(ValueError, match="output buffer"):
         ops.paged_attention(wl.q.to(DEV), wl.pool.to(DEV), meta, num_heads=wl.num_heads, noalloc=True)
+
+
+def test_noalloc_call_replays_from_a_captured_graph():
+    wl = make_decode_workload("qwen-fp16-b64", seed=5, batch=16)
+    meta = build_step_metadata(wl.positions, wl.seq_slices, wl.block_tables, wl.context_lens,
+                               block_size=wl.block_size, num_blocks=wl.num_blocks,
+                               partition_tokens=ops.partition_tokens(wl.dtype, wl.head_dim)).to(DEV)
+    assert meta.max_parts_per_row > 1
+    pool, q = wl.pool.to(DEV), wl.q.to(DEV)
+    want = ops.paged_attention(q, pool, meta, num_heads=wl.num_heads)
+    out = torch.full((wl.batch, wl.num_heads * wl.head_dim), float("nan"), dtype=wl.dtype, device=DEV)
+    ops.paged_attention(q, pool, meta, num_heads=wl.num_heads, out=out, noalloc=True)   # eager, before capture
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(out), _bits(want))
+    g = torch.cuda.CUDAGraph()
+    stream = torch.cuda.Stream(device=DEV)
+    stream.wait_stream(torch.cuda.current_stream(DEV))
+    with torch.cuda.graph(g, stream=stream):
+        ops.paged_attention(q, pool, meta, num_heads=wl.num_heads, out=out, noalloc=True)
+    for i in range(4):
+        out.fill_(float("nan"))                    # eager work between the replays
+        other = ops.paged_attention(q, pool, meta, num_heads=wl.num_heads)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(_bits(out), _bits(want)), f"replay {i}"
+        assert torch.equal(_bits(other), _bits(want))
