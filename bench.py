@@ -300,7 +300,8 @@ def run_mixed(args, dev, with_cpu: bool = True) -> dict:
         if which == "decode" and not args.no_decode_stream and ops.decode_kernel_preferred(
                 meta, num_kv_heads=wl.num_kv_heads, head_dim=wl.head_dim, dtype=wl.dtype):
             if ops.attach_decode_plan(meta, num_heads=Hq, num_kv_heads=wl.num_kv_heads, head_dim=wl.head_dim,
-                                      dtype=wl.dtype, device=dev):
+                                      dtype=wl.dtype, device=dev,
+                                      unit_cost=args.unit_cost if args.unit_cost >= 0 else None):
                 dec_kernel = "paged_stream_kernel"
         meta = meta.to(dev)
         q, k, v = w.q.to(dev), w.k_new.to(dev), w.v_new.to(dev)
@@ -740,7 +741,8 @@ def run_decode(args, dev, name: str, *, batch: int = 0, with_cpu: bool = True) -
             "head_dim": wl.head_dim, "block_size": wl.block_size, "num_blocks": wl.num_blocks,
             "mean_context": round(sum(wl.context_lens) / wl.batch, 1), "max_context": max(wl.context_lens),
             "layers": L, "mode": args.mode, "graph": graph,
-            "kernel": (f"decode ({meta.decode_waves} waves per workgroup)" if decode_kernel else
+            "kernel": (f"decode ({meta.decode_waves} waves per workgroup, unit cost {meta.decode_unit_cost})"
+                       if decode_kernel else
                        ("items, split rows merged in the launch" if merged else "items")),
             "partition_tokens": P,
             "bytes_per_layer_step": bytes_layer["total"],

@@ -435,6 +435,16 @@ size_t tb_paged_decode_workspace_bytes(int32_t max_pieces, int32_t num_heads, in
 int32_t tb_decode_defaults(int32_t head_dim, int32_t* waves, int32_t* unit_cost);
 int32_t tb_decode_variant_supported(int32_t head_dim, int32_t waves);
 
+/* The per-unit cost to build this step's decode plan with (the plan builders
+ * below take it): tb_decode_defaults' cost, or that cost - 2 when the lower one
+ * gives the busiest worker >= 5% fewer entries (tb_decode_plan_shape), since a
+ * worker's time goes by its entries. context_lens is host memory; returns the
+ * errors of tb_decode_plan_shape. No counterpart in the reference (part of the
+ * decode plan that replaces its per-sequence gather, src/tinybatch/kv_cache.py:40-45). */
+int32_t tb_decode_unit_cost(const int32_t* context_lens, int32_t num_seqs, int32_t num_kv_heads,
+                            int32_t head_dim, int32_t workgroups, int32_t waves, int32_t num_xcds,
+                            int32_t* unit_cost);
+
 /* Host-side plan of a decode step (no device call, nothing allocated): units
  * (sequence b, kv head h), each cut into ceil(context_lens[b] / 16) tiles, are
  * packed onto num_xcds XCDs (longest first, least loaded XCD; a unit weighs

@@ -269,3 +269,36 @@ def test_segments_carry_the_shared_newest_mark():
     host = build_decode_plan(ctx, tables, block_size=16, num_blocks=nb, num_kv_heads=2, head_dim=64, workgroups=8,
                              num_xcds=8, waves=4)[0]
     np.testing.assert_array_equal(counts[:32], host[:32])
+
+
+def _max_entries(ctx, hkv, D, uc, waves=4):
+    tables, nb = tables_for(ctx, 16, np.random.default_rng(7))
+    plan, w, stride, _ = build_decode_plan(ctx, tables, block_size=16, num_blocks=nb, num_kv_heads=hkv, head_dim=D,
+                                           workgroups=256, num_xcds=8, waves=waves, unit_cost=uc)
+    return int(decode(plan, 256 * w, stride)[0].max() & 0x3FFFFFFF)
+
+
+def test_unit_cost_is_lowered_only_when_it_empties_the_busiest_worker():
+    """tb_decode_unit_cost against the built plans' own counts: the headline step (64
+    sequences of 513..4096 positions) gets 18 entries per busiest worker at cost 6
+    against 20 at the default 8, so 6; the 56 decode rows of the mixed step tie (the
+    default stays); the Llama-geometry step saves < 5% (the default stays)."""
+    from tinybatch_amd.metadata import decode_defaults, decode_unit_cost
+    from tinybatch_amd.workloads import make_decode_workload, make_mixed_workload
+
+    mixed = make_mixed_workload()
+    cases = [
+        ("headline", make_decode_workload("qwen-fp16-b64").context_lens, 2, 64, 6),
+        ("mixed", [c for c, q in zip(mixed.context_lens, mixed.q_lens) if q == 1], 2, 64, 8),
+    ]
+    rng = np.random.default_rng(11)
+    cases.append(("llama", (rng.integers(256, 4096, 256) + 1).tolist(), 8, 128, None))
+    for name, ctx, hkv, D, want in cases:
+        dflt = decode_defaults(D)[1]
+        got = decode_unit_cost(ctx, num_kv_heads=hkv, head_dim=D, workgroups=256, num_xcds=8, waves=4)
+        me, me_lower = _max_entries(ctx, hkv, D, dflt), _max_entries(ctx, hkv, D, dflt - 2)
+        assert got in (dflt, dflt - 2), name
+        assert (got == dflt - 2) == (me_lower * 20 <= me * 19), name
+        if want is not None:
+            assert got == want, name
+    assert _max_entries(cases[0][1], 2, 64, 6) == 18 and _max_entries(cases[0][1], 2, 64, 8) == 20

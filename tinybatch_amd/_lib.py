@@ -82,6 +82,7 @@ SIGNATURES = {
     "tb_paged_decode_workspace_bytes": (c_sz, [c_i32, c_i32, c_i32, c_i32]),
     "tb_decode_defaults": (c_i32, [c_i32, c_vp, c_vp]),
     "tb_decode_variant_supported": (c_i32, [c_i32, c_i32]),
+    "tb_decode_unit_cost": (c_i32, [c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp]),
     "tb_decode_plan_shape": (c_i32, [c_vp, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_vp]),
     "tb_decode_plan_words": (c_sz, [c_i32, c_i32]),
     "tb_build_decode_plan": (c_i32, [c_vp, c_i32, c_i32, c_i32, c_vp, c_i32, c_i32, c_i64, c_i32, c_i32, c_i32,

@@ -301,12 +301,17 @@ __global__ __launch_bounds__(64 * W) void paged_stream_kernel(const stream_args 
       s_dma16_s(koff[i], baseA, dst + 1024 * i);
       s_dma16_s(voff[i], baseA, dst + TB + 1024 * i);
     }
+    // a pad loads nothing: its scores are masked and its V operand is tile A's, so its
+    // slot's stale bytes are never used
+    if (!(eB.y & E_NULL_D)) {
 #pragma unroll
-    for (int i = 0; i < TLD; ++i) {
-      s_dma16_s(koff[i], baseB, dst + 2 * TB + 1024 * i);
-      s_dma16_s(voff[i], baseB, dst + 3 * TB + 1024 * i);
+      for (int i = 0; i < TLD; ++i) {
+        s_dma16_s(koff[i], baseB, dst + 2 * TB + 1024 * i);
+        s_dma16_s(voff[i], baseB, dst + 3 * TB + 1024 * i);
+      }
+      issued += 2 * TLD;
     }
-    issued += 4 * TLD;
+    issued += 2 * TLD;
   };
 
   int4 esA[STEPS], esB[STEPS];                   // the entries of each step slot's pair
@@ -798,7 +803,7 @@ int32_t stream_assign(const int32_t* context_lens, int32_t num_seqs, int32_t num
             const int64_t off = (int64_t)blk * blk_bytes + h * tile_bytes + (int64_t)((pos0 % block_size) / 16) * tb;
             if ((off >> 8) >= ((int64_t)1 << 32)) return TB_ERR_UNSUPPORTED;
             const int rows = std::min(16, ctx - pos0);
-            e[0] = (int32_t)(uint32_t)(off >> 8);   // a pad reloads the segment's last tile (its bytes are unused)
+            e[0] = (int32_t)(uint32_t)(off >> 8);   // a pad: the segment's last tile (never loaded)
             e[1] = b | (h << 20) | ((rows - 1) << 24) | (!pad && t == t1 - 1 ? E_LAST : 0) | (pad ? E_NULL : 0);
             e[2] = ctx | ((int)(kk - k0) << 24);
             e[3] = np > 1 ? (base | ((np - 1) << 20) | ((int)(k0 % waves) << 28)) : -1;
@@ -935,6 +940,32 @@ extern "C" int32_t tb_decode_plan_shape(const int32_t* context_lens, int32_t num
   if (rc != TB_OK) return rc;
   if (max_entries) *max_entries = lay.max_entries;
   if (pieces) *pieces = lay.pieces;
+  return TB_OK;
+}
+
+// The plan balances weights (tiles + unit cost per unit), but a worker's time goes by
+// its entries, in pairs: when the weight shares round the busiest workers up to an
+// extra pair, a unit cost 2 lower that saves >= 5% of the busiest worker's entries is
+// used instead. Measured at head dim 64, four waves, 64 / 128 sequences of 513..4096
+// positions: 20 -> 18 and 38 -> 36 entries, +1.3..3.7% and +1.2% per call; where the
+// entries tie (56 decode rows of a mixed step) the lower cost was 2..6% slower.
+extern "C" int32_t tb_decode_unit_cost(const int32_t* context_lens, int32_t num_seqs, int32_t num_kv_heads,
+                                       int32_t head_dim, int32_t workgroups, int32_t waves, int32_t num_xcds,
+                                       int32_t* unit_cost) {
+  if (!unit_cost) return TB_ERR_INVALID_ARG;
+  int32_t dw = 0, uc = 0;
+  int32_t rc = tb_decode_defaults(head_dim, &dw, &uc);
+  if (rc != TB_OK) return rc;
+  int32_t me = 0, me_lower = 0;
+  rc = tb_decode_plan_shape(context_lens, num_seqs, num_kv_heads, head_dim, workgroups, waves, num_xcds, uc, &me,
+                            nullptr);
+  if (rc != TB_OK) return rc;
+  if (uc >= 2 &&
+      tb_decode_plan_shape(context_lens, num_seqs, num_kv_heads, head_dim, workgroups, waves, num_xcds, uc - 2,
+                           &me_lower, nullptr) == TB_OK &&
+      (int64_t)me_lower * 20 <= (int64_t)me * 19)
+    uc -= 2;
+  *unit_cost = uc;
   return TB_OK;
 }
 

@@ -85,6 +85,7 @@ class StepMetadata:
     decode_waves: int = 0
     decode_stride: int = 0
     decode_pieces: int = 0
+    decode_unit_cost: int = 0
     decode_units: int = 0
     decode_plan: torch.Tensor | None = None
     # the same plan built on the device by meta.to (attach_decode_plan(on_device=True)):
@@ -555,6 +556,25 @@ def decode_defaults(head_dim: int):
     return (w.value, uc.value) if st == 0 else None
 
 
+def decode_unit_cost(context_lens, *, num_kv_heads: int, head_dim: int, workgroups: int, num_xcds: int,
+                     waves: int) -> int:
+    """tb_decode_unit_cost: the per-unit cost a step's decode plan is built with by
+    default (the head dim's default cost, or 2 lower when that gives the busiest worker
+    >= 5% fewer entries)."""
+    import ctypes
+
+    from . import _lib
+
+    ctx = np.ascontiguousarray(np.asarray(context_lens, dtype=np.int32).reshape(-1))
+    uc = ctypes.c_int32()
+    st = _lib.lib().tb_decode_unit_cost(ctx.ctypes.data_as(ctypes.c_void_p), int(ctx.size), num_kv_heads,
+                                        head_dim, workgroups, waves, num_xcds, ctypes.byref(uc))
+    if st == _lib.TB_ERR_UNSUPPORTED and decode_defaults(head_dim) is not None:
+        return decode_defaults(head_dim)[1]   # no plan serves the step: the builder says so
+    _lib.check(st, "tb_decode_unit_cost")
+    return uc.value
+
+
 def build_decode_plan(context_lens, block_tables, *, block_size: int, num_blocks: int, num_kv_heads: int,
                       head_dim: int, workgroups: int, num_xcds: int, waves: int | None = None,
                       unit_cost: int | None = None) -> tuple[np.ndarray, int, int, int] | None:
@@ -570,7 +590,6 @@ def build_decode_plan(context_lens, block_tables, *, block_size: int, num_blocks
     if dflt is None:
         return None
     waves = dflt[0] if waves is None else int(waves)
-    unit_cost = dflt[1] if unit_cost is None else int(unit_cost)
     L = _lib.lib()
     if not L.tb_decode_variant_supported(head_dim, waves):
         raise ValueError(f"the decode kernel has no {waves}-wave variant for head_dim {head_dim}")
@@ -578,6 +597,10 @@ def build_decode_plan(context_lens, block_tables, *, block_size: int, num_blocks
     B = int(ctx.size)
     if B == 0 or np.any(ctx <= 0):
         raise ValueError("a decode plan needs >= 1 sequence, each with >= 1 position")
+    if unit_cost is None:
+        unit_cost = decode_unit_cost(ctx, num_kv_heads=num_kv_heads, head_dim=head_dim, workgroups=workgroups,
+                                     num_xcds=num_xcds, waves=waves)
+    unit_cost = int(unit_cost)
     tables = np.ascontiguousarray(np.asarray(block_tables, dtype=np.int32).reshape(B, -1))
     vp = lambda a: a.ctypes.data_as(ctypes.c_void_p)
     me, pieces = ctypes.c_int32(), ctypes.c_int32()
@@ -612,7 +635,6 @@ def build_decode_segments(context_lens, block_tables, *, block_size: int, num_kv
     if dflt is None:
         return None
     waves = dflt[0] if waves is None else int(waves)
-    unit_cost = dflt[1] if unit_cost is None else int(unit_cost)
     L = _lib.lib()
     if not L.tb_decode_variant_supported(head_dim, waves):
         raise ValueError(f"the decode kernel has no {waves}-wave variant for head_dim {head_dim}")
@@ -620,6 +642,10 @@ def build_decode_segments(context_lens, block_tables, *, block_size: int, num_kv
     B = int(ctx.size)
     if B == 0 or np.any(ctx <= 0):
         raise ValueError("a decode plan needs >= 1 sequence, each with >= 1 position")
+    if unit_cost is None:
+        unit_cost = decode_unit_cost(ctx, num_kv_heads=num_kv_heads, head_dim=head_dim, workgroups=workgroups,
+                                     num_xcds=num_xcds, waves=waves)
+    unit_cost = int(unit_cost)
     tables = np.ascontiguousarray(np.asarray(block_tables, dtype=np.int32).reshape(B, -1))
     workers = workgroups * waves
     counts = np.zeros((workers + 3) // 4 * 4, dtype=np.int32)
@@ -673,6 +699,14 @@ def attach_decode_plan(meta: StepMetadata, *, num_heads: int, num_kv_heads: int,
             or num_heads // num_kv_heads > 8 or num_kv_heads > 16):
         return False
     B = meta.num_seqs
+    dflt = decode_defaults(head_dim)
+    if dflt is None:
+        return False
+    if unit_cost is None:
+        unit_cost = decode_unit_cost(meta.row_ctx_np[:B], num_kv_heads=num_kv_heads, head_dim=head_dim,
+                                     workgroups=workgroups, num_xcds=num_xcds,
+                                     waves=dflt[0] if waves is None else int(waves))
+    meta.decode_unit_cost = int(unit_cost)
     if on_device:
         got = build_decode_segments(meta.row_ctx_np[:B], meta.block_tables_np[:B], block_size=meta.block_size,
                                     num_kv_heads=num_kv_heads, head_dim=head_dim, workgroups=workgroups,
