@@ -81,6 +81,7 @@ struct pshape {
   // 12.7 us per layer)
   static constexpr int CH = 64;
   static_assert(MAXT * TILE <= 160 * 1024, "LDS budget of a workgroup");
+  static_assert(MAXT <= CH, "one chunk: the tile loads may go out in any order");
 };
 
 // The reads of a step's two tiles (A at the given addresses, B one tile further,
@@ -335,27 +336,19 @@ __global__ __launch_bounds__(pshape<D>::MAXREP / pshape<D>::HPW * 128, 1) void p
   // state to A at the end); B also takes the earlier block.
   const int sl = (TL + 1) >> 1, se = (TE + 1) >> 1;   // steps (tile pairs) of the two blocks
 
-  // the block ids of this wave's tiles (tile t by wave t % NW; lane j: the wave's
-  // j-th tile), read together with q; both are complete before the tile loads
-  // are issued, so the tile waits below count tiles only
+  // q rows, then the block ids of this wave's tiles (tile t by wave t % NW; lane j: the
+  // wave's j-th tile). A tile load waits for the block ids (and with them q) only when the
+  // wave has tiles with pool rows (rows before pos0): a fresh prefill's tiles go out right
+  // after the work item; q is needed only once the range has landed
+  su32x4_t qa[HPW][KS], qb2[HPW][KS];              // the current task's q; B's second task (the later block)
+  pload_q<Tag, D, HPW>(a, qa, row0, pos0, nrows, role_b && has_e ? pair : blk_l, hd0, nh);
+  if (role_b && has_e) pload_q<Tag, D, HPW>(a, qb2, row0, pos0, nrows, blk_l, hd0, nh);
   int myb = 0;
   {
     const int32_t* table = a.block_tables + (int64_t)seq * a.max_nb;
     const int tl = wave + NW * lane;
-    if (tl < T) {
-      const int b = table[(tl << 4) >> a.log2_bs];
-      myb = (b < 0 || b >= a.num_blocks) ? 0 : b;                 // host validates; stay inside the pool
-    }
+    if (tl < T) myb = table[(tl << 4) >> a.log2_bs];   // checked where it is used
   }
-  su32x4_t qa[HPW][KS], qb2[HPW][KS];              // the current task's q; B's second task (the later block)
-  pload_q<Tag, D, HPW>(a, qa, row0, pos0, nrows, role_b && has_e ? pair : blk_l, hd0, nh);
-  if (role_b && has_e) pload_q<Tag, D, HPW>(a, qb2, row0, pos0, nrows, blk_l, hd0, nh);
-  // the loads are complete here, for the compiler too (no wait inside the loops)
-#pragma unroll
-  for (int h = 0; h < HPW; ++h)
-#pragma unroll
-    for (int s = 0; s < KS; ++s) asm volatile("" : "+v"(qa[h][s]), "+v"(qb2[h][s]));
-  asm volatile("" : "+v"(myb));
 
   // ---- the workgroup's K/V range into LDS: tile t by wave t % NW ----
   const int64_t head_bytes = ((int64_t)1 << a.log2_bs) * RB;     // one kv head's K (or V) rows of a block
@@ -371,42 +364,67 @@ __global__ __launch_bounds__(pshape<D>::MAXREP / pshape<D>::HPW * 128, 1) void p
       koff[i] = (uint32_t)(r * RB + 16 * (cs ^ stream_kswz(r)));
       voff[i] = v_off + (uint32_t)(r * RB + 16 * (cs ^ stream_vswz(r)));
     }
-    for (int j = 0; wave + NW * j < T; ++j) {
-      const int t = wave + NW * j;
-      char* const dst = lds + t * TILE;
-      const int b = __builtin_amdgcn_readlane(myb, j);
-      const char* base = a.pool + (int64_t)b * blk_bytes + kvh * head_bytes + (int64_t)(t & sub_mask) * TB;
-      if (a.k_new != nullptr && 16 * t + 15 >= pos0) {
-        // a tile holding new rows: those from the step's k / v rows (rows past the
-        // sequence's last one repeat it: their scores are masked and their V rows
-        // zeroed below), the tile's rows before pos0 from the pool
-        const char* kb = a.k_new + (int64_t)row0 * a.k_new_row_bytes + (int64_t)kvh * RB;
-        const char* vb = a.v_new + (int64_t)row0 * a.v_new_row_bytes + (int64_t)kvh * RB;
+    // the tiles that hold pool rows (rows before pos0) first, behind one wait for the
+    // block ids while nothing else is in flight; then those holding only new rows, which
+    // need no block id, so that a fresh prefill's tiles go out right after the work item
+    // (the range is one chunk, so the order is free)
+    auto issue = [&](auto pool_pass) {
+      constexpr bool POOL = decltype(pool_pass)::value;
+      for (int j = 0; wave + NW * j < T; ++j) {
+        const int t = wave + NW * j;
+        char* const dst = lds + t * TILE;
+        const bool new_rows = a.k_new != nullptr && 16 * t + 15 >= pos0;
+        const bool pool_rows = !new_rows || 16 * t < pos0;
+        if (pool_rows != POOL) continue;
+        const char* base = a.pool;                   // the tile's rows in the pool (when it holds any)
+        if (POOL) {
+          int b = __builtin_amdgcn_readlane(myb, j);
+          b = (b < 0 || b >= a.num_blocks) ? 0 : b;   // host validates; stay inside the pool
+          base = a.pool + (int64_t)b * blk_bytes + kvh * head_bytes + (int64_t)(t & sub_mask) * TB;
+        }
+        if (new_rows) {
+          // a tile holding new rows: those from the step's k / v rows (rows past the
+          // sequence's last one repeat it: their scores are masked and their V rows
+          // zeroed below), the tile's rows before pos0 from the pool
+          const char* kb = a.k_new + (int64_t)row0 * a.k_new_row_bytes + (int64_t)kvh * RB;
+          const char* vb = a.v_new + (int64_t)row0 * a.v_new_row_bytes + (int64_t)kvh * RB;
+#pragma unroll
+          for (int i = 0; i < TLD; ++i) {
+            const int f = 64 * i + lane;
+            const int r = f / VCOLS, cs = f % VCOLS;
+            const int nr = 16 * t + r - pos0;            // the row's index among the new rows
+            const int rr = nr < nrows - 1 ? nr : nrows - 1;
+            const uint32_t kc = 16u * (uint32_t)(cs ^ stream_kswz(r)), vc = 16u * (uint32_t)(cs ^ stream_vswz(r));
+            const char* ks = nr >= 0 ? kb + (int64_t)rr * a.k_new_row_bytes + kc : base + (int64_t)r * RB + kc;
+            const char* vs = nr >= 0 ? vb + (int64_t)rr * a.v_new_row_bytes + vc : base + v_off + (int64_t)r * RB + vc;
+            s_dma16_l2p(ks, dst + 1024 * i);
+            s_dma16_l2p(vs, dst + TB + 1024 * i);
+          }
+          continue;
+        }
 #pragma unroll
         for (int i = 0; i < TLD; ++i) {
-          const int f = 64 * i + lane;
-          const int r = f / VCOLS, cs = f % VCOLS;
-          const int nr = 16 * t + r - pos0;            // the row's index among the new rows
-          const int rr = nr < nrows - 1 ? nr : nrows - 1;
-          const uint32_t kc = 16u * (uint32_t)(cs ^ stream_kswz(r)), vc = 16u * (uint32_t)(cs ^ stream_vswz(r));
-          const char* ks = nr >= 0 ? kb + (int64_t)rr * a.k_new_row_bytes + kc : base + (int64_t)r * RB + kc;
-          const char* vs = nr >= 0 ? vb + (int64_t)rr * a.v_new_row_bytes + vc : base + v_off + (int64_t)r * RB + vc;
-          s_dma16_l2p(ks, dst + 1024 * i);
-          s_dma16_l2p(vs, dst + TB + 1024 * i);
+          s_dma16_l2(koff[i], base, dst + 1024 * i);
+          s_dma16_l2(voff[i], base, dst + TB + 1024 * i);
         }
-        continue;
       }
-#pragma unroll
-      for (int i = 0; i < TLD; ++i) {
-        s_dma16_l2(koff[i], base, dst + 1024 * i);
-        s_dma16_l2(voff[i], base, dst + TB + 1024 * i);
-      }
+    };
+    if (a.k_new == nullptr || 16 * wave < pos0) {   // this wave has pool rows (its first tile is its lowest)
+      asm volatile("" : "+v"(myb));
+      issue(std::integral_constant<bool, true>());
     }
+    issue(std::integral_constant<bool, false>());
     if (wave == 0) {   // the tile after the range stands in for a missing second tile of a step: finite V
       char* const vt = lds + T * TILE + TB;
       for (int f = lane; f < 16 * VCOLS; f += 64) *reinterpret_cast<su32x4_t*>(vt + 16 * f) = su32x4_t{0u, 0u, 0u, 0u};
     }
   }
+  // q complete here, for the compiler too (no wait inside the loops); the tiles are in
+  // flight behind it
+#pragma unroll
+  for (int h = 0; h < HPW; ++h)
+#pragma unroll
+    for (int s = 0; s < KS; ++s) asm volatile("" : "+v"(qa[h][s]), "+v"(qb2[h][s]));
 
   // ---- the wave's tasks over their tiles, chunk by chunk as the chunks land ----
   const float sl2e = a.scale_log2e, inv_sl2e = 1.f / a.scale_log2e;
@@ -476,7 +494,8 @@ __global__ __launch_bounds__(pshape<D>::MAXREP / pshape<D>::HPW * 128, 1) void p
         if (16 * t + 15 < pos0) continue;
         const int first = max(0, pos0 - 16 * t);           // the tile's rows first .. valid - 1 are new
         const int valid = min(16, pos0 + nrows - 16 * t);
-        const int b = __builtin_amdgcn_readlane(myb, j);
+        int b = __builtin_amdgcn_readlane(myb, j);
+        b = (b < 0 || b >= a.num_blocks) ? 0 : b;   // host validates; stay inside the pool
         char* const pk = a.pool + (int64_t)b * blk_bytes + kvh * head_bytes +
                          (int64_t)(t & sub_mask) * TB;
         const char* const src = lds + t * TILE;
