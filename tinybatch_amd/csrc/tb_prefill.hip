@@ -275,33 +275,44 @@ __device__ __forceinline__ void pwrite(const prefill_args& a, const pstate<D / 1
   }
 }
 
-// q rows 16 blk .. (heads hd0 .., rotated at the rows' positions) as B operands;
-// rows past the step's last row are zero.
-template <typename Tag, int D, int HPW>
-__device__ __forceinline__ void pload_q(const prefill_args& a, su32x4_t (&q)[HPW][D / 32], int row0, int pos0,
-                                       int nrows, int blk, int hd0, int nh) {
-  typedef typename smath<Tag>::scalar_t scalar_t;
+// q rows 16 blk .. (heads hd0 ..) as loaded; rows past the step's last row are zero.
+// The loads are left in flight (nothing here uses them).
+template <int D, int HPW>
+__device__ __forceinline__ void pload_q(const prefill_args& a, vec16 (&qv)[HPW][D / 32], int row0, int nrows, int blk,
+                                       int hd0, int nh) {
   constexpr int RB = 2 * D, KS = D / 32;
   const int lane = threadIdx.x & 63, lc = lane & 15, lg = lane >> 4;
   const int my_row = 16 * blk + lc;
 #pragma unroll
   for (int h = 0; h < HPW; ++h) {
-    vec16 qv[KS];
 #pragma unroll
-    for (int s = 0; s < KS; ++s) qv[s] = zero16();
+    for (int s = 0; s < KS; ++s) qv[h][s] = zero16();
     if (my_row < nrows && h < nh) {
       const char* qrow = a.q + (int64_t)(row0 + my_row) * a.q_row_bytes + (int64_t)(hd0 + h) * RB + 16 * lg;
 #pragma unroll
-      for (int s = 0; s < KS; ++s) qv[s] = ld16(qrow + 64 * s);
-      if (a.rope.cos) {                            // slices s and s + KS/2 pair (dims i and i + D/2)
-        const int64_t r = a.rope.row(pos0 + my_row, D / 2) + 8 * lg;
+      for (int s = 0; s < KS; ++s) qv[h][s] = ld16(qrow + 64 * s);
+    }
+  }
+}
+
+// The loaded q rows rotated at the rows' positions (with RoPE) as B operands.
+template <typename Tag, int D, int HPW>
+__device__ __forceinline__ void prot_q(const prefill_args& a, vec16 (&qv)[HPW][D / 32], su32x4_t (&q)[HPW][D / 32],
+                                      int pos0, int nrows, int blk, int nh) {
+  typedef typename smath<Tag>::scalar_t scalar_t;
+  constexpr int KS = D / 32;
+  const int lane = threadIdx.x & 63, lc = lane & 15, lg = lane >> 4;
+  const int my_row = 16 * blk + lc;
 #pragma unroll
-        for (int s = 0; s < KS / 2; ++s)
-          rope_pair<scalar_t>(qv[s], qv[s + KS / 2], a.rope.cos + r + 32 * s, a.rope.sin + r + 32 * s);
-      }
+  for (int h = 0; h < HPW; ++h) {
+    if (a.rope.cos && my_row < nrows && h < nh) {   // slices s and s + KS/2 pair (dims i and i + D/2)
+      const int64_t r = a.rope.row(pos0 + my_row, D / 2) + 8 * lg;
+#pragma unroll
+      for (int s = 0; s < KS / 2; ++s)
+        rope_pair<scalar_t>(qv[h][s], qv[h][s + KS / 2], a.rope.cos + r + 32 * s, a.rope.sin + r + 32 * s);
     }
 #pragma unroll
-    for (int s = 0; s < KS; ++s) q[h][s] = __builtin_bit_cast(su32x4_t, qv[s]);
+    for (int s = 0; s < KS; ++s) q[h][s] = __builtin_bit_cast(su32x4_t, qv[h][s]);
   }
 }
 
@@ -340,9 +351,10 @@ __global__ __launch_bounds__(pshape<D>::MAXREP / pshape<D>::HPW * 128, 1) void p
   // wave's j-th tile). A tile load waits for the block ids (and with them q) only when the
   // wave has tiles with pool rows (rows before pos0): a fresh prefill's tiles go out right
   // after the work item; q is needed only once the range has landed
-  su32x4_t qa[HPW][KS], qb2[HPW][KS];              // the current task's q; B's second task (the later block)
-  pload_q<Tag, D, HPW>(a, qa, row0, pos0, nrows, role_b && has_e ? pair : blk_l, hd0, nh);
-  if (role_b && has_e) pload_q<Tag, D, HPW>(a, qb2, row0, pos0, nrows, blk_l, hd0, nh);
+  const int blk_a = role_b && has_e ? pair : blk_l;   // the current task's block; B's second task: blk_l
+  vec16 qra[HPW][KS], qrb[HPW][KS];
+  pload_q<D, HPW>(a, qra, row0, nrows, blk_a, hd0, nh);
+  if (role_b && has_e) pload_q<D, HPW>(a, qrb, row0, nrows, blk_l, hd0, nh);
   int myb = 0;
   {
     const int32_t* table = a.block_tables + (int64_t)seq * a.max_nb;
@@ -419,8 +431,15 @@ __global__ __launch_bounds__(pshape<D>::MAXREP / pshape<D>::HPW * 128, 1) void p
       for (int f = lane; f < 16 * VCOLS; f += 64) *reinterpret_cast<su32x4_t*>(vt + 16 * f) = su32x4_t{0u, 0u, 0u, 0u};
     }
   }
-  // q complete here, for the compiler too (no wait inside the loops); the tiles are in
-  // flight behind it
+  // q rotated (RoPE rows loaded now, behind the tiles) and complete here, for the compiler
+  // too (no wait inside the loops)
+  su32x4_t qa[HPW][KS], qb2[HPW][KS];              // the current task's q; B's second task (the later block)
+  prot_q<Tag, D, HPW>(a, qra, qa, pos0, nrows, blk_a, nh);
+#pragma unroll
+  for (int h = 0; h < HPW; ++h)
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qb2[h][s] = su32x4_t{0u, 0u, 0u, 0u};
+  if (role_b && has_e) prot_q<Tag, D, HPW>(a, qrb, qb2, pos0, nrows, blk_l, nh);
 #pragma unroll
   for (int h = 0; h < HPW; ++h)
 #pragma unroll
