@@ -330,10 +330,33 @@ __global__ __launch_bounds__(pshape<D>::MAXREP / pshape<D>::HPW * 128, 1) void p
   const int row0 = wi.x, seq = wi.y, pos0 = wi.z;
   const int nrows = wi.w & 0xFFFF, pair = (wi.w >> 16) & 0xFF, kvh = (wi.w >> 24) & 0x7F;
   const int rep = a.rep;
-  const int G = (rep + HPW - 1) / HPW;            // head groups: waves g (A) and G + g (B)
+  const int G = (rep + HPW - 1) / HPW;            // head groups, two waves (A, B) each
   const int NW = 2 * G;
-  const int g = wave % G;
-  const bool role_b = wave >= G;
+  // Waves onto (head group g, role). Waves w and w + 4 of a workgroup share a SIMD
+  // (measured: the first SIMD rotates between workgroups, the grouping by w % 4 does
+  // not), so with an odd number of groups (2 G waves, G > 1) waves w % 4 = 0, 1 share
+  // their SIMD with one wave more than waves w % 4 = 2, 3. Groups 0 .. G - 2 then put A
+  // on such a busier SIMD (w % 4 = 0, 1) and B on a quieter one (w % 4 = 2, 3), B taking
+  // G / (2 (G - 1)) of the group's steps (sb24 in 24ths); the last group takes waves
+  // 2 G - 2 (A) and 2 G - 1 (B), evenly: every SIMD then carries G / 4 groups of steps.
+  // B's share never falls below the earlier block it must take (<= half the steps).
+  // An even number of groups is balanced as it is: A = wave g, B = wave G + g, evenly.
+  int g, sb24 = 12;
+  bool role_b;
+  if ((G & 1) && G > 1) {
+    const int K = G - 1;
+    if (wave < 2 * K) {
+      g = 2 * (wave >> 2) + (wave & 1);
+      role_b = (wave & 3) >= 2;
+      sb24 = 12 * G / K;
+    } else {
+      g = K;
+      role_b = wave == 2 * K + 1;
+    }
+  } else {
+    g = wave % G;
+    role_b = wave >= G;
+  }
   const int hd0 = kvh * rep + g * HPW;
   const int nh = min(HPW, rep - g * HPW);
   const int nb = (nrows + 15) >> 4;
@@ -532,7 +555,7 @@ __global__ __launch_bounds__(pshape<D>::MAXREP / pshape<D>::HPW * 128, 1) void p
     const int s0 = (CH / 2) * c;
     const int nl = max(0, min(s0 + CH / 2, sl) - s0);    // later-block steps in the chunk
     const int ne = max(0, min(s0 + CH / 2, se) - s0);    // earlier-block steps in the chunk
-    const int nbl = max(0, (nl - ne) >> 1);              // B's share of the later block's steps
+    const int nbl = min(nl, max(0, sb24 * (nl + ne) / 24 - ne));   // B's share of the later block's steps
     const int na = nl - nbl;
     // this wave's steps of the chunk: B's earlier-block ones first, then its share
     // of the later block; one call site keeps the registers of one step live
@@ -563,7 +586,7 @@ __global__ __launch_bounds__(pshape<D>::MAXREP / pshape<D>::HPW * 128, 1) void p
   for (int c = 0; c < nch; ++c) {
     const int s0 = (CH / 2) * c;
     const int nl = max(0, min(s0 + CH / 2, sl) - s0), ne = max(0, min(s0 + CH / 2, se) - s0);
-    b_has_l = b_has_l || ((nl - ne) >> 1) > 0;
+    b_has_l = b_has_l || min(nl, max(0, sb24 * (nl + ne) / 24 - ne)) > 0;
   }
   const bool has_l2 = b_has_l;
 
