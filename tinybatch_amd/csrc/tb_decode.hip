@@ -197,7 +197,7 @@ __global__ __launch_bounds__(64 * W) void paged_stream_kernel(const stream_args 
   constexpr int STATE = S::STATE;
   static_assert(R % 2 == 0, "a step is a pair of ring slots");
   __shared__ __align__(1024) char lds_all[S::LDS];
-  __shared__ int pend_sh[W][2][4];               // per wave: its partials (unit, np | w0 << 8 | idx << 16, base,
+  __shared__ __align__(16) int pend_sh[W][2][4];   // per wave: its partials (unit, np | w0 << 8 | idx << 16, base,
                                                  // sequence | kv head << 20)
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -542,21 +542,30 @@ __global__ __launch_bounds__(64 * W) void paged_stream_kernel(const stream_args 
   __syncthreads();
   constexpr int CPL = (8 * D / 4 + 63) / 64;
   const int n4 = rep * D / 4;
+  // this wave's partials and the first-partial unit of each later wave of the
+  // workgroup, read together (one LDS round trip)
+  const int4 own[2] = {*reinterpret_cast<const int4*>(&pend_sh[wave][0][0]),
+                       *reinterpret_cast<const int4*>(&pend_sh[wave][1][0])};
+  int mfirst[W];
+  mfirst[0] = own[0].x;
+#pragma unroll
+  for (int m = 1; m < W; ++m) mfirst[m] = pend_sh[min(wave + m, W - 1)][0][0];
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
-    const int u = __builtin_amdgcn_readfirstlane(pend_sh[wave][e][0]);
+    const int u = __builtin_amdgcn_readfirstlane(own[e].x);
     if (u < 0) continue;
-    const int info = __builtin_amdgcn_readfirstlane(pend_sh[wave][e][1]);
+    const int info = __builtin_amdgcn_readfirstlane(own[e].y);
     const int np = info & 0xFF, w0 = (info >> 8) & 0xFF, idx = info >> 16;   // np <= 255
-    const int pbase = __builtin_amdgcn_readfirstlane(pend_sh[wave][e][2]);
+    const int pbase = __builtin_amdgcn_readfirstlane(own[e].z);
     if (idx != 0 && (w0 + idx) % W != 0) continue;   // a member: its group's leader merges it
     // the group: this wave's piece and the next waves' pieces of the unit in this workgroup
     int cnt = 1;
     while (idx + cnt < np && (w0 + idx + cnt) % W != 0) ++cnt;
-    const int bh = __builtin_amdgcn_readfirstlane(pend_sh[wave][e][3]);
+    const int bh = __builtin_amdgcn_readfirstlane(own[e].w);
     const int b = bh & 0xFFFFF, h = bh >> 20;
-    // the members' states (LDS): every read of both column sets in flight at once,
-    // then one log-sum-exp per column
+    // the members' states (LDS; a member's piece of the unit is its first partial, in pst,
+    // or its last, in its ring): the reads of all members in flight at once, then one
+    // log-sum-exp per column
     float Mx[CPL], L[CPL];
     float4_t o[CPL];
     {
@@ -564,8 +573,8 @@ __global__ __launch_bounds__(64 * W) void paged_stream_kernel(const stream_args 
 #pragma unroll
       for (int m = 0; m < W; ++m) {
         const int w = m < cnt ? wave + m : wave;   // members are the next waves of this workgroup
-        const int sidx = pend_sh[w][0][0] == u ? 0 : 1;
-        stp[m] = lds_all + w * S::WAVE_LDS + (sidx == 0 ? (int)(pst - ring) : 0);
+        const bool first = __builtin_amdgcn_readfirstlane(mfirst[m < cnt ? m : 0]) == u;
+        stp[m] = lds_all + w * S::WAVE_LDS + (first ? (int)(pst - ring) : 0);
       }
       float2 ml[CPL][W];
       float4_t v[CPL][W];
@@ -576,6 +585,7 @@ __global__ __launch_bounds__(64 * W) void paged_stream_kernel(const stream_args 
         const int head = (4 * cc) / D;
 #pragma unroll
         for (int m = 0; m < W; ++m) {
+          if (m >= cnt) break;
           ml[q][m] = *reinterpret_cast<const float2*>(stp[m] + 4 * 8 * D + 8 * head);
           v[q][m] = *reinterpret_cast<const float4_t*>(stp[m] + 4 * (head * D + (4 * cc) % D));
         }
@@ -590,7 +600,8 @@ __global__ __launch_bounds__(64 * W) void paged_stream_kernel(const stream_args 
         float4_t acc_o = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int m = 0; m < W; ++m) {
-          const float wgt = (m < cnt && ml[q][m].y > 0.f) ? fast_exp2(ml[q][m].x - mb) : 0.f;
+          if (m >= cnt) break;
+          const float wgt = ml[q][m].y > 0.f ? fast_exp2(ml[q][m].x - mb) : 0.f;
           l = fmaf(ml[q][m].y, wgt, l);
           acc_o += v[q][m] * wgt;
         }
