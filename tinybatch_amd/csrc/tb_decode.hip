@@ -211,9 +211,10 @@ __global__ __launch_bounds__(64 * W) void paged_stream_kernel(const stream_args 
   const int4* const ent_g = a.entries + (int64_t)(k < a.workers ? k : 0) * a.stride;
 
   // ---- the worker's entry count and its first 64 entries (one round trip) ----
-  s_dma16(ent_g + lane, ents);                   // the entry array is padded by 64 entries
+  int4 ev = ent_g[lane];                         // the issuing cursor's entries, lane = tile (the
+                                                 // entry array is padded by 64 entries)
   int n = k < a.workers ? __builtin_amdgcn_readfirstlane(a.counts[k]) : 0;
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  asm volatile("" : "+v"(ev.x), "+v"(ev.y), "+v"(ev.z), "+v"(ev.w));   // complete here, for the compiler too
   {
     // count word: tiles | newest slots shared by two sequences << 30. A malformed count
     // (the plan builder never makes one) and a fused append the plan cannot serve are
@@ -226,7 +227,6 @@ __global__ __launch_bounds__(64 * W) void paged_stream_kernel(const stream_args 
       __hip_atomic_fetch_add(a.violations, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     n = (bad || refused) ? 0 : cnt;
   }
-  int4 ev = *reinterpret_cast<const int4*>(ents + 16 * lane);   // the issuing cursor's entries, lane = tile
 
   const bool fused = a.k_new != nullptr;
   const bool roped = a.rope.cos != nullptr;
