@@ -26,12 +26,12 @@ def _bits(t):
     return t.contiguous().view(torch.int16)
 
 
-def decode_meta(ctx, tables, NB, BS, Hq, Hkv, D, dtype, waves=None):
+def decode_meta(ctx, tables, NB, BS, Hq, Hkv, D, dtype, waves=None, unit_cost=None):
     B = len(ctx)
     meta = build_step_metadata([c - 1 for c in ctx], [(b, b + 1) for b in range(B)], tables, ctx, block_size=BS,
                                num_blocks=NB, partition_tokens=ops.partition_tokens(dtype, D))
     assert ops.attach_decode_plan(meta, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, dtype=dtype, device=DEV,
-                                  waves=waves)
+                                  waves=waves, unit_cost=unit_cost)
     return meta.to(DEV)
 
 
@@ -66,8 +66,9 @@ def oracle(c):
     return out, pool
 
 
-def run(c, fused=True, waves=None):
-    meta = decode_meta(c["ctx"], c["tables"], c["NB"], c["BS"], c["Hq"], c["Hkv"], c["D"], c["dtype"], waves)
+def run(c, fused=True, waves=None, unit_cost=None):
+    meta = decode_meta(c["ctx"], c["tables"], c["NB"], c["BS"], c["Hq"], c["Hkv"], c["D"], c["dtype"], waves,
+                       unit_cost)
     pool = c["pool"].to(DEV)
     q, k, v = c["q"].to(DEV), c["k"].to(DEV), c["v"].to(DEV)
     if fused:
@@ -95,6 +96,19 @@ def test_headline_shape(dtype, fused):
              k=wl.k_new.to(dtype), v=wl.v_new.to(dtype), NB=wl.num_blocks, BS=16, Hq=14, Hkv=2, D=64, dtype=dtype)
     _, meta = check(c, fused)
     assert meta.decode_pieces > 0                  # units cut over workgroups: partials merged
+
+
+@pytest.mark.parametrize("D,Hq,Hkv", [(64, 14, 2), (128, 32, 8)])
+def test_plans_of_every_unit_cost_agree_with_the_oracle(D, Hq, Hkv):
+    """The plan's unit cost moves the workers' cut points (and so the pieces, the pads
+    and the merges): every cost gives the oracle's attention and the bit-exact append."""
+    c = case(90 + D, 48 if D == 64 else 12, Hq, Hkv, D, 16, torch.bfloat16)
+    want, want_pool = oracle(c)
+    for uc in (0, 3, 6, 8, 12):
+        got, pool, meta = run(c, True, None, uc)
+        assert meta.decode_unit_cost == uc
+        assert torch.equal(_bits(pool), _bits(want_pool)), f"unit cost {uc}: pool differs (append)"
+        torch.testing.assert_close(got.float(), want.float(), **TOL, msg=f"unit cost {uc}")
 
 
 def test_llama_geometry_subset():
