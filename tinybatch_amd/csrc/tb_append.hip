@@ -37,7 +37,7 @@ __global__ __launch_bounds__(256) void kv_append_kernel(
                     (int64_t)h * head_bytes + (int64_t)c * 16;
   char* dst = pool + (((blk * 2 + kv) * num_kv_heads + h) * bs + off) * (int64_t)head_bytes +
               (int64_t)c * 16;
-  st16(dst, ld16(src));
+  st16_through(dst, ld16(src));
 }
 
 // K1 with the K rotation folded in (the engine's _rope, model.py:72-80,125,
@@ -84,7 +84,7 @@ __global__ __launch_bounds__(256) void kv_append_rope_kernel(
     }
   }
   char* dst = pool + (((blk * 2 + kv) * num_kv_heads + h) * bs + off) * (int64_t)head_bytes + (int64_t)c * 16;
-  st16(dst, x);
+  st16_through(dst, x);
 }
 
 // Reference: PagedKVCache.gather, src/tinybatch/kv_cache.py:40-45

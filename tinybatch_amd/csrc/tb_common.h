@@ -51,6 +51,27 @@ __device__ __forceinline__ void st16(void* p, const vec16& r) {
   *reinterpret_cast<uint4*>(p) = v;
 }
 
+// Stores of a kernel's results (outputs, appended rows, copied blocks), written
+// through this XCD's L2 at device scope (SC1). A plain store leaves the line
+// dirty in the L2. The L2 then writes it back at the kernel's end, and the
+// kernel completes only after that write-back. A written-through line goes to
+// memory while the kernel still runs. Same bits either way.
+// Measured, same box:
+// - the 1024-block copy over 24 pools: 73.0 against 86.9 us;
+// - the prefill rows of 8 x 512 bf16: 11.9 against 12.5 us per layer.
+// The 16-byte form is one vector store instruction; the compiler does not count
+// it in its own waits, so any later wait it makes only waits longer.
+__device__ __forceinline__ void st16_through(void* p, const vec16& r) {
+  const u32x4_t v = {r.w[0], r.w[1], r.w[2], r.w[3]};
+  asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+}
+template <typename T>
+__device__ __forceinline__ void st8_through(void* p, const T& r) {
+  static_assert(sizeof(T) == 8, "an 8-byte value");
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), __builtin_bit_cast(uint64_t, r), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
 __device__ __forceinline__ vec16 zero16() {
   vec16 r;
   r.w[0] = r.w[1] = r.w[2] = r.w[3] = 0u;

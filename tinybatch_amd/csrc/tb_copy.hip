@@ -16,11 +16,12 @@ namespace tb {
 // 256 x CU consecutive vectors of one layer; every thread issues its CU loads
 // before its first store. The host guarantees that no dst block is a src block
 // (and that dst blocks are distinct), so the loads may run ahead of the stores.
-// Measured on 24 pools x 1024 pairs of 8 KiB blocks (403 MB moved): 83.8 us
-// with CU = 2 and non-temporal loads and stores (4.81 TB/s), 84-89 us for
-// CU = 2..8 either way, 102-106 us at CU = 16; a plain contiguous device copy
-// of the same bytes takes 80.2 us (5.02 TB/s), the practical ceiling of mixed
-// read/write traffic here.
+// Measured on 24 pools x 1024 pairs of 8 KiB blocks (403 MB moved), with CU = 2,
+// non-temporal loads and the stores written through the L2 (st16_through):
+// 73.0 us (5.52 TB/s). With non-temporal stores it was 83.8-87 us: the copy's
+// last dirty L2 lines were written back only at the kernel's end. CU = 2..8
+// measured 84-89 us and CU = 16 102-106 us, both with non-temporal stores.
+// A plain contiguous device copy of the same bytes (torch) takes 80.2 us.
 constexpr int COPY_CU = 2;
 
 template <int CU, bool NT>
@@ -50,7 +51,7 @@ __global__ __launch_bounds__(256) void block_copy_kernel(const uint64_t* __restr
 #pragma unroll
   for (int u = 0; u < CU; ++u) {
     if (to[u]) {
-      if (NT) __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, r[u]), reinterpret_cast<u32x4_t*>(to[u]));
+      if (NT) st16_through(to[u], r[u]);
       else st16(to[u], r[u]);
     }
   }

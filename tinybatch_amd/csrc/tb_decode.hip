@@ -178,7 +178,7 @@ __device__ __forceinline__ void stream_merge(const stream_args& a, int b, int h,
     s4_t r;
 #pragma unroll
     for (int j = 0; j < 4; ++j) r[j] = (scalar_t)(o[q][j] * inv);
-    *reinterpret_cast<s4_t*>(a.out + b * a.out_row_bytes + ((int64_t)h * a.rep * D + 4 * c) * 2) = r;
+    st8_through(a.out + b * a.out_row_bytes + ((int64_t)h * a.rep * D + 4 * c) * 2, r);
   }
 }
 
@@ -416,13 +416,13 @@ __global__ __launch_bounds__(64 * W) void paged_stream_kernel(const stream_args 
             if (roped) rope_pair<scalar_t>(x1, x2, cosr + 8 * lane, sinr + 8 * lane);
             *reinterpret_cast<vec16*>(sl + rn * RB + 16 * (lane ^ S::kswz(rn))) = x1;
             *reinterpret_cast<vec16*>(sl + rn * RB + 16 * ((lane + VCOLS / 2) ^ S::kswz(rn))) = x2;
-            st16(prow + 16 * lane, x1);
-            st16(prow + 16 * (lane + VCOLS / 2), x2);
+            st16_through(prow + 16 * lane, x1);
+            st16_through(prow + 16 * (lane + VCOLS / 2), x2);
           } else if (lane >= 32 && lane < 32 + VCOLS) {   // V chunk lane - 32
             const int c = lane - 32;
             const vec16 x = *reinterpret_cast<const vec16*>(qd + QNEW + RB + 16 * c);
             *reinterpret_cast<vec16*>(sl + TB + rn * RB + 16 * (c ^ S::vswz(rn))) = x;
-            st16(prow + v_off + 16 * c, x);
+            st16_through(prow + v_off + 16 * c, x);
           }
         }
       }
@@ -499,7 +499,7 @@ __global__ __launch_bounds__(64 * W) void paged_stream_kernel(const stream_args 
               s4_t o;
 #pragma unroll
               for (int jj = 0; jj < 4; ++jj) o[jj] = (scalar_t)(acc[nn][jj] * inv);
-              *reinterpret_cast<s4_t*>(orow + 2 * (16 * nn + 4 * lg)) = o;
+              st8_through(orow + 2 * (16 * nn + 4 * lg), o);
             }
           }
         } else {
@@ -623,7 +623,7 @@ __global__ __launch_bounds__(64 * W) void paged_stream_kernel(const stream_args 
         s4_t r;
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) r[jj] = (scalar_t)(o[q][jj] * inv);
-        *reinterpret_cast<s4_t*>(a.out + b * a.out_row_bytes + ((int64_t)h * rep * D + 4 * c) * 2) = r;
+        st8_through(a.out + b * a.out_row_bytes + ((int64_t)h * rep * D + 4 * c) * 2, r);
       }
       continue;
     }

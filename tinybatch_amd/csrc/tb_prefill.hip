@@ -270,7 +270,7 @@ __device__ __forceinline__ void pwrite(const prefill_args& a, const pstate<D / 1
       s4_t o;
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) o[jj] = (scalar_t)(st.acc[h][nn][jj] * inv);
-      *reinterpret_cast<s4_t*>(orow + 2 * (16 * nn + 4 * lg)) = o;
+      st8_through(orow + 2 * (16 * nn + 4 * lg), o);
     }
   }
 }
@@ -546,8 +546,9 @@ __global__ __launch_bounds__(pshape<D>::MAXREP / pshape<D>::HPW * 128, 1) void p
           const int f = 64 * i + lane;
           const int r = f / VCOLS, cs = f % VCOLS;
           if (r >= first && r < valid) {
-            st16(pk + r * RB + 16 * (cs ^ stream_kswz(r)), *reinterpret_cast<const vec16*>(src + 16 * f));
-            st16(pk + v_off + r * RB + 16 * (cs ^ stream_vswz(r)), *reinterpret_cast<const vec16*>(src + TB + 16 * f));
+            st16_through(pk + r * RB + 16 * (cs ^ stream_kswz(r)), *reinterpret_cast<const vec16*>(src + 16 * f));
+            st16_through(pk + v_off + r * RB + 16 * (cs ^ stream_vswz(r)),
+                         *reinterpret_cast<const vec16*>(src + TB + 16 * f));
           }
         }
       }
