@@ -136,7 +136,7 @@ __device__ __forceinline__ void finish_valu(const attn_args& a, int row, int par
       vec16 o;
 #pragma unroll
       for (int e = 0; e < 4; ++e) o.w[e] = __float_as_uint(acc[h][e] * inv);
-      st16(orow + (int64_t)(head0 + h) * D * 4, o);
+      st16_through(orow + (int64_t)(head0 + h) * D * 4, o);
     }
     return;
   }
@@ -255,8 +255,8 @@ __global__ __launch_bounds__(64) void paged_attn_valu_kernel(const attn_args a) 
       for (int i = 0; i < CH_LOADS; ++i) {
         if (c0 + i * TPL + g == new_pos) {
           char* kp = const_cast<char*>(pool_kvh) + new_off;
-          st16(kp, kbuf[i]);
-          st16(kp + v_off, vbuf[i]);
+          st16_through(kp, kbuf[i]);
+          st16_through(kp + v_off, vbuf[i]);
         }
       }
     }
@@ -424,7 +424,7 @@ __device__ __forceinline__ void merge_in_launch(const attn_args& a, int row0, in
     s4_t r;
 #pragma unroll
     for (int j = 0; j < 4; ++j) r[j] = (scalar_t)(o[j] * inv);
-    *reinterpret_cast<s4_t*>(a.out + row * a.out_row_bytes + ((int64_t)head * D + 4 * d4) * 2) = r;
+    st_through(a.out + row * a.out_row_bytes + ((int64_t)head * D + 4 * d4) * 2, r);
   }
   if (threadIdx.x == 0) __hip_atomic_store(word, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -687,7 +687,7 @@ __device__ __forceinline__ void decode_items_body(const attn_args& a, char* cons
         if (first) rope_pair<scalar_t>(x, y, a.rope.cos + r, a.rope.sin + r);
         else rope_pair<scalar_t>(y, x, a.rope.cos + r, a.rope.sin + r);
       }
-      st16(dst + (is_v ? v_off : 0) + 16 * c, x);
+      st16_through(dst + (is_v ? v_off : 0) + 16 * c, x);
     }
   }
   __syncthreads();   // every wave is done with its V rows: the area takes the merge
@@ -1005,7 +1005,7 @@ __device__ __forceinline__ void prefill_tiles_body(const attn_args& a, char* con
         s4_t o;
 #pragma unroll
         for (int j = 0; j < 4; ++j) o[j] = (scalar_t)(acc[nn][j] * inv);
-        *reinterpret_cast<s4_t*>(orow + (16 * nn + 4 * lg) * EB) = o;
+        st_through(orow + (16 * nn + 4 * lg) * EB, o);
       }
     } else {                     // partial of a split row
       const int64_t pidx = pbeg + part;
@@ -1103,7 +1103,7 @@ __global__ __launch_bounds__(COMBINE_THREADS) void combine_partials_kernel(const
     s4_t r;
 #pragma unroll
     for (int j = 0; j < 4; ++j) r[j] = (s_t)(o[j] * inv);
-    *reinterpret_cast<s4_t*>(dst) = r;
+    st_through(dst, r);
   }
 }
 

@@ -71,6 +71,17 @@ __device__ __forceinline__ void st8_through(void* p, const T& r) {
   __hip_atomic_store(reinterpret_cast<uint64_t*>(p), __builtin_bit_cast(uint64_t, r), __ATOMIC_RELAXED,
                      __HIP_MEMORY_SCOPE_AGENT);
 }
+// An 8- or 16-byte value (four 16-bit or four 32-bit elements) written through.
+template <typename T>
+__device__ __forceinline__ void st_through(void* p, const T& r) {
+  static_assert(sizeof(T) == 8 || sizeof(T) == 16, "an 8- or 16-byte value");
+  if constexpr (sizeof(T) == 8) {
+    st8_through(p, r);
+  } else {
+    const u32x4_t v = __builtin_bit_cast(u32x4_t, r);
+    asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+  }
+}
 
 __device__ __forceinline__ vec16 zero16() {
   vec16 r;
