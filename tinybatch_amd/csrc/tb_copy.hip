@@ -20,7 +20,8 @@ namespace tb {
 // non-temporal loads and the stores written through the L2 (st16_through):
 // 73.0 us (5.52 TB/s). With non-temporal stores it was 83.8-87 us: the copy's
 // last dirty L2 lines were written back only at the kernel's end. CU = 1 / 4 / 8
-// measure 78.9 / 73.2-73.4 / 76.3-76.8 us (CU = 2: 72.7-73.7, same box).
+// measure 78.9 / 73.2-73.4 / 76.3-76.8 us (CU = 2: 72.7-73.7, same box); plain
+// loads in place of the non-temporal ones 83.8-85.3 us.
 // A plain contiguous device copy of the same bytes (torch) takes 80.2 us.
 constexpr int COPY_CU = 2;
 
