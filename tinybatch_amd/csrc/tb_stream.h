@@ -75,7 +75,8 @@ __device__ __forceinline__ void s_dma16_s(uint32_t off, const void* base, const 
 }
 
 // The same without the non-temporal hint, for bytes that other workgroups read
-// again soon (the lines stay in the L2).
+// again soon (the lines stay in the L2). The prefill kernel's K/V range with the
+// hint measured 12.6-12.8 against 12.2-12.4 us per layer on 8 x 512 bf16 rows.
 __device__ __forceinline__ void s_dma16_l2(uint32_t off, const void* base, const void* lds_dst) {
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(s_lds_addr(lds_dst))
                : "memory");
